@@ -1,0 +1,277 @@
+"""Benchmark of the fused causal attention path on one MI355X.
+
+Headline (BASELINE.json metric "attn fwd/bwd TFLOP/s (B16 H12 T1024 D64 bf16); KV-decode HBM
+GB/s"): one step = the bf16 causal forward (saving lse) plus the backward from that lse at
+B=16, H=12, T=1024, D=64, inputs N(0,1) synthetic and resident in HBM.
+value = algorithmic FLOPs of the step / time per step:
+  forward  4*B*H*T^2*D/2           = 25.770 GFLOP
+  backward 2.5 x forward (5 GEMMs) = 64.425 GFLOP
+The same line carries each kernel's time and roofline fraction, the KV-decode HBM bandwidth
+(config 4: 32 ragged sequences, H12, D64, bf16 cache, timed over rotating cache copies so
+the 256 MB MALL cannot hold them), the roofline of the dominant kernel, and the reference's
+CPU path timed on a bounded sample on this host.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 4096 flop/clk/CU x 2.4 GHz, dense
+PEAK_HBM_GBPS = 8000.0
+
+B, H, T, D = 16, 12, 1024, 64
+BH = B * H
+SCALE = 0.125
+UNIT = 2.0 * BH * T * T * D / 2          # one causal S x S x D product: 12.885 GFLOP
+FWD_FLOPS = 2 * UNIT                     # 25.770 GFLOP
+BWD_FLOPS = 5 * UNIT                     # 64.425 GFLOP
+# Algorithmic share per backward kernel: dK/dV computes S, dP, dV, dK (4 units); dQ computes
+# dQ (1 unit) and recomputes S and dP (executed, not algorithmic).
+KERNEL_FLOPS = {"fwd": FWD_FLOPS, "bwd_dq": UNIT, "bwd_dkdv": 4 * UNIT}
+
+DEC_N, DEC_H, DEC_L, DEC_D = 32, 12, 1024, 64
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--reps", type=int, default=20, help="launches per kernel timing")
+    p.add_argument("--decode-copies", type=int, default=8)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-slices", type=int, default=12)
+    return p.parse_args()
+
+
+def event_time_ms(fn, reps, stream):
+    """Average ms per call of fn() over `reps` back-to-back calls, HIP events on `stream`."""
+    import torch
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def load_traffic(kernel):
+    """HBM bytes per launch measured with rocprofv3 --pmc (committed summary), or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{kernel}.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(n_slices):
+    """The reference's CPU path (oracle/_ref: its own tensor_ops.cpp/backward.cpp) or, when
+    that is not built, the C restatement, on n_slices of the B16 H12 T1024 D64 problem."""
+    import numpy as np
+    import oracle
+    from dadgpt_amd import synth
+
+    q, k, v, g = synth.attn_inputs(n_slices, T, D, seed=synth.BASE_SEED + 3, with_dout=True,
+                                   bf16=True)
+    kind = "reference" if oracle.ref_available() else "port"
+    t0 = time.perf_counter()
+    if kind == "reference":
+        oracle.ref_attn_fwd(q, k, v, SCALE)
+        oracle.ref_attn_bwd(g, q, k, v, SCALE)
+    else:
+        oracle.attn_fwd_slices(q, k, v, SCALE, 0, n_slices)
+        oracle.attn_bwd_slices(g, q, k, v, SCALE, 0, n_slices)
+    dt = time.perf_counter() - t0
+    flops = (FWD_FLOPS + BWD_FLOPS) * n_slices / BH
+    return {
+        "value": flops / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": (f"fp32 forward+backward of {n_slices} of {BH} (b,h) slices of B16 H12 T1024 "
+                   f"D64 (bf16-rounded inputs), single thread, {dt:.2f} s; the backward "
+                   f"recomputes P as the reference's materialized path stores it"),
+        "seconds": dt,
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 "
+                                   "(every (b,h) slice is independent, see the sharding "
+                                   "design)", "n_gpus": args.gpus}), flush=True)
+        sys.exit(2)
+
+    import torch
+    from dadgpt_amd import attention as A
+
+    A.lib()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xDAD6B7)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32).to(
+            torch.bfloat16)
+
+    q, k, v, g = (randn(BH, T, D) for _ in range(4))
+    out = torch.empty_like(q)
+    lse = torch.empty(BH, T, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    delta = torch.empty(BH, T, device=dev)
+
+    def fwd():
+        A.flash_attention_forward_bf16(out, lse, q, k, v, BH, T, D, SCALE, None)
+
+    def bwd():
+        A.flash_attention_backward_bf16(dq, dk, dv, delta, g, out, lse, q, k, v, BH, T, D,
+                                        SCALE, None)
+
+    def phase(p):
+        return lambda: A.flash_attention_backward_bf16_phase(p, dq, dk, dv, delta, g, out, lse,
+                                                             q, k, v, BH, T, D, SCALE, None)
+
+    def step():
+        fwd()
+        bwd()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_step = start.elapsed_time(end) / args.steps
+    print(f"[bench] step fwd+bwd {ms_step:.3f} ms (wall {1e3 * wall / args.steps:.3f} ms)",
+          file=sys.stderr, flush=True)
+
+    # per-kernel averages (same stream, back-to-back launches)
+    kern_ms = {
+        "fwd": event_time_ms(fwd, args.reps, stream),
+        "bwd_delta": event_time_ms(phase(0), args.reps, stream),
+        "bwd_dq": event_time_ms(phase(1), args.reps, stream),
+        "bwd_dkdv": event_time_ms(phase(2), args.reps, stream),
+    }
+    bwd_ms = event_time_ms(bwd, args.reps, stream)
+    print(f"[bench] kernels {json.dumps({k: round(x, 4) for k, x in kern_ms.items()})}",
+          file=sys.stderr, flush=True)
+
+    # ---- decode (config 4), rotating cache copies, launches captured in a graph ----
+    import numpy as np
+    from dadgpt_amd import synth
+    lens_h = synth.uniform_int(1, DEC_L, DEC_N, synth.BASE_SEED ^ synth.TENSOR_ID["lens"])
+    lens = torch.from_numpy(lens_h.astype(np.int32)).to(dev)
+    dec_bytes = int(2 * lens_h.sum() * DEC_H * DEC_D * 2 + 2 * DEC_N * DEC_H * DEC_D * 2)
+    ncopy = args.decode_copies
+    kcs = [randn(DEC_N, DEC_H, DEC_L, DEC_D) for _ in range(ncopy)]
+    vcs = [randn(DEC_N, DEC_H, DEC_L, DEC_D) for _ in range(ncopy)]
+    qd = randn(DEC_N, DEC_H, DEC_D)
+    od = torch.empty_like(qd)
+    ws = A.decode_workspace(DEC_N, DEC_H, DEC_L, DEC_D)
+
+    def decode(i):
+        A.decode_attention(od, qd, kcs[i % ncopy], vcs[i % ncopy], lens, DEC_N, DEC_H, DEC_L,
+                           DEC_D, SCALE, ws, None)
+
+    for i in range(ncopy):
+        decode(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    per_graph = 4 * ncopy
+    with torch.cuda.graph(graph):
+        for i in range(per_graph):
+            decode(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    gstream = torch.cuda.current_stream()
+    dec_ms = event_time_ms(graph.replay, 5, gstream) / per_graph
+    dec_gbps = dec_bytes / (dec_ms * 1e-3) / 1e9
+    # eager launches of one copy: the cache stays MALL-resident, launch gaps included
+    eager_dec_ms = event_time_ms(lambda: decode(0), args.reps, stream)
+    print(f"[bench] decode {dec_ms * 1e3:.2f} us/launch in graph ({dec_gbps:.0f} GB/s), eager "
+          f"same-copy {eager_dec_ms * 1e3:.2f} us", file=sys.stderr, flush=True)
+
+    comps = {}
+    for name, ms in kern_ms.items():
+        c = {"ms": round(ms, 5)}
+        if name in KERNEL_FLOPS:
+            tf = KERNEL_FLOPS[name] / (ms * 1e-3) / 1e12
+            c.update({"algorithmic_gflop": round(KERNEL_FLOPS[name] / 1e9, 3),
+                      "tflops": round(tf, 2), "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)})
+        comps[name] = c
+    comps["fwd_total"] = {"ms": round(kern_ms["fwd"], 5),
+                          "tflops": round(FWD_FLOPS / (kern_ms["fwd"] * 1e-3) / 1e12, 2)}
+    comps["bwd_total"] = {"ms": round(bwd_ms, 5),
+                          "tflops": round(BWD_FLOPS / (bwd_ms * 1e-3) / 1e12, 2)}
+    comps["bwd_total"]["frac_mfma_peak"] = round(comps["bwd_total"]["tflops"] / PEAK_BF16_TFLOPS, 4)
+    comps["fwd_total"]["frac_mfma_peak"] = round(comps["fwd_total"]["tflops"] / PEAK_BF16_TFLOPS, 4)
+    comps["decode"] = {"us_per_launch": round(dec_ms * 1e3, 3), "bytes": dec_bytes,
+                       "gbps": round(dec_gbps, 1), "frac_hbm_peak": round(dec_gbps / PEAK_HBM_GBPS, 4),
+                       "eager_same_copy_us_per_launch": round(eager_dec_ms * 1e3, 3),
+                       "cache_copies": ncopy,
+                       "config": "32 seqs, H12, D64, bf16 cache [32,12,1024,64], lens U[1,1024]"}
+
+    dom = max(("fwd", "bwd_dq", "bwd_dkdv"), key=lambda n: kern_ms[n])
+    ach = KERNEL_FLOPS[dom] / (kern_ms[dom] * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": load_traffic(dom)}
+
+    value = (FWD_FLOPS + BWD_FLOPS) / (ms_step * 1e-3) / 1e12
+    line = {
+        "metric": "attn fwd/bwd TFLOP/s (B16 H12 T1024 D64 bf16); KV-decode HBM GB/s",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1), resident in HBM",
+        "config": {"workload": "causal attention forward+backward, B16 H12 T1024 D64 "
+                               "(BASELINE config 3)",
+                   "B": B, "H": H, "T": T, "D": D, "scale": SCALE, "causal": True,
+                   "dropout": 0.0},
+        "roofline": roofline,
+        "components": comps,
+        "decode_gbps": round(dec_gbps, 1),
+    }
+    if not args.no_cpu_baseline:
+        print(f"[bench] cpu baseline on {args.cpu_slices} slices ...", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline(args.cpu_slices)
+        line["cpu_baseline"]["seconds"] = round(line["cpu_baseline"]["seconds"], 3)
+        line["cpu_baseline"]["value"] = float(f"{line['cpu_baseline']['value']:.6g}")
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

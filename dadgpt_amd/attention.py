@@ -1,0 +1,265 @@
+"""Python mirror of the attention wrappers, over the C ABI of ``libdadgpt_attn.so``.
+
+Function names, argument order and meaning follow the reference's launch wrappers
+(``cuda/gpu_ops.cuh:112-122``): raw device buffers in ``[BH, S, d_head]`` layout, ``lse`` and
+``delta`` ``[BH, S]``, outputs overwritten; errors raise (``RuntimeError`` as the reference's
+``CUDA_CHECK`` throws ``std::runtime_error``, ``cuda/gpu_ops.cuh:10-17``). Here the buffers
+are torch tensors: torch provides device memory and the stream, the library does the work.
+
+The product path has no fallback: if the HIP library is missing or fails to load, every
+call raises ``LibraryNotBuilt``.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libdadgpt_attn.so")
+
+# Symbols declared in include/dadgpt/gpu_attention.h (C linkage) and
+# include/dadgpt/gpu_ops_attention.hpp (C++ linkage, reference names).
+C_SYMBOLS = (
+    "dadgpt_last_error",
+    "dadgpt_status_string",
+    "dadgpt_version",
+    "dadgpt_flash_attention_supported",
+    "dadgpt_flash_attention_forward",
+    "dadgpt_flash_attention_backward",
+    "dadgpt_flash_attention_forward_async",
+    "dadgpt_flash_attention_backward_async",
+    "dadgpt_flash_attention_forward_bf16",
+    "dadgpt_flash_attention_backward_bf16",
+    "dadgpt_flash_attention_backward_bf16_phase",
+    "dadgpt_decode_workspace_bytes",
+    "dadgpt_decode_attention_bf16",
+    "dadgpt_decode_attention_f32",
+)
+CXX_SYMBOLS = (
+    "_Z29gpu_flash_attention_supportedi",
+    "_Z27gpu_flash_attention_forwardPfS_PKfS1_S1_iiif",
+    "_Z28gpu_flash_attention_backwardPfS_S_S_PKfS1_S1_S1_S1_S1_iiif",
+)
+
+STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported", 3: "hip error", 4: "workspace"}
+
+
+class LibraryNotBuilt(RuntimeError):
+    pass
+
+
+class AttentionError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(message or STATUS.get(status, f"status {status}"))
+        self.status = status
+
+
+_lib = None
+
+
+def lib():
+    """The loaded HIP library. torch is imported first so the library binds to the same HIP
+    runtime (libamdhip64.so.7) torch already loaded."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise LibraryNotBuilt(f"{LIB_PATH} is not built; run __graft_entry__.build() or "
+                              f"`make -C dadgpt_amd/csrc`")
+    try:
+        L = ctypes.CDLL(LIB_PATH)
+    except OSError as e:  # pragma: no cover - depends on the machine
+        raise LibraryNotBuilt(f"cannot load {LIB_PATH}: {e}") from e
+    vp, i, f, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    L.dadgpt_last_error.restype = ctypes.c_char_p
+    L.dadgpt_last_error.argtypes = []
+    L.dadgpt_status_string.restype = ctypes.c_char_p
+    L.dadgpt_status_string.argtypes = [i]
+    L.dadgpt_version.restype = ctypes.c_char_p
+    L.dadgpt_version.argtypes = []
+    L.dadgpt_flash_attention_supported.argtypes = [i]
+    L.dadgpt_flash_attention_forward.argtypes = [vp] * 5 + [i, i, i, f]
+    L.dadgpt_flash_attention_backward.argtypes = [vp] * 10 + [i, i, i, f]
+    L.dadgpt_flash_attention_forward_async.argtypes = [vp] * 5 + [i, i, i, f, vp]
+    L.dadgpt_flash_attention_backward_async.argtypes = [vp] * 10 + [i, i, i, f, vp]
+    L.dadgpt_flash_attention_forward_bf16.argtypes = [vp] * 5 + [i, i, i, f, vp]
+    L.dadgpt_flash_attention_backward_bf16.argtypes = [vp] * 10 + [i, i, i, f, vp]
+    L.dadgpt_flash_attention_backward_bf16_phase.argtypes = [i] + [vp] * 10 + [i, i, i, f, vp]
+    L.dadgpt_decode_workspace_bytes.restype = sz
+    L.dadgpt_decode_workspace_bytes.argtypes = [i, i, i, i]
+    L.dadgpt_decode_attention_bf16.argtypes = [vp] * 5 + [i, i, i, i, f, vp, sz, vp]
+    L.dadgpt_decode_attention_f32.argtypes = [vp] * 5 + [i, i, i, i, f, vp, sz, vp]
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return lib().dadgpt_last_error().decode()
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise AttentionError(status, last_error())
+
+
+def _ptr(t) -> int | None:
+    """Device address of a tensor (None for None: the C side reports the null pointer)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def _stream_ptr(stream) -> int | None:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream or None
+
+
+def _require(t, name, dtype, numel, device=None):
+    if t is None:
+        return
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.numel() < numel:
+        raise ValueError(f"{name} has {t.numel()} elements, needs {numel}")
+
+
+# --------------------------------------------------------------- reference-named wrappers
+
+def flash_attention_supported(d_head: int) -> bool:
+    """gpu_flash_attention_supported (cuda/gpu_ops.cuh:115)."""
+    return bool(lib().dadgpt_flash_attention_supported(int(d_head)))
+
+
+def flash_attention_forward(out, lse, q, k, v, BH: int, S: int, d_head: int, scale: float,
+                            stream=None) -> None:
+    """gpu_flash_attention_forward (cuda/gpu_ops.cuh:116-117). fp32 buffers, overwritten."""
+    n = BH * S * d_head
+    for t, nm in ((out, "out"), (q, "q"), (k, "k"), (v, "v")):
+        _require(t, nm, torch.float32, n)
+    _require(lse, "lse", torch.float32, BH * S)
+    _check(lib().dadgpt_flash_attention_forward_async(
+        _ptr(out), _ptr(lse), _ptr(q), _ptr(k), _ptr(v), BH, S, d_head, scale,
+        _stream_ptr(stream)))
+
+
+def flash_attention_backward(dq, dk, dv, delta, dout, out, lse, q, k, v, BH: int, S: int,
+                             d_head: int, scale: float, stream=None) -> None:
+    """gpu_flash_attention_backward (cuda/gpu_ops.cuh:119-122). Writes dq, dk, dv and the
+    delta scratch."""
+    n = BH * S * d_head
+    for t, nm in ((dq, "dq"), (dk, "dk"), (dv, "dv"), (dout, "dout"), (out, "out"),
+                  (q, "q"), (k, "k"), (v, "v")):
+        _require(t, nm, torch.float32, n)
+    _require(delta, "delta", torch.float32, BH * S)
+    _require(lse, "lse", torch.float32, BH * S)
+    _check(lib().dadgpt_flash_attention_backward_async(
+        _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta), _ptr(dout), _ptr(out), _ptr(lse), _ptr(q),
+        _ptr(k), _ptr(v), BH, S, d_head, scale, _stream_ptr(stream)))
+
+
+def flash_attention_forward_bf16(out, lse, q, k, v, BH: int, S: int, d_head: int,
+                                 scale: float, stream=None) -> None:
+    n = BH * S * d_head
+    for t, nm in ((out, "out"), (q, "q"), (k, "k"), (v, "v")):
+        _require(t, nm, torch.bfloat16, n)
+    _require(lse, "lse", torch.float32, BH * S)
+    _check(lib().dadgpt_flash_attention_forward_bf16(
+        _ptr(out), _ptr(lse), _ptr(q), _ptr(k), _ptr(v), BH, S, d_head, scale,
+        _stream_ptr(stream)))
+
+
+def flash_attention_backward_bf16(dq, dk, dv, delta, dout, out, lse, q, k, v, BH: int, S: int,
+                                  d_head: int, scale: float, stream=None) -> None:
+    n = BH * S * d_head
+    for t, nm in ((dq, "dq"), (dk, "dk"), (dv, "dv"), (dout, "dout"), (out, "out"),
+                  (q, "q"), (k, "k"), (v, "v")):
+        _require(t, nm, torch.bfloat16, n)
+    _require(delta, "delta", torch.float32, BH * S)
+    _require(lse, "lse", torch.float32, BH * S)
+    _check(lib().dadgpt_flash_attention_backward_bf16(
+        _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta), _ptr(dout), _ptr(out), _ptr(lse), _ptr(q),
+        _ptr(k), _ptr(v), BH, S, d_head, scale, _stream_ptr(stream)))
+
+
+def flash_attention_backward_bf16_phase(phase: int, dq, dk, dv, delta, dout, out, lse, q, k, v,
+                                        BH: int, S: int, d_head: int, scale: float,
+                                        stream=None) -> None:
+    """One kernel of the bf16 backward (0 delta, 1 dq, 2 dk/dv), for per-kernel timing."""
+    _check(lib().dadgpt_flash_attention_backward_bf16_phase(
+        int(phase), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta), _ptr(dout), _ptr(out), _ptr(lse),
+        _ptr(q), _ptr(k), _ptr(v), BH, S, d_head, scale, _stream_ptr(stream)))
+
+
+def decode_workspace_bytes(n_seq: int, n_heads: int, max_len: int, d_head: int) -> int:
+    return int(lib().dadgpt_decode_workspace_bytes(n_seq, n_heads, max_len, d_head))
+
+
+def decode_workspace(n_seq, n_heads, max_len, d_head, device="cuda"):
+    """A zero-filled workspace for decode_attention (its counters must start at zero)."""
+    nbytes = decode_workspace_bytes(n_seq, n_heads, max_len, d_head)
+    return torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
+
+
+def decode_attention(out, q, k_cache, v_cache, lens, n_seq, n_heads, max_len, d_head, scale,
+                     workspace, stream=None) -> None:
+    """Ragged KV-cache decode (the per-head composition of src/model.cpp:758-790 as one
+    launch). bf16 or fp32 by the tensors' dtype; lens is a device int32 tensor."""
+    dt = q.dtype
+    if dt not in (torch.bfloat16, torch.float32):
+        raise TypeError("decode_attention: q must be bfloat16 or float32")
+    _require(q, "q", dt, n_seq * n_heads * d_head)
+    _require(out, "out", dt, n_seq * n_heads * d_head)
+    _require(k_cache, "k_cache", dt, n_seq * n_heads * max_len * d_head)
+    _require(v_cache, "v_cache", dt, n_seq * n_heads * max_len * d_head)
+    _require(lens, "lens", torch.int32, n_seq)
+    if workspace is not None and (not workspace.is_cuda or not workspace.is_contiguous()):
+        raise ValueError("workspace must be a contiguous device tensor")
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    fn = (lib().dadgpt_decode_attention_bf16 if dt == torch.bfloat16
+          else lib().dadgpt_decode_attention_f32)
+    _check(fn(_ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(lens), n_seq, n_heads,
+              max_len, d_head, scale, _ptr(workspace), ws_bytes, _stream_ptr(stream)))
+
+
+# --------------------------------------------------------------- allocating conveniences
+
+def default_scale(d_head: int) -> float:
+    """1/sqrt(d_head), as src/model.cpp:389 computes it (in fp32)."""
+    return float(torch.tensor(1.0 / math.sqrt(d_head), dtype=torch.float32))
+
+
+def attention_forward(q, k, v, scale=None):
+    """Allocating forward: q, k, v [BH, S, D] (fp32 or bf16) -> (out, lse)."""
+    BH, S, D = q.shape
+    scale = default_scale(D) if scale is None else scale
+    out = torch.empty_like(q)
+    lse = torch.empty((BH, S), dtype=torch.float32, device=q.device)
+    if q.dtype == torch.bfloat16:
+        flash_attention_forward_bf16(out, lse, q, k, v, BH, S, D, scale)
+    else:
+        flash_attention_forward(out, lse, q, k, v, BH, S, D, scale)
+    return out, lse
+
+
+def attention_backward(dout, out, lse, q, k, v, scale=None):
+    """Allocating backward -> (dq, dk, dv, delta)."""
+    BH, S, D = q.shape
+    scale = default_scale(D) if scale is None else scale
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    delta = torch.empty((BH, S), dtype=torch.float32, device=q.device)
+    if q.dtype == torch.bfloat16:
+        flash_attention_backward_bf16(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, D,
+                                      scale)
+    else:
+        flash_attention_backward(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, D, scale)
+    return dq, dk, dv, delta

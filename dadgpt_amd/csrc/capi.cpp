@@ -1,0 +1,227 @@
+// extern "C" entry points of libdadgpt_attn.so (declared in include/dadgpt/gpu_attention.h).
+// Every argument check runs on the host before any HIP call, so each error path can be
+// exercised on a machine without a GPU; a failing call records a thread-local message and
+// returns a status instead of throwing across the C boundary.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+
+#include "dadgpt/gpu_attention.h"
+#include "kernels.hpp"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int ok() {
+  g_last_error[0] = '\0';
+  return DADGPT_OK;
+}
+
+int from_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(DADGPT_ERR_HIP, "%s: HIP error %d (%s)", what, static_cast<int>(e),
+              hipGetErrorString(e));
+}
+
+bool supported(int d_head) { return d_head == 32 || d_head == 64; }
+
+// Tensors are read with 16-byte vector loads: every buffer must be non-null and 16-byte
+// aligned (any contiguous [BH,S,D] tensor from a device allocator is).
+int check_ptrs(const char* fn, std::initializer_list<const void*> ptrs) {
+  int i = 0;
+  for (const void* p : ptrs) {
+    if (p == nullptr)
+      return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: pointer argument %d is null", fn, i);
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+      return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: pointer argument %d is not 16-byte aligned",
+                  fn, i);
+    ++i;
+  }
+  return DADGPT_OK;
+}
+
+// Largest S for one grid row: the kernels index rows with int and grid.y <= 65535 blocks.
+constexpr long kMaxRows = 1L << 24;
+
+int check_attn(const char* fn, int BH, int S, int d_head, float scale,
+               std::initializer_list<const void*> ptrs) {
+  if (int st = check_ptrs(fn, ptrs)) return st;
+  if (BH < 1 || S < 1)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: BH=%d and S=%d must be positive", fn, BH, S);
+  if (S > kMaxRows) return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: S=%d too large", fn, S);
+  if (!supported(d_head))
+    return fail(DADGPT_ERR_UNSUPPORTED, "flash attention: unsupported d_head %d", d_head);
+  if (!std::isfinite(scale))
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: scale must be finite", fn);
+  return DADGPT_OK;
+}
+
+int check_decode(const char* fn, int n_seq, int H, int max_len, int d_head, float scale,
+                 const void* ws, size_t ws_bytes, std::initializer_list<const void*> ptrs) {
+  if (int st = check_ptrs(fn, ptrs)) return st;
+  if (n_seq < 1 || H < 1 || max_len < 1)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                "%s: n_seq=%d, n_heads=%d, max_len=%d must be positive", fn, n_seq, H, max_len);
+  if (n_seq > 65535 || H > 65535 || max_len > kMaxRows)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: shape exceeds launch limits", fn);
+  if (!supported(d_head))
+    return fail(DADGPT_ERR_UNSUPPORTED, "decode attention: unsupported d_head %d", d_head);
+  if (!std::isfinite(scale))
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: scale must be finite", fn);
+  const size_t need = dadgpt::decode_workspace_bytes(n_seq, H, max_len, d_head);
+  if (ws == nullptr || ws_bytes < need)
+    return fail(DADGPT_ERR_WORKSPACE, "%s: workspace of %zu bytes given, %zu needed", fn,
+                ws == nullptr ? 0 : ws_bytes, need);
+  return DADGPT_OK;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+using dadgpt::bf16;
+const bf16* B(const uint16_t* p) { return reinterpret_cast<const bf16*>(p); }
+bf16* B(uint16_t* p) { return reinterpret_cast<bf16*>(p); }
+
+}  // namespace
+
+extern "C" {
+
+const char* dadgpt_last_error(void) { return g_last_error; }
+
+const char* dadgpt_status_string(int status) {
+  switch (status) {
+    case DADGPT_OK: return "ok";
+    case DADGPT_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case DADGPT_ERR_UNSUPPORTED: return "unsupported";
+    case DADGPT_ERR_HIP: return "hip error";
+    case DADGPT_ERR_WORKSPACE: return "workspace";
+    default: return "unknown status";
+  }
+}
+
+const char* dadgpt_version(void) { return "dadgpt-mi355x attention 0.1 (gfx950)"; }
+
+int dadgpt_flash_attention_supported(int d_head) { return supported(d_head) ? 1 : 0; }
+
+int dadgpt_flash_attention_forward_async(float* out, float* lse, const float* q, const float* k,
+                                         const float* v, int BH, int S, int d_head,
+                                         float scale, void* stream) {
+  const char* fn = "dadgpt_flash_attention_forward";
+  if (int st = check_attn(fn, BH, S, d_head, scale, {out, lse, q, k, v})) return st;
+  return from_hip(dadgpt::launch_fwd_f32(out, lse, q, k, v, BH, S, d_head, scale,
+                                         as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_flash_attention_forward(float* out, float* lse, const float* q, const float* k,
+                                   const float* v, int BH, int S, int d_head, float scale) {
+  return dadgpt_flash_attention_forward_async(out, lse, q, k, v, BH, S, d_head, scale, nullptr);
+}
+
+int dadgpt_flash_attention_backward_async(float* dq, float* dk, float* dv, float* delta,
+                                          const float* dout, const float* out,
+                                          const float* lse, const float* q, const float* k,
+                                          const float* v, int BH, int S, int d_head,
+                                          float scale, void* stream) {
+  const char* fn = "dadgpt_flash_attention_backward";
+  if (int st = check_attn(fn, BH, S, d_head, scale, {dq, dk, dv, delta, dout, out, lse, q, k, v}))
+    return st;
+  return from_hip(dadgpt::launch_bwd_f32(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S,
+                                         d_head, scale, as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_flash_attention_backward(float* dq, float* dk, float* dv, float* delta,
+                                    const float* dout, const float* out, const float* lse,
+                                    const float* q, const float* k, const float* v, int BH,
+                                    int S, int d_head, float scale) {
+  return dadgpt_flash_attention_backward_async(dq, dk, dv, delta, dout, out, lse, q, k, v, BH,
+                                               S, d_head, scale, nullptr);
+}
+
+int dadgpt_flash_attention_forward_bf16(uint16_t* out, float* lse, const uint16_t* q,
+                                        const uint16_t* k, const uint16_t* v, int BH, int S,
+                                        int d_head, float scale, void* stream) {
+  const char* fn = "dadgpt_flash_attention_forward_bf16";
+  if (int st = check_attn(fn, BH, S, d_head, scale, {out, lse, q, k, v})) return st;
+  return from_hip(dadgpt::launch_fwd_bf16(B(out), lse, B(q), B(k), B(v), BH, S, d_head, scale,
+                                          as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_flash_attention_backward_bf16(uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                                         float* delta, const uint16_t* dout,
+                                         const uint16_t* out, const float* lse,
+                                         const uint16_t* q, const uint16_t* k,
+                                         const uint16_t* v, int BH, int S, int d_head,
+                                         float scale, void* stream) {
+  const char* fn = "dadgpt_flash_attention_backward_bf16";
+  if (int st = check_attn(fn, BH, S, d_head, scale, {dq, dk, dv, delta, dout, out, lse, q, k, v}))
+    return st;
+  return from_hip(dadgpt::launch_bwd_bf16(B(dq), B(dk), B(dv), delta, B(dout), B(out), lse,
+                                          B(q), B(k), B(v), BH, S, d_head, scale,
+                                          as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_flash_attention_backward_bf16_phase(int phase, uint16_t* dq, uint16_t* dk,
+                                               uint16_t* dv, float* delta, const uint16_t* dout,
+                                               const uint16_t* out, const float* lse,
+                                               const uint16_t* q, const uint16_t* k,
+                                               const uint16_t* v, int BH, int S, int d_head,
+                                               float scale, void* stream) {
+  const char* fn = "dadgpt_flash_attention_backward_bf16_phase";
+  if (phase < 0 || phase > 2)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: phase %d not in {0,1,2}", fn, phase);
+  if (int st = check_attn(fn, BH, S, d_head, scale, {dq, dk, dv, delta, dout, out, lse, q, k, v}))
+    return st;
+  return from_hip(dadgpt::launch_bwd_bf16(B(dq), B(dk), B(dv), delta, B(dout), B(out), lse,
+                                          B(q), B(k), B(v), BH, S, d_head, scale,
+                                          as_stream(stream), 1 << phase),
+                  fn);
+}
+
+size_t dadgpt_decode_workspace_bytes(int n_seq, int n_heads, int max_len, int d_head) {
+  if (n_seq < 1 || n_heads < 1 || max_len < 1 || !supported(d_head)) return 0;
+  return dadgpt::decode_workspace_bytes(n_seq, n_heads, max_len, d_head);
+}
+
+int dadgpt_decode_attention_bf16(uint16_t* out, const uint16_t* q, const uint16_t* k_cache,
+                                 const uint16_t* v_cache, const int32_t* lens, int n_seq,
+                                 int n_heads, int max_len, int d_head, float scale,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "dadgpt_decode_attention_bf16";
+  if (int st = check_decode(fn, n_seq, n_heads, max_len, d_head, scale, workspace,
+                            workspace_bytes, {out, q, k_cache, v_cache, lens}))
+    return st;
+  return from_hip(dadgpt::launch_decode_bf16(B(out), B(q), B(k_cache), B(v_cache), lens, n_seq,
+                                             n_heads, max_len, d_head, scale, workspace,
+                                             as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_decode_attention_f32(float* out, const float* q, const float* k_cache,
+                                const float* v_cache, const int32_t* lens, int n_seq,
+                                int n_heads, int max_len, int d_head, float scale,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "dadgpt_decode_attention_f32";
+  if (int st = check_decode(fn, n_seq, n_heads, max_len, d_head, scale, workspace,
+                            workspace_bytes, {out, q, k_cache, v_cache, lens}))
+    return st;
+  return from_hip(dadgpt::launch_decode_f32(out, q, k_cache, v_cache, lens, n_seq, n_heads,
+                                            max_len, d_head, scale, workspace,
+                                            as_stream(stream)),
+                  fn);
+}
+
+}  // extern "C"

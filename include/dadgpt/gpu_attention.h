@@ -1,0 +1,129 @@
+/*
+ * libdadgpt_attn.so — C ABI of the MI355X (gfx950) fused causal attention path.
+ *
+ * Drop-in for the attention launch wrappers of the reference (Jimdrews/DadGPT,
+ * cuda/gpu_ops.cuh:112-122, defined in cuda/attention.cu:232-252) plus the KV-cache decode
+ * that the reference composes inline in src/model.cpp:758-790. The C++-linkage functions
+ * with the reference's exact names and signatures are declared in
+ * <dadgpt/gpu_ops_attention.hpp> and defined in the same library.
+ *
+ * Conventions (shared by every entry point):
+ *  - All tensor pointers are device pointers owned by the caller, 16-byte aligned (checked);
+ *    the library allocates nothing in these calls. Layout [BH, S, d_head] contiguous, heads
+ *    already split
+ *    (cuda/attention.cu:6); lse and delta are [BH, S] fp32; lse is the natural-log
+ *    logsumexp of the scaled scores (cuda/attention.cu:71).
+ *  - bf16 tensors are passed as uint16_t* holding IEEE bfloat16 bit patterns.
+ *  - Outputs are overwritten, never accumulated (cuda/gpu_ops.cuh:118).
+ *  - Arguments are validated on the host before any HIP call; a failing call returns a
+ *    nonzero dadgpt_status and dadgpt_last_error() describes it (thread-local). Launch errors
+ *    (hipGetLastError) map to DADGPT_ERR_HIP; asynchronous faults surface at the caller's
+ *    next synchronisation, as in the reference (cuda/gpu_ops.cuh:10-17).
+ *  - Functions without a stream argument launch on the null (legacy default) stream, as the
+ *    reference does (cuda/attention.cu:211,220-226). `stream` arguments take a hipStream_t;
+ *    NULL means the null stream.
+ */
+#ifndef DADGPT_GPU_ATTENTION_H
+#define DADGPT_GPU_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum dadgpt_status {
+  DADGPT_OK = 0,
+  DADGPT_ERR_INVALID_ARGUMENT = 1, /* null pointer, non-positive size, bad scale */
+  DADGPT_ERR_UNSUPPORTED = 2,      /* d_head outside the supported set */
+  DADGPT_ERR_HIP = 3,              /* a HIP launch reported an error */
+  DADGPT_ERR_WORKSPACE = 4         /* decode workspace missing or too small */
+} dadgpt_status;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* dadgpt_last_error(void);
+/* Static name of a status code. */
+const char* dadgpt_status_string(int status);
+/* Library version string. */
+const char* dadgpt_version(void);
+
+/* Replaces bool gpu_flash_attention_supported(int d_head) — cuda/gpu_ops.cuh:115,
+ * cuda/attention.cu:232. Returns 1 for d_head in {32, 64}, else 0. */
+int dadgpt_flash_attention_supported(int d_head);
+
+/* Replaces gpu_flash_attention_forward — cuda/gpu_ops.cuh:116-117, cuda/attention.cu:234-239.
+ * fp32 q,k,v -> out [BH,S,d_head], lse [BH,S]. Null stream. */
+int dadgpt_flash_attention_forward(float* out, float* lse, const float* q, const float* k,
+                                   const float* v, int BH, int S, int d_head, float scale);
+
+/* Replaces gpu_flash_attention_backward — cuda/gpu_ops.cuh:119-122,
+ * cuda/attention.cu:241-252. Writes dq, dk, dv; delta [BH,S] is caller scratch
+ * (src/model.cpp:250). Null stream. */
+int dadgpt_flash_attention_backward(float* dq, float* dk, float* dv, float* delta,
+                                    const float* dout, const float* out, const float* lse,
+                                    const float* q, const float* k, const float* v, int BH,
+                                    int S, int d_head, float scale);
+
+/* Stream-ordered variants of the two fp32 calls above (no reference counterpart: the
+ * reference has no stream argument). */
+int dadgpt_flash_attention_forward_async(float* out, float* lse, const float* q,
+                                         const float* k, const float* v, int BH, int S,
+                                         int d_head, float scale, void* stream);
+int dadgpt_flash_attention_backward_async(float* dq, float* dk, float* dv, float* delta,
+                                          const float* dout, const float* out,
+                                          const float* lse, const float* q, const float* k,
+                                          const float* v, int BH, int S, int d_head,
+                                          float scale, void* stream);
+
+/* bf16 sibling of gpu_flash_attention_forward (no reference counterpart: the reference's
+ * attention is fp32-only, cuda/attention.cu:1). bf16 q,k,v,out; fp32 lse. MFMA, fp32
+ * accumulation. */
+int dadgpt_flash_attention_forward_bf16(uint16_t* out, float* lse, const uint16_t* q,
+                                        const uint16_t* k, const uint16_t* v, int BH, int S,
+                                        int d_head, float scale, void* stream);
+
+/* bf16 sibling of gpu_flash_attention_backward (no reference counterpart). bf16
+ * dout/out/q/k/v in, bf16 dq/dk/dv out (overwritten); fp32 lse in; delta [BH,S] fp32
+ * scratch, written. */
+int dadgpt_flash_attention_backward_bf16(uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                                         float* delta, const uint16_t* dout,
+                                         const uint16_t* out, const float* lse,
+                                         const uint16_t* q, const uint16_t* k,
+                                         const uint16_t* v, int BH, int S, int d_head,
+                                         float scale, void* stream);
+
+/* One kernel of dadgpt_flash_attention_backward_bf16, for per-kernel timing and profiling
+ * (no reference counterpart). phase 0: delta = rowsum(dout * out); 1: dq (reads delta);
+ * 2: dk, dv (reads delta). Running phases 0, 1, 2 in order equals the full backward. */
+int dadgpt_flash_attention_backward_bf16_phase(int phase, uint16_t* dq, uint16_t* dk,
+                                               uint16_t* dv, float* delta,
+                                               const uint16_t* dout, const uint16_t* out,
+                                               const float* lse, const uint16_t* q,
+                                               const uint16_t* k, const uint16_t* v, int BH,
+                                               int S, int d_head, float scale, void* stream);
+
+/* Bytes of decode workspace for a cache shape. The workspace must be zero-filled once when
+ * allocated (it holds arrival counters that every call leaves at zero); calls that share a
+ * workspace must not overlap in time. */
+size_t dadgpt_decode_workspace_bytes(int n_seq, int n_heads, int max_len, int d_head);
+
+/* KV-cache decode attention (replaces the per-head composition in src/model.cpp:758-790:
+ * q K^T, *scale, softmax over the cache length, P V; no reference signature exists).
+ *  q [n_seq, n_heads, d_head]; k_cache, v_cache [n_seq, n_heads, max_len, d_head];
+ *  lens: DEVICE int32 [n_seq], valid cache rows per sequence (clamped to [0, max_len];
+ *  a length of 0 yields a zero output row); out [n_seq, n_heads, d_head]. */
+int dadgpt_decode_attention_bf16(uint16_t* out, const uint16_t* q, const uint16_t* k_cache,
+                                 const uint16_t* v_cache, const int32_t* lens, int n_seq,
+                                 int n_heads, int max_len, int d_head, float scale,
+                                 void* workspace, size_t workspace_bytes, void* stream);
+int dadgpt_decode_attention_f32(float* out, const float* q, const float* k_cache,
+                                const float* v_cache, const int32_t* lens, int n_seq,
+                                int n_heads, int max_len, int d_head, float scale,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DADGPT_GPU_ATTENTION_H */

@@ -1,0 +1,21 @@
+// The reference's fused-attention wrappers under their own names and C++ signatures
+// (cuda/gpu_ops.cuh:112-122), defined in libdadgpt_attn.so on top of the C ABI in
+// <dadgpt/gpu_attention.h>. A caller compiled against the reference's gpu_ops.cuh (for
+// example src/model.cpp:186,392,570) links against these symbols unchanged.
+//
+// Error behaviour follows the reference: argument and launch errors throw
+// std::runtime_error (cuda/gpu_ops.cuh:10-17; unsupported d_head at cuda/attention.cu:238,251).
+#pragma once
+
+// cuda/gpu_ops.cuh:115
+bool gpu_flash_attention_supported(int d_head);
+
+// cuda/gpu_ops.cuh:116-117
+void gpu_flash_attention_forward(float* out, float* lse, const float* q, const float* k,
+                                 const float* v, int BH, int S, int d_head, float scale);
+
+// cuda/gpu_ops.cuh:119-122
+void gpu_flash_attention_backward(float* dq, float* dk, float* dv, float* delta, const float* dout,
+                                  const float* out, const float* lse, const float* q,
+                                  const float* k, const float* v, int BH, int S, int d_head,
+                                  float scale);

@@ -1,0 +1,138 @@
+"""CPU tests of the C ABI boundary: the library loads, exports every symbol the headers
+declare, and rejects bad arguments on the host before any HIP call (no compute calls are
+made here)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from dadgpt_amd import attention as A
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dadgpt", "gpu_attention.h")
+FAKE = 0x1000  # a non-null address; every call below fails validation before using it
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(dadgpt_\w+)\s*\(", text)))
+
+
+def exported_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", A.LIB_PATH], check=True,
+                         capture_output=True, text=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_header_and_binding_agree():
+    assert header_functions() == sorted(A.C_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    syms = exported_symbols()
+    missing = [s for s in A.C_SYMBOLS + A.CXX_SYMBOLS if s not in syms]
+    assert not missing, missing
+    L = A.lib()
+    for s in A.C_SYMBOLS:
+        assert hasattr(L, s)
+
+
+def test_version_and_status_strings():
+    L = A.lib()
+    assert b"gfx950" in L.dadgpt_version()
+    assert L.dadgpt_status_string(0) == b"ok"
+    assert L.dadgpt_status_string(2) == b"unsupported"
+
+
+def test_supported_predicate():
+    assert A.flash_attention_supported(32) and A.flash_attention_supported(64)
+    for d in (0, 16, 48, 80, 128, -64):
+        assert not A.flash_attention_supported(d)
+
+
+@pytest.mark.parametrize("fn", ["dadgpt_flash_attention_forward",
+                                "dadgpt_flash_attention_forward_bf16"])
+def test_forward_validation(fn):
+    L = A.lib()
+    f = getattr(L, fn)
+    extra = [None] if fn.endswith("bf16") else []
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 48, 0.125, *extra) == 2
+    assert A.last_error() == "flash attention: unsupported d_head 48"
+    assert f(None, FAKE, FAKE, FAKE, FAKE, 4, 64, 64, 0.125, *extra) == 1
+    assert "pointer argument 0 is null" in A.last_error()
+    assert f(FAKE, FAKE, FAKE, FAKE, None, 4, 64, 64, 0.125, *extra) == 1
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 64, 64, 0.125, *extra) == 1
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 0, 64, 0.125, *extra) == 1
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 4, -3, 64, 0.125, *extra) == 1
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 64, float("nan"), *extra) == 1
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 64, float("inf"), *extra) == 1
+
+
+@pytest.mark.parametrize("fn", ["dadgpt_flash_attention_backward",
+                                "dadgpt_flash_attention_backward_bf16"])
+def test_backward_validation(fn):
+    f = getattr(A.lib(), fn)
+    extra = [None] if fn.endswith("bf16") else []
+    ptrs = [FAKE] * 10
+    assert f(*ptrs, 4, 64, 100, 0.125, *extra) == 2
+    for i in range(10):
+        bad = list(ptrs)
+        bad[i] = None
+        assert f(*bad, 4, 64, 64, 0.125, *extra) == 1
+        assert f"pointer argument {i} is null" in A.last_error()
+
+
+def test_backward_phase_validation():
+    f = A.lib().dadgpt_flash_attention_backward_bf16_phase
+    assert f(3, *[FAKE] * 10, 4, 64, 64, 0.125, None) == 1
+    assert f(-1, *[FAKE] * 10, 4, 64, 64, 0.125, None) == 1
+    assert f(1, *[FAKE] * 10, 4, 64, 40, 0.125, None) == 2
+
+
+def expected_ws(n, h, max_len, d):
+    return 4 * n * h * ((max_len + 255) // 256) * (d + 2) + 4 * n * h
+
+
+@pytest.mark.parametrize("n,h,L,d", [(32, 12, 1024, 64), (1, 1, 1, 32), (3, 5, 257, 64)])
+def test_decode_workspace_bytes(n, h, L, d):
+    assert A.decode_workspace_bytes(n, h, L, d) == expected_ws(n, h, L, d)
+
+
+def test_decode_workspace_bytes_rejects_bad_shapes():
+    assert A.decode_workspace_bytes(0, 12, 1024, 64) == 0
+    assert A.decode_workspace_bytes(4, 12, 1024, 48) == 0
+
+
+@pytest.mark.parametrize("fn", ["dadgpt_decode_attention_bf16", "dadgpt_decode_attention_f32"])
+def test_decode_validation(fn):
+    f = getattr(A.lib(), fn)
+    need = expected_ws(4, 2, 64, 64)
+    args = lambda **kw: [kw.get("out", FAKE), FAKE, FAKE, FAKE, kw.get("lens", FAKE),
+                         kw.get("n", 4), kw.get("h", 2), kw.get("L", 64), kw.get("d", 64),
+                         kw.get("scale", 0.125), kw.get("ws", FAKE), kw.get("wsb", need), None]
+    assert f(*args(d=48)) == 2
+    assert f(*args(out=None)) == 1
+    assert f(*args(lens=None)) == 1
+    assert f(*args(n=0)) == 1
+    assert f(*args(L=0)) == 1
+    assert f(*args(n=70000)) == 1
+    assert f(*args(scale=float("nan"))) == 1
+    assert f(*args(ws=None)) == 4
+    assert f(*args(wsb=need - 1)) == 4
+    assert "needed" in A.last_error()
+
+
+def test_cxx_reference_names_link_and_throw(tmp_path):
+    """A C++ caller using the reference's names/signatures links and gets the reference's
+    exceptions (built with g++ here; needs no GPU)."""
+    exe = tmp_path / "boundary_test"
+    libdir = os.path.dirname(A.LIB_PATH)
+    subprocess.run(["g++", "-std=c++20", "-O1", f"-I{ROOT}/include",
+                    os.path.join(ROOT, "tests", "cxx", "boundary_test.cpp"),
+                    f"-L{libdir}", "-ldadgpt_attn", f"-Wl,-rpath,{libdir}", "-o", str(exe)],
+                   check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.strip().endswith("OK")

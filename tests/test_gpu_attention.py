@@ -1,0 +1,315 @@
+"""GPU parity tests of the HIP attention kernels, through the C ABI, against the CPU oracle.
+
+Tolerances (from the path's specification):
+  fp32 kernels             max-abs <= 1e-5 against the fp32 CPU path (O, lse, dQ, dK, dV)
+  bf16 forward             O max-abs <= 2e-2 against the fp32 CPU path on the same
+                           bf16-rounded inputs; lse <= 1e-3
+  bf16 backward            dQ, dK, dV max-abs <= 5e-2
+  bf16 decode              max-abs <= 2e-2; fp32 decode <= 1e-5
+Full-size configurations are checked against the oracle on sampled (b,h) slices and through
+size-independent properties on every slice (row 0, causal prefix, column sums of dK and dV,
+bitwise repeatability).
+"""
+import ctypes
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from dadgpt_amd import attention as A
+from dadgpt_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5
+TOL_O = 2e-2
+TOL_LSE = 1e-3
+TOL_GRAD = 5e-2
+TOL_DEC = 2e-2
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def dev(x, dtype):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to("cuda").to(dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+def max_abs(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+def scale_of(D):
+    return float(np.float32(1.0 / math.sqrt(D)))
+
+
+# ----------------------------------------------------------------------------- fp32 path
+
+@pytest.mark.parametrize("name", ["cfg1_fwd_bwd.npz", "ragged70_fwd_bwd.npz"])
+def test_fp32_forward_backward_golden(gpu, golden_dir, name):
+    z = np.load(os.path.join(golden_dir, name))
+    BH, S, D = z["q"].shape
+    case(f"fp32 golden {name} BH={BH} S={S} D={D}")
+    scale = float(z["scale"][0])
+    q, k, v, g = (dev(z[n], torch.float32) for n in ("q", "k", "v", "dout"))
+    out, lse = A.attention_forward(q, k, v, scale)
+    dq, dk, dv, delta = A.attention_backward(g, out, lse, q, k, v, scale)
+    torch.cuda.synchronize()
+    _, lse_ref = oracle.attn_fwd(z["q"], z["k"], z["v"], scale)
+    assert max_abs(host(out), z["o"]) <= TOL_F32
+    assert max_abs(host(lse), lse_ref) <= TOL_F32
+    for got, key in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+        assert max_abs(host(got), z[key]) <= TOL_F32, key
+    assert max_abs(host(delta), oracle.attn_delta(z["dout"], host(out))) <= TOL_F32
+
+
+def test_fp32_reference_named_symbols(gpu):
+    """The C++-linkage wrappers with the reference's names run the same kernels."""
+    case("fp32 via gpu_flash_attention_forward/backward symbols")
+    BH, S, D = 3, 100, 64
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=41, with_dout=True)
+    q, k, v, g = (dev(x, torch.float32) for x in (qn, kn, vn, gn))
+    scale = scale_of(D)
+    out = torch.empty_like(q)
+    lse = torch.empty(BH, S, device="cuda")
+    L = A.lib()
+    fwd = getattr(L, "_Z27gpu_flash_attention_forwardPfS_PKfS1_S1_iiif")
+    fwd.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 3 + [ctypes.c_float]
+    fwd.restype = None
+    torch.cuda.synchronize()
+    fwd(out.data_ptr(), lse.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), BH, S, D,
+        scale)
+    bwd = getattr(L, "_Z28gpu_flash_attention_backwardPfS_S_S_PKfS1_S1_S1_S1_S1_iiif")
+    bwd.argtypes = [ctypes.c_void_p] * 10 + [ctypes.c_int] * 3 + [ctypes.c_float]
+    bwd.restype = None
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    delta = torch.empty(BH, S, device="cuda")
+    bwd(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), g.data_ptr(),
+        out.data_ptr(), lse.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), BH, S, D,
+        scale)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oracle.attn_fwd(qn, kn, vn, scale)
+    dq_r, dk_r, dv_r, _ = oracle.attn_bwd(gn, qn, kn, vn, scale)
+    assert max_abs(host(out), o_ref) <= TOL_F32
+    assert max_abs(host(lse), l_ref) <= TOL_F32
+    for a, b in ((dq, dq_r), (dk, dk_r), (dv, dv_r)):
+        assert max_abs(host(a), b) <= TOL_F32
+
+
+@pytest.mark.parametrize("BH,S,D", [(2, 1024, 64), (4, 257, 32), (1, 1, 64)])
+def test_fp32_against_oracle(gpu, BH, S, D):
+    case(f"fp32 oracle BH={BH} S={S} D={D}")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=50 + S, with_dout=True)
+    scale = scale_of(D)
+    q, k, v, g = (dev(x, torch.float32) for x in (qn, kn, vn, gn))
+    out, lse = A.attention_forward(q, k, v, scale)
+    dq, dk, dv, _ = A.attention_backward(g, out, lse, q, k, v, scale)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oracle.attn_fwd(qn, kn, vn, scale, threads=8)
+    assert max_abs(host(out), o_ref) <= TOL_F32
+    assert max_abs(host(lse), l_ref) <= TOL_F32
+    ref = oracle.attn_bwd(gn, qn, kn, vn, scale, threads=8)[:3]
+    for a, b in zip((dq, dk, dv), ref):
+        assert max_abs(host(a), b) <= TOL_F32
+
+
+# ----------------------------------------------------------------------------- bf16 path
+
+SMALL_BF16 = [(1, 1, 64), (2, 70, 64), (3, 129, 64), (1, 64, 64), (2, 300, 32), (1, 65, 32),
+              (4, 256, 64), (1, 1000, 64)]
+
+
+@pytest.mark.parametrize("BH,S,D", SMALL_BF16)
+def test_bf16_forward_backward_small(gpu, BH, S, D):
+    case(f"bf16 small BH={BH} S={S} D={D}")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=70 + S + D, with_dout=True, bf16=True)
+    scale = scale_of(D)
+    q, k, v, g = (dev(x, torch.bfloat16) for x in (qn, kn, vn, gn))
+    out, lse = A.attention_forward(q, k, v, scale)
+    dq, dk, dv, _ = A.attention_backward(g, out, lse, q, k, v, scale)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oracle.attn_fwd(qn, kn, vn, scale, threads=8)
+    assert max_abs(host(out), o_ref) <= TOL_O
+    assert max_abs(host(lse), l_ref) <= TOL_LSE
+    ref = oracle.attn_bwd(gn, qn, kn, vn, scale, threads=8)[:3]
+    for a, b, nm in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+        assert max_abs(host(a), b) <= TOL_GRAD, nm
+
+
+def test_bf16_forward_cfg2_full(gpu):
+    """B8 H12 T1024 D64 bf16 forward."""
+    BH, S, D = 96, 1024, 64
+    case("bf16 cfg2 forward B8 H12 T1024 D64")
+    qn, kn, vn = synth.attn_inputs(BH, S, D, seed=synth.BASE_SEED + 2, bf16=True)
+    scale = 0.125
+    q, k, v = (dev(x, torch.bfloat16) for x in (qn, kn, vn))
+    out, lse = A.attention_forward(q, k, v, scale)
+    out2, lse2 = A.attention_forward(q, k, v, scale)
+    torch.cuda.synchronize()
+    o, l = host(out), host(lse)
+    assert np.isfinite(o).all() and np.isfinite(l).all()
+    assert torch.equal(out, out2) and torch.equal(lse, lse2), "forward not repeatable"
+    assert np.array_equal(o[:, 0], vn[:, 0]), "row 0 must equal V row 0"
+    sl = [0, 37, 95]
+    o_ref, l_ref = oracle.attn_fwd(qn[sl], kn[sl], vn[sl], scale, threads=8)
+    assert max_abs(o[sl], o_ref) <= TOL_O
+    assert max_abs(l[sl], l_ref) <= TOL_LSE
+
+
+def test_bf16_forward_backward_cfg3_full(gpu):
+    """B16 H12 T1024 D64 bf16 forward + backward from the saved lse."""
+    BH, S, D = 192, 1024, 64
+    case("bf16 cfg3 fwd+bwd B16 H12 T1024 D64")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=synth.BASE_SEED + 3, with_dout=True,
+                                       bf16=True)
+    scale = 0.125
+    q, k, v, g = (dev(x, torch.bfloat16) for x in (qn, kn, vn, gn))
+    out, lse = A.attention_forward(q, k, v, scale)
+    dq, dk, dv, _ = A.attention_backward(g, out, lse, q, k, v, scale)
+    dq2, dk2, dv2, _ = A.attention_backward(g, out, lse, q, k, v, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(dq, dq2) and torch.equal(dk, dk2) and torch.equal(dv, dv2), \
+        "backward not bitwise repeatable"
+    hq, hk, hv = host(dq), host(dk), host(dv)
+    for a in (hq, hk, hv):
+        assert np.isfinite(a).all()
+    sl = [0, 191]
+    ref = oracle.attn_bwd(gn[sl], qn[sl], kn[sl], vn[sl], scale, threads=8)[:3]
+    for a, b, nm in zip((hq[sl], hk[sl], hv[sl]), ref, ("dq", "dk", "dv")):
+        assert max_abs(a, b) <= TOL_GRAD, nm
+    # Column sums on every slice: sum_j dK_j = 0 and sum_j dV_j = sum_i dO_i, up to the bf16
+    # rounding of S outputs (bound: 6 sigma of S independent errors of 2^-9 relative).
+    for got, want, nm in ((hk, np.zeros_like(gn[:, 0]), "dK"), (hv, gn, "dV")):
+        want_sum = want.sum(1) if nm == "dV" else want
+        err = np.abs(got.astype(np.float64).sum(1) - want_sum)
+        rms = np.sqrt((got.astype(np.float64) ** 2).mean(1, keepdims=True))
+        bound = 6 * 2.0 ** -9 * rms * math.sqrt(S) + 1e-3
+        assert (err <= bound).all(), f"{nm} column sum off by {float(err.max()):.3e}"
+
+
+def test_bf16_causal_prefix(gpu):
+    """Changing K/V rows after a cut leaves O, lse and dQ of earlier rows bitwise equal."""
+    BH, S, D, cut = 4, 333, 64, 150
+    case("bf16 causal prefix")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=88, with_dout=True, bf16=True)
+    k2, v2 = kn.copy(), vn.copy()
+    k2[:, cut + 1:] = synth.bf16_round(synth.normal(k2[:, cut + 1:].shape, 5))
+    v2[:, cut + 1:] = synth.bf16_round(synth.normal(v2[:, cut + 1:].shape, 6))
+    scale = 0.125
+    q, g = dev(qn, torch.bfloat16), dev(gn, torch.bfloat16)
+    o1, l1 = A.attention_forward(q, dev(kn, torch.bfloat16), dev(vn, torch.bfloat16), scale)
+    o2, l2 = A.attention_forward(q, dev(k2, torch.bfloat16), dev(v2, torch.bfloat16), scale)
+    torch.cuda.synchronize()
+    assert torch.equal(o1[:, :cut + 1], o2[:, :cut + 1])
+    assert torch.equal(l1[:, :cut + 1], l2[:, :cut + 1])
+    assert not torch.equal(o1[:, cut + 1:], o2[:, cut + 1:])
+
+
+def test_bf16_errors_raise(gpu):
+    case("bf16 error paths")
+    q = torch.zeros(2, 16, 48, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(A.AttentionError, match="unsupported d_head 48"):
+        A.attention_forward(q, q, q)
+    q64 = torch.zeros(2, 16, 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(TypeError):
+        A.flash_attention_forward_bf16(torch.empty_like(q64).float(),
+                                       torch.empty(2, 16, device="cuda"), q64, q64, q64, 2, 16,
+                                       64, 0.125)
+    with pytest.raises(ValueError):
+        A.flash_attention_forward_bf16(torch.empty_like(q64), torch.empty(2, 8, device="cuda"),
+                                       q64, q64, q64, 2, 16, 64, 0.125)
+
+
+# ----------------------------------------------------------------------------- decode
+
+def run_decode(qn, kc, vc, lens, scale, dtype, ws=None):
+    n, H, L, D = kc.shape
+    q = dev(qn, dtype)
+    k_cache, v_cache = dev(kc, dtype), dev(vc, dtype)
+    lens_d = torch.from_numpy(np.asarray(lens, np.int32)).cuda()
+    out = torch.empty(n, H, D, dtype=dtype, device="cuda")
+    ws = A.decode_workspace(n, H, L, D) if ws is None else ws
+    A.decode_attention(out, q, k_cache, v_cache, lens_d, n, H, L, D, scale, ws)
+    return out, ws
+
+
+def test_decode_cfg4_full(gpu):
+    """32 ragged sequences, H12, D64, bf16 cache, lens ~ U[1,1024]."""
+    n, H, L, D = 32, 12, 1024, 64
+    case("decode cfg4 bf16 32x12x1024x64")
+    qn, kc, vc, lens = synth.decode_inputs(n, H, L, D, seed=synth.BASE_SEED + 4)
+    scale = 0.125
+    out, ws = run_decode(qn, kc, vc, lens, scale, torch.bfloat16)
+    out2, _ = run_decode(qn, kc, vc, lens, scale, torch.bfloat16, ws=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), "decode not repeatable (or counters not reset)"
+    ref = oracle.decode(qn, kc, vc, lens, scale)
+    assert max_abs(host(out), ref) <= TOL_DEC
+    assert int(ws[-4 * n * H:].view(torch.int32).abs().sum()) == 0, "counters left nonzero"
+
+
+def test_decode_fp32_against_oracle(gpu):
+    n, H, L, D = 5, 3, 700, 64
+    case("decode fp32")
+    qn, kc, vc, lens = synth.decode_inputs(n, H, L, D, seed=101, bf16=False)
+    lens[0], lens[1] = 1, L
+    out, _ = run_decode(qn, kc, vc, lens, 0.125, torch.float32)
+    torch.cuda.synchronize()
+    assert max_abs(host(out), oracle.decode(qn, kc, vc, lens, 0.125)) <= TOL_F32
+
+
+@pytest.mark.parametrize("D", [32, 64])
+def test_decode_edge_lengths(gpu, D):
+    n, H, L = 8, 2, 600
+    case(f"decode edge lengths D={D}")
+    qn, kc, vc, _ = synth.decode_inputs(n, H, L, D, seed=102 + D)
+    lens = np.array([1, 2, 63, 64, 255, 256, 257, 600], np.int32)
+    out, ws = run_decode(qn, kc, vc, lens, 0.2, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert max_abs(host(out), oracle.decode(qn, kc, vc, lens, 0.2)) <= TOL_DEC
+    assert np.array_equal(host(out)[0], vc[0, :, 0]), "length 1 must return V row 0"
+    # same workspace, different lengths (counters must have been reset by the last call)
+    lens2 = np.array([600, 1, 300, 512, 513, 7, 64, 65], np.int32)
+    out2, _ = run_decode(qn, kc, vc, lens2, 0.2, torch.bfloat16, ws=ws)
+    torch.cuda.synchronize()
+    assert max_abs(host(out2), oracle.decode(qn, kc, vc, lens2, 0.2)) <= TOL_DEC
+
+
+def test_decode_length_clamping(gpu):
+    n, H, L, D = 3, 2, 100, 64
+    case("decode length clamping")
+    qn, kc, vc, _ = synth.decode_inputs(n, H, L, D, seed=103)
+    out, _ = run_decode(qn, kc, vc, np.array([0, 100, 1000], np.int32), 0.125, torch.bfloat16)
+    torch.cuda.synchronize()
+    o = host(out)
+    assert np.all(o[0] == 0.0), "length 0 gives a zero row"
+    ref = oracle.decode(qn[1:], kc[1:], vc[1:], np.array([100, 100], np.int32), 0.125)
+    assert max_abs(o[1:], ref) <= TOL_DEC, "lengths beyond max_len clamp to max_len"
+
+
+def test_decode_matches_forward_rows(gpu):
+    """Decoding query t over cache rows 0..t equals row t of the causal forward (GPU vs GPU,
+    both bf16)."""
+    BH, S, D = 12, 400, 64
+    case("decode vs forward rows")
+    qn, kn, vn = synth.attn_inputs(BH, S, D, seed=104, bf16=True)
+    q, k, v = (dev(x, torch.bfloat16) for x in (qn, kn, vn))
+    out, _ = A.attention_forward(q, k, v, 0.125)
+    ts = [0, 1, 63, 64, 255, 256, 399]
+    qd = np.stack([qn[:, t] for t in ts])  # [len(ts), H=BH, D]
+    kc = np.broadcast_to(kn[None], (len(ts), BH, S, D)).copy()
+    vc = np.broadcast_to(vn[None], (len(ts), BH, S, D)).copy()
+    dec, _ = run_decode(qd, kc, vc, np.array([t + 1 for t in ts], np.int32), 0.125,
+                        torch.bfloat16)
+    torch.cuda.synchronize()
+    o = host(out)
+    for i, t in enumerate(ts):
+        assert max_abs(host(dec)[i], o[:, t]) <= TOL_DEC, f"row {t}"
