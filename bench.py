@@ -12,13 +12,15 @@ the 256 MB MALL cannot hold them), the roofline of the dominant kernel, and the 
 CPU path timed on a bounded sample on this host.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+    python bench.py --profile-sample     # each kernel --reps times + a copy of known size,
+                                         # for rocprofv3 --pmc runs; prints no bench line
 """
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
+import re
 import sys
 import time
 
@@ -39,6 +41,11 @@ BWD_FLOPS = 5 * UNIT                     # 64.425 GFLOP
 KERNEL_FLOPS = {"fwd": FWD_FLOPS, "bwd_dq": UNIT, "bwd_dkdv": 4 * UNIT}
 
 DEC_N, DEC_H, DEC_L, DEC_D = 32, 12, 1024, 64
+COPY_BYTES = 256 << 20                   # calibration copy for the --pmc traffic factor
+
+# HBM bytes per launch from the rocprofv3 --pmc runs (FETCH_SIZE + WRITE_SIZE, each scaled by
+# the factor a plain copy of known size reads): lines "traffic <kernel> <bytes>".
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic_cfg3_cfg4.txt")
 
 
 def parse():
@@ -49,12 +56,14 @@ def parse():
     p.add_argument("--reps", type=int, default=20, help="launches per kernel timing")
     p.add_argument("--decode-copies", type=int, default=8)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-slices", type=int, default=12)
+    p.add_argument("--cpu-slices", type=int, default=24)
+    p.add_argument("--profile-sample", action="store_true")
     return p.parse_args()
 
 
 def event_time_ms(fn, reps, stream):
-    """Average ms per call of fn() over `reps` back-to-back calls, HIP events on `stream`."""
+    """Average ms per call of fn() over `reps` back-to-back calls, HIP events on `stream`
+    (the stream every kernel here is launched on)."""
     import torch
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -66,22 +75,23 @@ def event_time_ms(fn, reps, stream):
     return start.elapsed_time(end) / reps
 
 
-def load_traffic(kernel):
-    """HBM bytes per launch measured with rocprofv3 --pmc (committed summary), or None."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{kernel}.json")
-    if not os.path.exists(path):
-        return None
+def load_traffic():
+    """{kernel: HBM bytes per launch} from the committed --pmc summary (empty if absent)."""
+    out = {}
     try:
-        with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
-    except (OSError, ValueError):
-        return None
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                m = re.match(r"^traffic\s+(\w+)\s+(\d+)\s*$", line)
+                if m:
+                    out[m.group(1)] = int(m.group(2))
+    except OSError:
+        pass
+    return out
 
 
 def cpu_baseline(n_slices):
     """The reference's CPU path (oracle/_ref: its own tensor_ops.cpp/backward.cpp) or, when
     that is not built, the C restatement, on n_slices of the B16 H12 T1024 D64 problem."""
-    import numpy as np
     import oracle
     from dadgpt_amd import synth
 
@@ -98,15 +108,98 @@ def cpu_baseline(n_slices):
     dt = time.perf_counter() - t0
     flops = (FWD_FLOPS + BWD_FLOPS) * n_slices / BH
     return {
-        "value": flops / dt / 1e12,
+        "value": float(f"{flops / dt / 1e12:.6g}"),
         "unit": "TFLOP/s",
         "cores": 1,
         "kind": kind,
         "sample": (f"fp32 forward+backward of {n_slices} of {BH} (b,h) slices of B16 H12 T1024 "
-                   f"D64 (bf16-rounded inputs), single thread, {dt:.2f} s; the backward "
-                   f"recomputes P as the reference's materialized path stores it"),
-        "seconds": dt,
+                   f"D64 (bf16-rounded inputs), single thread, {dt:.2f} s; algorithmic FLOPs "
+                   f"of those slices / wall time"),
+        "seconds": round(dt, 3),
     }
+
+
+class Workload:
+    """Device buffers of config 3 (fwd+bwd) and config 4 (decode, rotating cache copies)."""
+
+    def __init__(self, decode_copies):
+        import numpy as np
+        import torch
+        from dadgpt_amd import attention as A
+        from dadgpt_amd import synth
+
+        self.A = A
+        dev = torch.device("cuda:0")
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(0xDAD6B7)
+
+        def randn(*shape):
+            return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32).to(
+                torch.bfloat16)
+
+        self.q, self.k, self.v, self.g = (randn(BH, T, D) for _ in range(4))
+        self.out = torch.empty_like(self.q)
+        self.lse = torch.empty(BH, T, device=dev)
+        self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
+        self.delta = torch.empty(BH, T, device=dev)
+
+        lens_h = synth.uniform_int(1, DEC_L, DEC_N, synth.BASE_SEED ^ synth.TENSOR_ID["lens"])
+        self.lens = torch.from_numpy(lens_h.astype(np.int32)).to(dev)
+        # K and V rows actually read, plus q and out
+        self.dec_bytes = int(2 * lens_h.sum() * DEC_H * DEC_D * 2 + 2 * DEC_N * DEC_H * DEC_D * 2)
+        self.ncopy = decode_copies
+        self.kcs = [randn(DEC_N, DEC_H, DEC_L, DEC_D) for _ in range(decode_copies)]
+        self.vcs = [randn(DEC_N, DEC_H, DEC_L, DEC_D) for _ in range(decode_copies)]
+        self.qd = randn(DEC_N, DEC_H, DEC_D)
+        self.od = torch.empty_like(self.qd)
+        self.ws = A.decode_workspace(DEC_N, DEC_H, DEC_L, DEC_D)
+
+    def fwd(self):
+        self.A.flash_attention_forward_bf16(self.out, self.lse, self.q, self.k, self.v, BH, T, D,
+                                            SCALE, None)
+
+    def bwd(self):
+        self.A.flash_attention_backward_bf16(self.dq, self.dk, self.dv, self.delta, self.g,
+                                             self.out, self.lse, self.q, self.k, self.v, BH, T,
+                                             D, SCALE, None)
+
+    def phase(self, p):
+        def run():
+            self.A.flash_attention_backward_bf16_phase(p, self.dq, self.dk, self.dv, self.delta,
+                                                       self.g, self.out, self.lse, self.q,
+                                                       self.k, self.v, BH, T, D, SCALE, None)
+        return run
+
+    def step(self):
+        self.fwd()
+        self.bwd()
+
+    def decode(self, i):
+        self.A.decode_attention(self.od, self.qd, self.kcs[i % self.ncopy],
+                                self.vcs[i % self.ncopy], self.lens, DEC_N, DEC_H, DEC_L, DEC_D,
+                                SCALE, self.ws, None)
+
+
+def profile_sample(wl, reps):
+    """Each kernel `reps` times, then a device copy of COPY_BYTES (the calibration kernel
+    for FETCH_SIZE / WRITE_SIZE), for rocprofv3 runs."""
+    import torch
+    for _ in range(reps):
+        wl.fwd()
+    for p in (0, 1, 2):
+        run = wl.phase(p)
+        for _ in range(reps):
+            run()
+    for i in range(reps):
+        wl.decode(i)
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[profile-sample] {reps} launches each of fwd, bwd phases 0-2, decode, and a "
+          f"{COPY_BYTES} B copy", flush=True)
 
 
 def main():
@@ -114,54 +207,29 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 "
-                                   "(every (b,h) slice is independent, see the sharding "
-                                   "design)", "n_gpus": args.gpus}), flush=True)
+                                   "(every (b,h) slice is independent, so the path shards "
+                                   "over (b,h) with no exchange)", "n_gpus": args.gpus}),
+              flush=True)
         sys.exit(2)
 
     import torch
-    from dadgpt_amd import attention as A
 
-    A.lib()
-    dev = torch.device("cuda:0")
+    wl = Workload(args.decode_copies)
+    wl.A.lib()
+    if args.profile_sample:
+        profile_sample(wl, args.reps)
+        return
     stream = torch.cuda.current_stream()
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(0xDAD6B7)
-
-    def randn(*shape):
-        return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32).to(
-            torch.bfloat16)
-
-    q, k, v, g = (randn(BH, T, D) for _ in range(4))
-    out = torch.empty_like(q)
-    lse = torch.empty(BH, T, device=dev)
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
-    delta = torch.empty(BH, T, device=dev)
-
-    def fwd():
-        A.flash_attention_forward_bf16(out, lse, q, k, v, BH, T, D, SCALE, None)
-
-    def bwd():
-        A.flash_attention_backward_bf16(dq, dk, dv, delta, g, out, lse, q, k, v, BH, T, D,
-                                        SCALE, None)
-
-    def phase(p):
-        return lambda: A.flash_attention_backward_bf16_phase(p, dq, dk, dv, delta, g, out, lse,
-                                                             q, k, v, BH, T, D, SCALE, None)
-
-    def step():
-        fwd()
-        bwd()
 
     for _ in range(args.warmup):
-        step()
+        wl.step()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     wall0 = time.perf_counter()
     start.record(stream)
     for _ in range(args.steps):
-        step()
+        wl.step()
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
@@ -171,50 +239,35 @@ def main():
 
     # per-kernel averages (same stream, back-to-back launches)
     kern_ms = {
-        "fwd": event_time_ms(fwd, args.reps, stream),
-        "bwd_delta": event_time_ms(phase(0), args.reps, stream),
-        "bwd_dq": event_time_ms(phase(1), args.reps, stream),
-        "bwd_dkdv": event_time_ms(phase(2), args.reps, stream),
+        "fwd": event_time_ms(wl.fwd, args.reps, stream),
+        "bwd_delta": event_time_ms(wl.phase(0), args.reps, stream),
+        "bwd_dq": event_time_ms(wl.phase(1), args.reps, stream),
+        "bwd_dkdv": event_time_ms(wl.phase(2), args.reps, stream),
     }
-    bwd_ms = event_time_ms(bwd, args.reps, stream)
+    bwd_ms = event_time_ms(wl.bwd, args.reps, stream)
     print(f"[bench] kernels {json.dumps({k: round(x, 4) for k, x in kern_ms.items()})}",
           file=sys.stderr, flush=True)
 
-    # ---- decode (config 4), rotating cache copies, launches captured in a graph ----
-    import numpy as np
-    from dadgpt_amd import synth
-    lens_h = synth.uniform_int(1, DEC_L, DEC_N, synth.BASE_SEED ^ synth.TENSOR_ID["lens"])
-    lens = torch.from_numpy(lens_h.astype(np.int32)).to(dev)
-    dec_bytes = int(2 * lens_h.sum() * DEC_H * DEC_D * 2 + 2 * DEC_N * DEC_H * DEC_D * 2)
-    ncopy = args.decode_copies
-    kcs = [randn(DEC_N, DEC_H, DEC_L, DEC_D) for _ in range(ncopy)]
-    vcs = [randn(DEC_N, DEC_H, DEC_L, DEC_D) for _ in range(ncopy)]
-    qd = randn(DEC_N, DEC_H, DEC_D)
-    od = torch.empty_like(qd)
-    ws = A.decode_workspace(DEC_N, DEC_H, DEC_L, DEC_D)
-
-    def decode(i):
-        A.decode_attention(od, qd, kcs[i % ncopy], vcs[i % ncopy], lens, DEC_N, DEC_H, DEC_L,
-                           DEC_D, SCALE, ws, None)
-
-    for i in range(ncopy):
-        decode(i)
+    # ---- decode (config 4): rotating cache copies, launches captured in a graph ----
+    for i in range(wl.ncopy):
+        wl.decode(i)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    per_graph = 4 * ncopy
+    per_graph = 4 * wl.ncopy
     with torch.cuda.graph(graph):
         for i in range(per_graph):
-            decode(i)
+            wl.decode(i)
     graph.replay()
     torch.cuda.synchronize()
-    gstream = torch.cuda.current_stream()
-    dec_ms = event_time_ms(graph.replay, 5, gstream) / per_graph
-    dec_gbps = dec_bytes / (dec_ms * 1e-3) / 1e9
-    # eager launches of one copy: the cache stays MALL-resident, launch gaps included
-    eager_dec_ms = event_time_ms(lambda: decode(0), args.reps, stream)
+    dec_ms = event_time_ms(graph.replay, 5, torch.cuda.current_stream()) / per_graph
+    dec_gbps = wl.dec_bytes / (dec_ms * 1e-3) / 1e9
+    # eager launches over the rotating copies (launch gaps included)
+    eager_dec_ms = event_time_ms(lambda it=iter(range(10 ** 9)): wl.decode(next(it)),
+                                 args.reps, stream)
     print(f"[bench] decode {dec_ms * 1e3:.2f} us/launch in graph ({dec_gbps:.0f} GB/s), eager "
-          f"same-copy {eager_dec_ms * 1e3:.2f} us", file=sys.stderr, flush=True)
+          f"{eager_dec_ms * 1e3:.2f} us", file=sys.stderr, flush=True)
 
+    traffic = load_traffic()
     comps = {}
     for name, ms in kern_ms.items():
         c = {"ms": round(ms, 5)}
@@ -222,24 +275,26 @@ def main():
             tf = KERNEL_FLOPS[name] / (ms * 1e-3) / 1e12
             c.update({"algorithmic_gflop": round(KERNEL_FLOPS[name] / 1e9, 3),
                       "tflops": round(tf, 2), "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)})
+        if name in traffic:
+            c["hbm_bytes_per_launch"] = traffic[name]
         comps[name] = c
-    comps["fwd_total"] = {"ms": round(kern_ms["fwd"], 5),
-                          "tflops": round(FWD_FLOPS / (kern_ms["fwd"] * 1e-3) / 1e12, 2)}
-    comps["bwd_total"] = {"ms": round(bwd_ms, 5),
-                          "tflops": round(BWD_FLOPS / (bwd_ms * 1e-3) / 1e12, 2)}
-    comps["bwd_total"]["frac_mfma_peak"] = round(comps["bwd_total"]["tflops"] / PEAK_BF16_TFLOPS, 4)
-    comps["fwd_total"]["frac_mfma_peak"] = round(comps["fwd_total"]["tflops"] / PEAK_BF16_TFLOPS, 4)
-    comps["decode"] = {"us_per_launch": round(dec_ms * 1e3, 3), "bytes": dec_bytes,
-                       "gbps": round(dec_gbps, 1), "frac_hbm_peak": round(dec_gbps / PEAK_HBM_GBPS, 4),
-                       "eager_same_copy_us_per_launch": round(eager_dec_ms * 1e3, 3),
-                       "cache_copies": ncopy,
+    for name, ms, fl in (("fwd_total", kern_ms["fwd"], FWD_FLOPS), ("bwd_total", bwd_ms,
+                                                                     BWD_FLOPS)):
+        tf = fl / (ms * 1e-3) / 1e12
+        comps[name] = {"ms": round(ms, 5), "tflops": round(tf, 2),
+                       "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+    comps["decode"] = {"us_per_launch": round(dec_ms * 1e3, 3), "bytes": wl.dec_bytes,
+                       "gbps": round(dec_gbps, 1),
+                       "frac_hbm_peak": round(dec_gbps / PEAK_HBM_GBPS, 4),
+                       "eager_us_per_launch": round(eager_dec_ms * 1e3, 3),
+                       "cache_copies": wl.ncopy, "hbm_bytes_per_launch": traffic.get("decode"),
                        "config": "32 seqs, H12, D64, bf16 cache [32,12,1024,64], lens U[1,1024]"}
 
     dom = max(("fwd", "bwd_dq", "bwd_dkdv"), key=lambda n: kern_ms[n])
     ach = KERNEL_FLOPS[dom] / (kern_ms[dom] * 1e-3) / 1e12
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": load_traffic(dom)}
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic.get(dom)}
 
     value = (FWD_FLOPS + BWD_FLOPS) / (ms_step * 1e-3) / 1e12
     line = {
@@ -264,10 +319,9 @@ def main():
         "decode_gbps": round(dec_gbps, 1),
     }
     if not args.no_cpu_baseline:
-        print(f"[bench] cpu baseline on {args.cpu_slices} slices ...", file=sys.stderr, flush=True)
+        print(f"[bench] cpu baseline on {args.cpu_slices} slices ...", file=sys.stderr,
+              flush=True)
         line["cpu_baseline"] = cpu_baseline(args.cpu_slices)
-        line["cpu_baseline"]["seconds"] = round(line["cpu_baseline"]["seconds"], 3)
-        line["cpu_baseline"]["value"] = float(f"{line['cpu_baseline']['value']:.6g}")
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

@@ -205,9 +205,12 @@ def decode_workspace_bytes(n_seq: int, n_heads: int, max_len: int, d_head: int) 
 
 
 def decode_workspace(n_seq, n_heads, max_len, d_head, device="cuda"):
-    """A zero-filled workspace for decode_attention (its counters must start at zero)."""
+    """The workspace decode_attention needs for this cache shape, or None when it needs
+    none (max_len fits one workgroup span)."""
     nbytes = decode_workspace_bytes(n_seq, n_heads, max_len, d_head)
-    return torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
 def decode_attention(out, q, k_cache, v_cache, lens, n_seq, n_heads, max_len, d_head, scale,

@@ -80,7 +80,7 @@ int check_decode(const char* fn, int n_seq, int H, int max_len, int d_head, floa
   if (!std::isfinite(scale))
     return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: scale must be finite", fn);
   const size_t need = dadgpt::decode_workspace_bytes(n_seq, H, max_len, d_head);
-  if (ws == nullptr || ws_bytes < need)
+  if (need > 0 && (ws == nullptr || ws_bytes < need))
     return fail(DADGPT_ERR_WORKSPACE, "%s: workspace of %zu bytes given, %zu needed", fn,
                 ws == nullptr ? 0 : ws_bytes, need);
   return DADGPT_OK;

@@ -32,9 +32,9 @@ hipError_t launch_bwd_f32(float* dq, float* dk, float* dv, float* delta, const f
                           const float* v, int BH, int S, int D, float scale,
                           hipStream_t stream);
 
-// Split-K decode over ragged KV caches [n_seq,H,max_len,D]. The workspace holds fp32
-// per-split partials followed by one uint32 arrival counter per (sequence, head); the
-// counters must be zero before the first call and are left zero by every call.
+// Decode over ragged KV caches [n_seq,H,max_len,D]. A cache longer than one workgroup span
+// (1024 keys bf16, 512 fp32) is split into spans whose fp32 partials go to the workspace and
+// are merged by a second kernel; decode_workspace_bytes is 0 when no split is needed.
 size_t decode_workspace_bytes(int n_seq, int H, int max_len, int D);
 hipError_t launch_decode_bf16(bf16* out, const bf16* q, const bf16* k_cache,
                               const bf16* v_cache, const int* lens, int n_seq, int H,

@@ -103,9 +103,11 @@ int dadgpt_flash_attention_backward_bf16_phase(int phase, uint16_t* dq, uint16_t
                                                const uint16_t* k, const uint16_t* v, int BH,
                                                int S, int d_head, float scale, void* stream);
 
-/* Bytes of decode workspace for a cache shape. The workspace must be zero-filled once when
- * allocated (it holds arrival counters that every call leaves at zero); calls that share a
- * workspace must not overlap in time. */
+/* Bytes of decode workspace for a cache shape, valid for both element types. It is 0 when
+ * max_len fits one workgroup span (512 keys fp32, 1024 keys bf16): then no workspace is
+ * needed and NULL may be passed. Longer caches are split into spans whose fp32 partials go to
+ * the workspace and are merged by a second kernel. The workspace needs no initialisation;
+ * calls that share a workspace must not overlap in time. */
 size_t dadgpt_decode_workspace_bytes(int n_seq, int n_heads, int max_len, int d_head);
 
 /* KV-cache decode attention (replaces the per-head composition in src/model.cpp:758-790:

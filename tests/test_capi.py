@@ -92,10 +92,14 @@ def test_backward_phase_validation():
 
 
 def expected_ws(n, h, max_len, d):
-    return 4 * n * h * ((max_len + 255) // 256) * (d + 2) + 4 * n * h
+    """fp32 partials (max, sum, o[d]) per 512-key span when the cache needs more than one
+    span (fp32 spans are 512 keys, bf16 spans 1024: the fp32 count serves both)."""
+    spans = (max_len + 511) // 512
+    return 0 if spans == 1 else 4 * n * h * spans * (d + 2)
 
 
-@pytest.mark.parametrize("n,h,L,d", [(32, 12, 1024, 64), (1, 1, 1, 32), (3, 5, 257, 64)])
+@pytest.mark.parametrize("n,h,L,d", [(32, 12, 1024, 64), (1, 1, 1, 32), (3, 5, 257, 64),
+                                     (2, 3, 512, 64), (2, 3, 513, 32), (4, 12, 4096, 64)])
 def test_decode_workspace_bytes(n, h, L, d):
     assert A.decode_workspace_bytes(n, h, L, d) == expected_ws(n, h, L, d)
 
@@ -108,9 +112,10 @@ def test_decode_workspace_bytes_rejects_bad_shapes():
 @pytest.mark.parametrize("fn", ["dadgpt_decode_attention_bf16", "dadgpt_decode_attention_f32"])
 def test_decode_validation(fn):
     f = getattr(A.lib(), fn)
-    need = expected_ws(4, 2, 64, 64)
+    need = expected_ws(4, 2, 2000, 64)
+    assert need > 0
     args = lambda **kw: [kw.get("out", FAKE), FAKE, FAKE, FAKE, kw.get("lens", FAKE),
-                         kw.get("n", 4), kw.get("h", 2), kw.get("L", 64), kw.get("d", 64),
+                         kw.get("n", 4), kw.get("h", 2), kw.get("L", 2000), kw.get("d", 64),
                          kw.get("scale", 0.125), kw.get("ws", FAKE), kw.get("wsb", need), None]
     assert f(*args(d=48)) == 2
     assert f(*args(out=None)) == 1
