@@ -3,22 +3,27 @@
 // (delta, dK/dV, dQ), restructured for MFMA:
 //
 //   delta kernel   delta[r] = sum_d dO[r,d] * O[r,d]                  (attention.cu:75-85)
-//   dQ kernel      query-major; per 64-key tile:  S^T = K Q^T, dP^T = V dO^T,
-//                  dS = P (dP - delta), dQ^T += K^T dS^T              (attention.cu:154-205)
-//   dK/dV kernel   key-major; per 64-query tile: S = Q K^T, dP = dO V^T,
+//   dK/dV kernel   key-major; per 32-query block:  S = Q K^T, dP = dO V^T,
+//                  P = exp(S*scale - lse), dS = P (dP - delta),
 //                  dV^T += dO^T P, dK^T += Q^T dS                    (attention.cu:87-152)
+//   dQ kernel      query-major; per 32-key chunk:  S^T = K Q^T, dP^T = V dO^T,
+//                  dQ^T += K^T dS^T                                   (attention.cu:154-205)
 //
-// Both kernels own their outputs outright (no atomics, bitwise repeatable). The score
+// Both MFMA kernels own their outputs outright (no atomics, bitwise repeatable). The score
 // tiles use the same sigma32 row permutation as the forward so that P and dS feed the next
-// MFMA as B operands from registers; the operands that must be read along the score
-// dimension (K^T in the dQ kernel, Q^T and dO^T in the dK/dV kernel) come from transposed
-// LDS tiles built during staging.
+// MFMA as B operands from registers; the operands that must be read along the score dimension
+// (Q^T and dO^T in the dK/dV kernel, K^T in the dQ kernel) come from transposed LDS tiles
+// built during staging. Masking is compiled only into the blocks that straddle the diagonal
+// (template DIAG), so the other blocks run branch-free. Registers stay under 256 per lane
+// (launch bound: 2 waves per SIMD) so each SIMD interleaves two waves.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "tiles.hpp"
 
 namespace dadgpt {
 namespace {
+
+constexpr int kWaves = 4;
 
 // ---------------------------------------------------------------- delta
 template <int D>
@@ -48,143 +53,93 @@ __global__ __launch_bounds__(256) void delta_bf16_kernel(float* __restrict__ del
   if (row < rows && part == 0) delta[row] = acc;
 }
 
-// ---------------------------------------------------------------- dQ
-constexpr int kQWb = 32;  // queries per wave in the dQ kernel
-
-template <int D, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void dq_bf16_kernel(
-    bf16* __restrict__ dq, const bf16* __restrict__ q, const bf16* __restrict__ k,
-    const bf16* __restrict__ v, const bf16* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ delta, int S, float scale_log2, float scale) {
-  constexpr int NT = 64 * WAVES;
-  constexpr int QB = kQWb * WAVES;
-  constexpr int DS = D / 16, DB = D / 32;
-  __shared__ __attribute__((aligned(16))) bf16 sk[2][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 skt[2][D * kTileRows];
-  __shared__ __attribute__((aligned(16))) bf16 sv[2][kTileRows * D];
-
-  const int bh = blockIdx.x;
-  const int qblk = gridDim.y - 1 - blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hi = lane >> 5;
-  const size_t base = (size_t)bh * S * D;
-  const bf16* kg = k + base;
-  const bf16* vg = v + base;
-
-  const int q0 = qblk * QB + wave * kQWb;
-  const int qrow = q0 + l32;
-  const int wg_last = min(S, (qblk + 1) * QB) - 1;
-  const int n_tiles = wg_last / kTileRows + 1;
-
-  bf16x8 qop[DS], doop[DS];
+// Stores lanes' f32x16 accumulators C[d][row] (lane = row l32, element r = d row
+// 32*db + c32_row(r, hi)) as bf16 rows of `dst`, times `mul`.
+template <int DB>
+__device__ __forceinline__ void store_rows_bf16(bf16* dst, const f32x16 (&acc)[DB], float mul,
+                                                int hi) {
 #pragma unroll
-  for (int ds = 0; ds < DS; ++ds) {
-    const bool in = qrow < S;
-    qop[ds] = in ? ld_g128(q + base + (size_t)qrow * D + 16 * ds + 8 * hi)
-                 : as_bf16x8(u32x4{0, 0, 0, 0});
-    doop[ds] = in ? ld_g128(dout + base + (size_t)qrow * D + 16 * ds + 8 * hi)
-                  : as_bf16x8(u32x4{0, 0, 0, 0});
-  }
-  const float lse2 = qrow < S ? lse[(size_t)bh * S + qrow] * kLog2e : 0.f;
-  const float dlt = qrow < S ? delta[(size_t)bh * S + qrow] : 0.f;
-
-  f32x16 dqacc[DB];
+  for (int db = 0; db < DB; ++db)
 #pragma unroll
-  for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
-
-  PairTile<D, NT> kt;
-  RowTile<D, NT> vt;
-  kt.load(kg, 0, S, tid);
-  vt.load(vg, 0, S, tid);
-  kt.store_rm(sk[0], tid);
-  kt.store_tr(skt[0], tid);
-  vt.store_rm(sv[0], tid);
-  __syncthreads();
-
-  for (int t = 0; t < n_tiles; ++t) {
-    const int st = t & 1;
-    const int k0 = t * kTileRows;
-    if (t + 1 < n_tiles) {
-      kt.load(kg, k0 + kTileRows, S, tid);
-      vt.load(vg, k0 + kTileRows, S, tid);
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * db + c32_row(4 * g, hi);
+      u32x2 w;
+      w[0] = pack_bf16x2(acc[db][4 * g] * mul, acc[db][4 * g + 1] * mul);
+      w[1] = pack_bf16x2(acc[db][4 * g + 2] * mul, acc[db][4 * g + 3] * mul);
+      st_g64(dst + d0, w);
     }
-    if (q0 < S && k0 <= q0 + kQWb - 1) {
-      f32x16 s[2], dp[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        s[kb] = f32x16{};
-        dp[kb] = f32x16{};
-        const int krow = 32 * kb + sigma32(l32);
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-          s[kb] = mfma32(lds_op(sk[st], rm_off<D>(krow, 2 * ds + hi)), qop[ds], s[kb]);
-          dp[kb] = mfma32(lds_op(sv[st], rm_off<D>(krow, 2 * ds + hi)), doop[ds], dp[kb]);
-        }
-      }
-      const bool diag = k0 + kTileRows - 1 > q0;
-      bf16x8 dsb[4];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float p = fast_exp2(s[kb][r] * scale_log2 - lse2);
-          if (diag) {
-            const int key = k0 + 32 * kb + 16 * (r >> 3) + 8 * hi + (r & 7);
-            if (key > qrow) p = 0.f;
-          }
-          s[kb][r] = p * (dp[kb][r] - dlt);
-        }
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const f32x16& src = s[ks >> 1];
-        const int r0 = (ks & 1) * 8;
-        u32x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(src[r0 + 2 * e], src[r0 + 2 * e + 1]);
-        dsb[ks] = as_bf16x8(w);
-      }
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int col = 32 * db + l32;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          dqacc[db] = mfma32(lds_op(skt[st], tr_off(col, 2 * ks + hi)), dsb[ks], dqacc[db]);
-      }
-    }
-    if (t + 1 < n_tiles) {
-      kt.store_rm(sk[st ^ 1], tid);
-      kt.store_tr(skt[st ^ 1], tid);
-      vt.store_rm(sv[st ^ 1], tid);
-    }
-    __syncthreads();
-  }
-
-  if (qrow < S) {
-    bf16* orow = dq + base + (size_t)qrow * D;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = 32 * db + c32_row(4 * g, hi);
-        u32x2 w;
-        w[0] = pack_bf16x2(dqacc[db][4 * g] * scale, dqacc[db][4 * g + 1] * scale);
-        w[1] = pack_bf16x2(dqacc[db][4 * g + 2] * scale, dqacc[db][4 * g + 3] * scale);
-        st_g64(orow + d0, w);
-      }
-  }
 }
 
 // ---------------------------------------------------------------- dK / dV
-constexpr int kKWb = 32;  // keys per wave in the dK/dV kernel
+constexpr int kKW = 32;  // keys per wave
 
-template <int D, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void dkdv_bf16_kernel(
+// One 32-query block (tile rows 32*qb ..) against the wave's 32 keys. Register 8j+e of lane
+// half hi holds tile query 32qb + 16j + 8hi + e.
+template <int D, bool DIAG>
+__device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dvacc)[D / 32],
+                                           const bf16x8 (&kop)[D / 16],
+                                           const bf16x8 (&vop)[D / 16], const bf16* sq,
+                                           const bf16* sqt, const bf16* sdo, const bf16* sdot,
+                                           const float* slse, const float* sdel, int qb,
+                                           int key_minus_r0, int l32, int hi,
+                                           float scale_log2) {
+  constexpr int DS = D / 16, DB = D / 32;
+  f32x16 s = f32x16{}, dp = f32x16{};
+  const int qr = 32 * qb + sigma32(l32);
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    s = mfma32(lds_op(sq, rm_off<D>(qr, 2 * ds + hi)), kop[ds], s);
+    dp = mfma32(lds_op(sdo, rm_off<D>(qr, 2 * ds + hi)), vop[ds], dp);
+  }
+  bf16x8 pb[2], dsb[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int qt0 = 32 * qb + 16 * j + 8 * hi;
+    const f32x4 la = *reinterpret_cast<const f32x4*>(slse + qt0);
+    const f32x4 lb = *reinterpret_cast<const f32x4*>(slse + qt0 + 4);
+    const f32x4 da = *reinterpret_cast<const f32x4*>(sdel + qt0);
+    const f32x4 dbv = *reinterpret_cast<const f32x4*>(sdel + qt0 + 4);
+    u32x4 wp, wd;
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      float p[2], d[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int e = 2 * e2 + h;
+        const float l2 = e < 4 ? la[e] : lb[e - 4];
+        const float de = e < 4 ? da[e] : dbv[e - 4];
+        float pe = fast_exp2(fmaf(s[8 * j + e], scale_log2, -l2));
+        // key > query: masked (key - r0 > tile query index)
+        if (DIAG) pe = key_minus_r0 > qt0 + e ? 0.f : pe;
+        p[h] = pe;
+        d[h] = pe * (dp[8 * j + e] - de);
+      }
+      wp[e2] = pack_bf16x2(p[0], p[1]);
+      wd[e2] = pack_bf16x2(d[0], d[1]);
+    }
+    pb[j] = as_bf16x8(wp);
+    dsb[j] = as_bf16x8(wd);
+  }
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    const int col = 32 * db + l32;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int chunk = 4 * qb + 2 * j + hi;  // tile queries 32qb + 16j + 8hi ..
+      dvacc[db] = mfma32(lds_op(sdot, tr_off(col, chunk)), pb[j], dvacc[db]);
+      dkacc[db] = mfma32(lds_op(sqt, tr_off(col, chunk)), dsb[j], dkacc[db]);
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kWaves, 2) void dkdv_bf16_kernel(
     bf16* __restrict__ dk, bf16* __restrict__ dv, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, float scale_log2,
     float scale) {
-  constexpr int NT = 64 * WAVES;
-  constexpr int KB = kKWb * WAVES;
+  constexpr int NT = 64 * kWaves;
+  constexpr int KB = kKW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
   __shared__ __attribute__((aligned(16))) bf16 sq[2][kTileRows * D];
   __shared__ __attribute__((aligned(16))) bf16 sqt[2][D * kTileRows];
@@ -203,7 +158,7 @@ __global__ __launch_bounds__(64 * WAVES) void dkdv_bf16_kernel(
   const float* lseg = lse + (size_t)bh * S;
   const float* delg = delta + (size_t)bh * S;
 
-  const int kw0 = kblk * KB + wave * kKWb;
+  const int kw0 = kblk * KB + wave * kKW;
   const int key = kw0 + l32;
   const int t_first = (kblk * KB) / kTileRows;
   const int t_end = (S - 1) / kTileRows + 1;
@@ -257,54 +212,16 @@ __global__ __launch_bounds__(64 * WAVES) void dkdv_bf16_kernel(
     const int r0 = t * kTileRows;
     if (t + 1 < t_end) load_rows(r0 + kTileRows);
     if (kw0 < S && r0 + kTileRows - 1 >= kw0) {
-      const bool diag = r0 < kw0 + kKWb - 1;
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        f32x16 s = f32x16{}, dp = f32x16{};
-        const int qr = 32 * qb + sigma32(l32);
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-          s = mfma32(lds_op(sq[st], rm_off<D>(qr, 2 * ds + hi)), kop[ds], s);
-          dp = mfma32(lds_op(sdo[st], rm_off<D>(qr, 2 * ds + hi)), vop[ds], dp);
-        }
-        bf16x8 pb[2], dsb[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          // Registers 8j..8j+7 of lane half hi hold tile queries 32qb + 16j + 8hi + 0..7.
-          const int qt0 = 32 * qb + 16 * j + 8 * hi;
-          const f32x4 la = *reinterpret_cast<const f32x4*>(&slse[st][qt0]);
-          const f32x4 lb = *reinterpret_cast<const f32x4*>(&slse[st][qt0 + 4]);
-          const f32x4 da = *reinterpret_cast<const f32x4*>(&sdel[st][qt0]);
-          const f32x4 dbv = *reinterpret_cast<const f32x4*>(&sdel[st][qt0 + 4]);
-          float p[8], d[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float l2 = e < 4 ? la[e] : lb[e - 4];
-            const float de = e < 4 ? da[e] : dbv[e - 4];
-            float pe = fast_exp2(s[8 * j + e] * scale_log2 - l2);
-            if (diag && key > r0 + qt0 + e) pe = 0.f;
-            p[e] = pe;
-            d[e] = pe * (dp[8 * j + e] - de);
-          }
-          u32x4 wp, wd;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            wp[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
-            wd[e] = pack_bf16x2(d[2 * e], d[2 * e + 1]);
-          }
-          pb[j] = as_bf16x8(wp);
-          dsb[j] = as_bf16x8(wd);
-        }
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const int col = 32 * db + l32;
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int chunk = 4 * qb + 2 * j + hi;  // tile queries 32qb + 16j + 8hi ..
-            dvacc[db] = mfma32(lds_op(sdot[st], tr_off(col, chunk)), pb[j], dvacc[db]);
-            dkacc[db] = mfma32(lds_op(sqt[st], tr_off(col, chunk)), dsb[j], dkacc[db]);
-          }
-        }
+        const int qlo = r0 + 32 * qb;  // first query of the block
+        if (qlo + 31 < kw0) continue;   // every key of the wave is after every query
+        if (qlo < kw0 + kKW - 1)        // some key after some query: mask
+          dkdv_block<D, true>(dkacc, dvacc, kop, vop, sq[st], sqt[st], sdo[st], sdot[st],
+                              slse[st], sdel[st], qb, key - r0, l32, hi, scale_log2);
+        else
+          dkdv_block<D, false>(dkacc, dvacc, kop, vop, sq[st], sqt[st], sdo[st], sdot[st],
+                               slse[st], sdel[st], qb, key - r0, l32, hi, scale_log2);
       }
     }
     if (t + 1 < t_end) store_rows(st ^ 1);
@@ -312,25 +229,139 @@ __global__ __launch_bounds__(64 * WAVES) void dkdv_bf16_kernel(
   }
 
   if (key < S) {
-    bf16* krow = dk + base + (size_t)key * D;
-    bf16* vrow = dv + base + (size_t)key * D;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = 32 * db + c32_row(4 * g, hi);
-        u32x2 wk, wv;
-        wk[0] = pack_bf16x2(dkacc[db][4 * g] * scale, dkacc[db][4 * g + 1] * scale);
-        wk[1] = pack_bf16x2(dkacc[db][4 * g + 2] * scale, dkacc[db][4 * g + 3] * scale);
-        wv[0] = pack_bf16x2(dvacc[db][4 * g], dvacc[db][4 * g + 1]);
-        wv[1] = pack_bf16x2(dvacc[db][4 * g + 2], dvacc[db][4 * g + 3]);
-        st_g64(krow + d0, wk);
-        st_g64(vrow + d0, wv);
-      }
+    store_rows_bf16<DB>(dk + base + (size_t)key * D, dkacc, scale, hi);
+    store_rows_bf16<DB>(dv + base + (size_t)key * D, dvacc, 1.0f, hi);
   }
 }
 
-template <int D, int WAVES>
+// ---------------------------------------------------------------- dQ
+constexpr int kQW = 32;  // queries per wave
+
+// One 32-key chunk (tile keys 32*kb ..) against the wave's 32 queries. Register 8j+e of lane
+// half hi holds tile key 32kb + 16j + 8hi + e.
+template <int D, bool DIAG>
+__device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (&qop)[D / 16],
+                                         const bf16x8 (&doop)[D / 16], const bf16* sk,
+                                         const bf16* skt, const bf16* sv, int kb,
+                                         int qrow_minus_k0, float lse2, float dlt, int l32,
+                                         int hi, float scale_log2) {
+  constexpr int DS = D / 16, DB = D / 32;
+  f32x16 s = f32x16{}, dp = f32x16{};
+  const int krow = 32 * kb + sigma32(l32);
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    s = mfma32(lds_op(sk, rm_off<D>(krow, 2 * ds + hi)), qop[ds], s);
+    dp = mfma32(lds_op(sv, rm_off<D>(krow, 2 * ds + hi)), doop[ds], dp);
+  }
+  bf16x8 dsb[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    u32x4 w;
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      float d[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int e = 2 * e2 + h;
+        float p = fast_exp2(fmaf(s[8 * j + e], scale_log2, -lse2));
+        if (DIAG) p = 32 * kb + 16 * j + 8 * hi + e > qrow_minus_k0 ? 0.f : p;
+        d[h] = p * (dp[8 * j + e] - dlt);
+      }
+      w[e2] = pack_bf16x2(d[0], d[1]);
+    }
+    dsb[j] = as_bf16x8(w);
+  }
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    const int col = 32 * db + l32;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      dqacc[db] = mfma32(lds_op(skt, tr_off(col, 4 * kb + 2 * j + hi)), dsb[j], dqacc[db]);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kWaves, 2) void dq_bf16_kernel(
+    bf16* __restrict__ dq, const bf16* __restrict__ q, const bf16* __restrict__ k,
+    const bf16* __restrict__ v, const bf16* __restrict__ dout, const float* __restrict__ lse,
+    const float* __restrict__ delta, int S, float scale_log2, float scale) {
+  constexpr int NT = 64 * kWaves;
+  constexpr int QB = kQW * kWaves;
+  constexpr int DS = D / 16, DB = D / 32;
+  __shared__ __attribute__((aligned(16))) bf16 sk[2][kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 skt[2][D * kTileRows];
+  __shared__ __attribute__((aligned(16))) bf16 sv[2][kTileRows * D];
+
+  const int bh = blockIdx.x;
+  const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const size_t base = (size_t)bh * S * D;
+  const bf16* kg = k + base;
+  const bf16* vg = v + base;
+
+  const int q0 = qblk * QB + wave * kQW;
+  const int qrow = q0 + l32;
+  const int wg_last = min(S, (qblk + 1) * QB) - 1;
+  const int n_tiles = wg_last / kTileRows + 1;
+
+  bf16x8 qop[DS], doop[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    const bool in = qrow < S;
+    qop[ds] = in ? ld_g128(q + base + (size_t)qrow * D + 16 * ds + 8 * hi)
+                 : as_bf16x8(u32x4{0, 0, 0, 0});
+    doop[ds] = in ? ld_g128(dout + base + (size_t)qrow * D + 16 * ds + 8 * hi)
+                  : as_bf16x8(u32x4{0, 0, 0, 0});
+  }
+  const float lse2 = qrow < S ? lse[(size_t)bh * S + qrow] * kLog2e : 0.f;
+  const float dlt = qrow < S ? delta[(size_t)bh * S + qrow] : 0.f;
+
+  f32x16 dqacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
+
+  PairTile<D, NT> kt;
+  RowTile<D, NT> vt;
+  kt.load(kg, 0, S, tid);
+  vt.load(vg, 0, S, tid);
+  kt.store_rm(sk[0], tid);
+  kt.store_tr(skt[0], tid);
+  vt.store_rm(sv[0], tid);
+  __syncthreads();
+
+  for (int t = 0; t < n_tiles; ++t) {
+    const int st = t & 1;
+    const int k0 = t * kTileRows;
+    if (t + 1 < n_tiles) {
+      kt.load(kg, k0 + kTileRows, S, tid);
+      vt.load(vg, k0 + kTileRows, S, tid);
+    }
+    if (q0 < S) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int klo = k0 + 32 * kb;        // first key of the chunk
+        if (klo > q0 + kQW - 1) continue;    // every key after every query of the wave
+        if (klo + 31 > q0)                   // some key after some query: mask
+          dq_chunk<D, true>(dqacc, qop, doop, sk[st], skt[st], sv[st], kb, qrow - k0, lse2,
+                            dlt, l32, hi, scale_log2);
+        else
+          dq_chunk<D, false>(dqacc, qop, doop, sk[st], skt[st], sv[st], kb, qrow - k0, lse2,
+                             dlt, l32, hi, scale_log2);
+      }
+    }
+    if (t + 1 < n_tiles) {
+      kt.store_rm(sk[st ^ 1], tid);
+      kt.store_tr(skt[st ^ 1], tid);
+      vt.store_rm(sv[st ^ 1], tid);
+    }
+    __syncthreads();
+  }
+
+  if (qrow < S) store_rows_bf16<DB>(dq + base + (size_t)qrow * D, dqacc, scale, hi);
+}
+
+template <int D>
 hipError_t launch_bwd_bf16_t(bf16* dq, bf16* dk, bf16* dv, float* delta, const bf16* dout,
                              const bf16* out, const float* lse, const bf16* q, const bf16* k,
                              const bf16* v, int BH, int S, float scale, hipStream_t stream,
@@ -343,16 +374,17 @@ hipError_t launch_bwd_bf16_t(bf16* dq, bf16* dk, bf16* dv, float* delta, const b
                                                                                out, rows);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
+  // P = exp2(S * scale * log2(e) - lse * log2(e)) holds for either sign of the scale.
   const float sl2 = scale * kLog2e;
   if (phases & kBwdDq) {
-    constexpr int QB = kQWb * WAVES;
-    dq_bf16_kernel<D, WAVES><<<dim3(BH, (S + QB - 1) / QB), 64 * WAVES, 0, stream>>>(
+    constexpr int QB = kQW * kWaves;
+    dq_bf16_kernel<D><<<dim3(BH, (S + QB - 1) / QB), 64 * kWaves, 0, stream>>>(
         dq, q, k, v, dout, lse, delta, S, sl2, scale);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (phases & kBwdDkdv) {
-    constexpr int KB = kKWb * WAVES;
-    dkdv_bf16_kernel<D, WAVES><<<dim3(BH, (S + KB - 1) / KB), 64 * WAVES, 0, stream>>>(
+    constexpr int KB = kKW * kWaves;
+    dkdv_bf16_kernel<D><<<dim3(BH, (S + KB - 1) / KB), 64 * kWaves, 0, stream>>>(
         dk, dv, q, k, v, dout, lse, delta, S, sl2, scale);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
@@ -366,11 +398,11 @@ hipError_t launch_bwd_bf16(bf16* dq, bf16* dk, bf16* dv, float* delta, const bf1
                            const bf16* v, int BH, int S, int D, float scale,
                            hipStream_t stream, int phases) {
   if (D == 64)
-    return launch_bwd_bf16_t<64, 4>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale,
-                                    stream, phases);
+    return launch_bwd_bf16_t<64>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale,
+                                 stream, phases);
   if (D == 32)
-    return launch_bwd_bf16_t<32, 4>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale,
-                                    stream, phases);
+    return launch_bwd_bf16_t<32>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale,
+                                 stream, phases);
   return hipErrorInvalidValue;
 }
 

@@ -2,20 +2,30 @@
 // fp32 natural-log logsumexp. Replaces the role of flash_fwd_kernel (cuda/attention.cu:17-73)
 // at bf16; the fp32 path is attn_f32.hip.
 //
-// Work decomposition: one workgroup = WAVES waves x 64 queries of one (b,h) slice; it walks
-// the 64-key tiles up to its last query (causal tile skipping). Each wave owns 64 queries as
-// two 32-query MFMA blocks.
-//
-// Per 64-key tile and wave, on v_mfma_f32_32x32x16_bf16:
-//   S^T[key][query] = K . Q^T   A = K rows from LDS (rows loaded through sigma32), B = Q
-//                               held in registers for the whole kernel
-//   online softmax in registers: each lane owns one query, so the row max is an in-lane
-//                               max3 chain plus one exchange with the other lane half, and the
-//                               row sum is kept per lane half until the epilogue
+// Work decomposition: one workgroup = 4 waves x 64 queries of one (b,h) slice; it walks the
+// 64-key tiles up to its last query (causal tile skipping). Each wave owns 64 queries as two
+// 32-query MFMA blocks and handles each key tile as two 32-key chunks. Per chunk and wave, on
+// v_mfma_f32_32x32x16_bf16:
+//   S^T[key][query] = K . Q^T   A = K rows from LDS (rows loaded through sigma32), B = Q held
+//                               in registers for the whole kernel; one K operand read feeds
+//                               both query blocks
+//   online softmax in registers: each lane owns one query, so the row max is an in-lane max3
+//                               chain plus one exchange with the other lane half
 //   O^T[d][query] += V^T . P^T  A = V^T from the transposed LDS tile, B = P straight from the
 //                               score registers (bf16), no lane exchange
-// K and V^T tiles are double-buffered in LDS: the next tile's global loads are in flight
-// while the current tile is on the MFMA pipes; one barrier per tile.
+//
+// VALU per score, the forward's other bound at d_head 64: the scale is folded into the
+// exponent (one FMA: exp2(s*c - m)), the max takes half a v_max3 per score, the bf16 pack
+// half a v_cvt_pk, and the row sum one fp32 add (in fp32, before the bf16 rounding, so the
+// saved logsumexp keeps fp32 accuracy). Rescaling is lazy: the running max m only moves when a row's new
+// maximum exceeds it by more than kRescale (log2 units), so the O accumulators are rescaled
+// on a few chunks per row instead of every chunk; P stays below 2^kRescale, and O and l carry
+// the same factor, which the epilogue's division removes.
+//
+// Registers stay under 256 per lane (launch bound: 2 waves per SIMD), so a SIMD interleaves
+// one wave's softmax with the other's MFMAs. K and V^T tiles are double-buffered in LDS: the
+// next tile's global loads are in flight while the current tile is on the MFMA pipes; one
+// barrier per tile.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "tiles.hpp"
@@ -23,14 +33,100 @@
 namespace dadgpt {
 namespace {
 
-constexpr int kQW = 64;  // queries per wave
+constexpr int kQW = 64;             // queries per wave
+constexpr int kWaves = 4;           // waves per workgroup
+constexpr float kRescale = 8.0f;    // lazy-rescale threshold, log2 units
 
-template <int D, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void fwd_bf16_kernel(
+// One 32-key chunk (tile keys 32*kb ..) against the wave's 64 queries (two 32-query blocks).
+// Register r of lane half hi holds key c0 + 16*(r>>3) + 8*hi + (r&7); DIAG chunks mask keys
+// after the query.
+template <int D, bool DIAG>
+__device__ __forceinline__ void fwd_chunk(f32x16 (&oacc)[2][D / 32], float (&mrun)[2],
+                                          float (&lrun)[2], const bf16x8 (&qop)[2][D / 16],
+                                          const bf16* lk, const bf16* lv, int kb,
+                                          int qrow_minus_c0, int l32, int hi,
+                                          float scale_log2) {
+  constexpr int DS = D / 16, DB = D / 32;
+  // ---- S^T chunk = K[chunk] Q^T for both query blocks; each K operand read once ----
+  f32x16 s[2] = {f32x16{}, f32x16{}};
+  const int krow = 32 * kb + sigma32(l32);
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    const bf16x8 a = lds_op(lk, rm_off<D>(krow, 2 * ds + hi));
+    s[0] = mfma32(a, qop[0][ds], s[0]);
+    s[1] = mfma32(a, qop[1][ds], s[1]);
+  }
+  // ---- online softmax, per query = per lane ----
+  bf16x8 pb[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    // key offset within the chunk minus (query - c0): > 0 means masked
+    const int rel = qrow_minus_c0 + 32 * i - 8 * hi;
+    if (DIAG) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        s[i][r] = 16 * (r >> 3) + (r & 7) > rel ? neg_inf() : s[i][r];
+    }
+    float mx = s[i][0];
+#pragma unroll
+    for (int r = 1; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s[i][r]), s[i][r + 1]);
+    mx = max_halves(fmaxf(mx, s[i][15]));
+    if (DIAG) mx = mx == neg_inf() ? mx : mx * scale_log2;  // a fully masked row stays -inf
+    else mx *= scale_log2;
+    // Lazy rescale (wave-uniform branch): move m only when some row's max exceeds it by more
+    // than kRescale. A row whose chunk is fully masked has mx = -inf: no change.
+    if (__builtin_amdgcn_ballot_w64(mx > mrun[i] + kRescale) != 0) {
+      const float mnew = fmaxf(mrun[i], mx);
+      // 0 on a row's first chunk (mrun = -inf); 1 while a row has seen no key
+      const float corr = mnew == neg_inf() ? 1.0f : fast_exp2(mrun[i] - mnew);
+      mrun[i] = mnew;
+      lrun[i] *= corr;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) oacc[i][db] *= corr;
+    }
+    const float mneg = -mrun[i];
+    float ls = lrun[i];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 8 * j + 2 * e;
+        float p0 = fast_exp2(fmaf(s[i][r], scale_log2, mneg));
+        float p1 = fast_exp2(fmaf(s[i][r + 1], scale_log2, mneg));
+        if (DIAG) {  // exact zeros for masked keys, whatever the scale
+          p0 = 16 * j + 2 * e > rel ? 0.f : p0;
+          p1 = 16 * j + 2 * e + 1 > rel ? 0.f : p1;
+        }
+        w[e] = pack_bf16x2(p0, p1);
+        ls += p0 + p1;
+      }
+      pb[i][j] = as_bf16x8(w);
+    }
+    lrun[i] = ls;
+  }
+  // ---- O^T += V^T[:, chunk] P^T; each V^T operand read once for both query blocks ----
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    const int col = 32 * db + l32;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const bf16x8 a = lds_op(lv, tr_off(col, 4 * kb + 2 * j + hi));
+      oacc[0][db] = mfma32(a, pb[0][j], oacc[0][db]);
+      oacc[1][db] = mfma32(a, pb[1][j], oacc[1][db]);
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kWaves, 2) void fwd_bf16_kernel(
     bf16* __restrict__ out, float* __restrict__ lse, const bf16* __restrict__ q,
-    const bf16* __restrict__ k, const bf16* __restrict__ v, int S, float scale_log2) {
-  constexpr int NT = 64 * WAVES;
-  constexpr int QB = kQW * WAVES;
+    const bf16* __restrict__ k, const bf16* __restrict__ v, int S, float scale_log2,
+    int negate_q) {
+  // scale_log2 = |scale| * log2(e); a negative scale is applied by negating Q (exact in bf16),
+  // so the row max of the raw scores is the row max of the scaled ones.
+  constexpr int NT = 64 * kWaves;
+  constexpr int QB = kQW * kWaves;
   constexpr int DS = D / 16;  // 16-wide K-steps along D
   constexpr int DB = D / 32;  // 32-row blocks of O^T
   __shared__ __attribute__((aligned(16))) bf16 sk[2][kTileRows * D];
@@ -58,6 +154,7 @@ __global__ __launch_bounds__(64 * WAVES) void fwd_bf16_kernel(
     for (int ds = 0; ds < DS; ++ds) {
       qop[i][ds] = row < S ? ld_g128(qg + (size_t)row * D + 16 * ds + 8 * hi)
                            : as_bf16x8(u32x4{0, 0, 0, 0});
+      if (negate_q) qop[i][ds] = neg_bf16x8(qop[i][ds]);
     }
   }
 
@@ -66,8 +163,8 @@ __global__ __launch_bounds__(64 * WAVES) void fwd_bf16_kernel(
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[i][db] = f32x16{};
-  float mrun[2] = {neg_inf(), neg_inf()};
-  float lrun[2] = {0.f, 0.f};
+  float mrun[2] = {neg_inf(), neg_inf()};  // running max, scaled log2 units
+  float lrun[2] = {0.f, 0.f};              // per lane half; halves summed in the epilogue
 
   RowTile<D, NT> kt;
   PairTile<D, NT> vt;
@@ -84,78 +181,18 @@ __global__ __launch_bounds__(64 * WAVES) void fwd_bf16_kernel(
       kt.load(kg, k0 + kTileRows, S, tid);
       vt.load(vg, k0 + kTileRows, S, tid);
     }
-    if (q0 < S && k0 <= q0 + kQW - 1) {
-      const bf16* lk = sk[st];
-      const bf16* lv = svt[st];
-      // ---- S^T = K Q^T for both query blocks; each K operand read once ----
-      f32x16 s[2][2];
+    if (q0 < S) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        s[0][kb] = f32x16{};
-        s[1][kb] = f32x16{};
-        const int krow = 32 * kb + sigma32(l32);
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-          const bf16x8 a = lds_op(lk, rm_off<D>(krow, 2 * ds + hi));
-          s[0][kb] = mfma32(a, qop[0][ds], s[0][kb]);
-          s[1][kb] = mfma32(a, qop[1][ds], s[1][kb]);
-        }
-      }
-      // ---- online softmax (log2 domain), per query = per lane ----
-      const bool diag = k0 + kTileRows - 1 > q0;
-      bf16x8 pb[2][4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int qrow = q0 + 32 * i + l32;
-        float mx = neg_inf();
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float x = s[i][kb][r] * scale_log2;
-            if (diag) {
-              const int key = k0 + 32 * kb + 16 * (r >> 3) + 8 * hi + (r & 7);
-              if (key > qrow) x = neg_inf();
-            }
-            s[i][kb][r] = x;
-            mx = fmaxf(mx, x);
-          }
-        mx = fmaxf(mx, other_half(mx));
-        const float mnew = fmaxf(mrun[i], mx);
-        const float corr = fast_exp2(mrun[i] - mnew);
-        mrun[i] = mnew;
-        float ls = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = fast_exp2(s[i][kb][r] - mnew);
-            s[i][kb][r] = p;
-            ls += p;
-          }
-        lrun[i] = lrun[i] * corr + ls;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) oacc[i][db] *= corr;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const f32x16& src = s[i][ks >> 1];
-          const int r0 = (ks & 1) * 8;
-          u32x4 w;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(src[r0 + 2 * e], src[r0 + 2 * e + 1]);
-          pb[i][ks] = as_bf16x8(w);
-        }
-      }
-      // ---- O^T += V^T P^T; each V^T operand read once for both query blocks ----
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int col = 32 * db + l32;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 a = lds_op(lv, tr_off(col, 2 * ks + hi));
-          oacc[0][db] = mfma32(a, pb[0][ks], oacc[0][db]);
-          oacc[1][db] = mfma32(a, pb[1][ks], oacc[1][db]);
-        }
+        const int c0 = k0 + 32 * kb;           // first key of the chunk
+        if (c0 > q0 + kQW - 1) continue;       // every key after every query of the wave
+        const int rel = q0 + l32 - c0;
+        if (c0 + 31 > q0)                      // some key after some query: mask
+          fwd_chunk<D, true>(oacc, mrun, lrun, qop, sk[st], svt[st], kb, rel, l32, hi,
+                             scale_log2);
+        else
+          fwd_chunk<D, false>(oacc, mrun, lrun, qop, sk[st], svt[st], kb, rel, l32, hi,
+                              scale_log2);
       }
     }
     if (t + 1 < n_tiles) {
@@ -169,7 +206,7 @@ __global__ __launch_bounds__(64 * WAVES) void fwd_bf16_kernel(
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int qrow = q0 + 32 * i + l32;
-    const float l = lrun[i] + other_half(lrun[i]);
+    const float l = sum_halves(lrun[i]);
     const float inv = 1.0f / l;
     if (qrow < S) {
       bf16* orow = out + base + (size_t)qrow * D;
@@ -188,13 +225,13 @@ __global__ __launch_bounds__(64 * WAVES) void fwd_bf16_kernel(
   }
 }
 
-template <int D, int WAVES>
+template <int D>
 hipError_t launch_fwd_bf16_t(bf16* out, float* lse, const bf16* q, const bf16* k, const bf16* v,
                              int BH, int S, float scale, hipStream_t stream) {
-  constexpr int QB = kQW * WAVES;
+  constexpr int QB = kQW * kWaves;
   dim3 grid(BH, (S + QB - 1) / QB);
-  fwd_bf16_kernel<D, WAVES><<<grid, 64 * WAVES, 0, stream>>>(out, lse, q, k, v, S,
-                                                              scale * kLog2e);
+  fwd_bf16_kernel<D><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S,
+                                                       fabsf(scale) * kLog2e, scale < 0.f);
   return hipGetLastError();
 }
 
@@ -202,8 +239,8 @@ hipError_t launch_fwd_bf16_t(bf16* out, float* lse, const bf16* q, const bf16* k
 
 hipError_t launch_fwd_bf16(bf16* out, float* lse, const bf16* q, const bf16* k, const bf16* v,
                            int BH, int S, int D, float scale, hipStream_t stream) {
-  if (D == 64) return launch_fwd_bf16_t<64, 4>(out, lse, q, k, v, BH, S, scale, stream);
-  if (D == 32) return launch_fwd_bf16_t<32, 2>(out, lse, q, k, v, BH, S, scale, stream);
+  if (D == 64) return launch_fwd_bf16_t<64>(out, lse, q, k, v, BH, S, scale, stream);
+  if (D == 32) return launch_fwd_bf16_t<32>(out, lse, q, k, v, BH, S, scale, stream);
   return hipErrorInvalidValue;
 }
 
