@@ -12,8 +12,8 @@
 // Both MFMA kernels own their outputs outright (no atomics, bitwise repeatable). The score
 // tiles use the same sigma32 row permutation as the forward so that P and dS feed the next
 // MFMA as B operands from registers; the operands that must be read along the score dimension
-// (Q^T and dO^T in the dK/dV kernel, K^T in the dQ kernel) come from transposed LDS tiles
-// built during staging. Masking is compiled only into the blocks that straddle the diagonal
+// (Q^T and dO^T in the dK/dV kernel, K^T in the dQ kernel) are read across the rows of the
+// row-major LDS tiles with ds_read_b64_tr_b16, so every tile is staged once, row-major. Masking is compiled only into the blocks that straddle the diagonal
 // (template DIAG), so the other blocks run branch-free. Registers stay under 256 per lane
 // (launch bound: 2 waves per SIMD) so each SIMD interleaves two waves.
 #include "common.hpp"
@@ -79,11 +79,11 @@ template <int D, bool DIAG>
 __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dvacc)[D / 32],
                                            const bf16x8 (&kop)[D / 16],
                                            const bf16x8 (&vop)[D / 16], const bf16* sq,
-                                           const bf16* sqt, const bf16* sdo, const bf16* sdot,
-                                           const float* slse, const float* sdel, int qb,
-                                           int key_minus_r0, int l32, int hi,
-                                           float scale_log2) {
+                                           const bf16* sdo, const float* slse,
+                                           const float* sdel, int qb, int key_minus_r0,
+                                           int lane, float scale_log2) {
   constexpr int DS = D / 16, DB = D / 32;
+  const int l32 = lane & 31, hi = lane >> 5;
   f32x16 s = f32x16{}, dp = f32x16{};
   const int qr = 32 * qb + sigma32(l32);
 #pragma unroll
@@ -122,12 +122,11 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
   }
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
-    const int col = 32 * db + l32;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int chunk = 4 * qb + 2 * j + hi;  // tile queries 32qb + 16j + 8hi ..
-      dvacc[db] = mfma32(lds_op(sdot, tr_off(col, chunk)), pb[j], dvacc[db]);
-      dkacc[db] = mfma32(lds_op(sqt, tr_off(col, chunk)), dsb[j], dkacc[db]);
+      // A = dO^T / Q^T: lane d = 32db + l32 gets tile queries 32qb + 16j + 8hi + 0..7
+      dvacc[db] = mfma32(lds_tr_op<D>(sdo, 32 * qb + 16 * j, 32 * db, lane), pb[j], dvacc[db]);
+      dkacc[db] = mfma32(lds_tr_op<D>(sq, 32 * qb + 16 * j, 32 * db, lane), dsb[j], dkacc[db]);
     }
   }
 }
@@ -142,9 +141,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void dkdv_bf16_kernel(
   constexpr int KB = kKW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
   __shared__ __attribute__((aligned(16))) bf16 sq[2][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sqt[2][D * kTileRows];
   __shared__ __attribute__((aligned(16))) bf16 sdo[2][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sdot[2][D * kTileRows];
   __shared__ __attribute__((aligned(16))) float slse[2][kTileRows];
   __shared__ __attribute__((aligned(16))) float sdel[2][kTileRows];
 
@@ -181,7 +178,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void dkdv_bf16_kernel(
     dvacc[db] = f32x16{};
   }
 
-  PairTile<D, NT> qt, dot;
+  RowTile<D, NT> qt, dot;
   float lse_r = 0.f, del_r = 0.f;
   auto load_rows = [&](int row0) {
     qt.load(qg, row0, S, tid);
@@ -194,10 +191,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void dkdv_bf16_kernel(
     }
   };
   auto store_rows = [&](int st) {
-    qt.store_rm(sq[st], tid);
-    qt.store_tr(sqt[st], tid);
-    dot.store_rm(sdo[st], tid);
-    dot.store_tr(sdot[st], tid);
+    qt.store(sq[st], tid);
+    dot.store(sdo[st], tid);
     if (tid < kTileRows) {
       slse[st][tid] = lse_r;
       sdel[st][tid] = del_r;
@@ -217,11 +212,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void dkdv_bf16_kernel(
         const int qlo = r0 + 32 * qb;  // first query of the block
         if (qlo + 31 < kw0) continue;   // every key of the wave is after every query
         if (qlo < kw0 + kKW - 1)        // some key after some query: mask
-          dkdv_block<D, true>(dkacc, dvacc, kop, vop, sq[st], sqt[st], sdo[st], sdot[st],
-                              slse[st], sdel[st], qb, key - r0, l32, hi, scale_log2);
+          dkdv_block<D, true>(dkacc, dvacc, kop, vop, sq[st], sdo[st], slse[st], sdel[st], qb,
+                              key - r0, lane, scale_log2);
         else
-          dkdv_block<D, false>(dkacc, dvacc, kop, vop, sq[st], sqt[st], sdo[st], sdot[st],
-                               slse[st], sdel[st], qb, key - r0, l32, hi, scale_log2);
+          dkdv_block<D, false>(dkacc, dvacc, kop, vop, sq[st], sdo[st], slse[st], sdel[st], qb,
+                               key - r0, lane, scale_log2);
       }
     }
     if (t + 1 < t_end) store_rows(st ^ 1);
@@ -242,10 +237,10 @@ constexpr int kQW = 32;  // queries per wave
 template <int D, bool DIAG>
 __device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (&qop)[D / 16],
                                          const bf16x8 (&doop)[D / 16], const bf16* sk,
-                                         const bf16* skt, const bf16* sv, int kb,
-                                         int qrow_minus_k0, float lse2, float dlt, int l32,
-                                         int hi, float scale_log2) {
+                                         const bf16* sv, int kb, int qrow_minus_k0, float lse2,
+                                         float dlt, int lane, float scale_log2) {
   constexpr int DS = D / 16, DB = D / 32;
+  const int l32 = lane & 31, hi = lane >> 5;
   f32x16 s = f32x16{}, dp = f32x16{};
   const int krow = 32 * kb + sigma32(l32);
 #pragma unroll
@@ -273,10 +268,9 @@ __device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (
   }
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
-    const int col = 32 * db + l32;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      dqacc[db] = mfma32(lds_op(skt, tr_off(col, 4 * kb + 2 * j + hi)), dsb[j], dqacc[db]);
+    for (int j = 0; j < 2; ++j)  // A = K^T: lane d = 32db + l32 gets keys 32kb + 16j + 8hi ..
+      dqacc[db] = mfma32(lds_tr_op<D>(sk, 32 * kb + 16 * j, 32 * db, lane), dsb[j], dqacc[db]);
   }
 }
 
@@ -289,7 +283,6 @@ __global__ __launch_bounds__(64 * kWaves, 2) void dq_bf16_kernel(
   constexpr int QB = kQW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
   __shared__ __attribute__((aligned(16))) bf16 sk[2][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 skt[2][D * kTileRows];
   __shared__ __attribute__((aligned(16))) bf16 sv[2][kTileRows * D];
 
   const int bh = blockIdx.x;
@@ -321,13 +314,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void dq_bf16_kernel(
 #pragma unroll
   for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
 
-  PairTile<D, NT> kt;
-  RowTile<D, NT> vt;
+  RowTile<D, NT> kt, vt;
   kt.load(kg, 0, S, tid);
   vt.load(vg, 0, S, tid);
-  kt.store_rm(sk[0], tid);
-  kt.store_tr(skt[0], tid);
-  vt.store_rm(sv[0], tid);
+  kt.store(sk[0], tid);
+  vt.store(sv[0], tid);
   __syncthreads();
 
   for (int t = 0; t < n_tiles; ++t) {
@@ -343,17 +334,16 @@ __global__ __launch_bounds__(64 * kWaves, 2) void dq_bf16_kernel(
         const int klo = k0 + 32 * kb;        // first key of the chunk
         if (klo > q0 + kQW - 1) continue;    // every key after every query of the wave
         if (klo + 31 > q0)                   // some key after some query: mask
-          dq_chunk<D, true>(dqacc, qop, doop, sk[st], skt[st], sv[st], kb, qrow - k0, lse2,
-                            dlt, l32, hi, scale_log2);
+          dq_chunk<D, true>(dqacc, qop, doop, sk[st], sv[st], kb, qrow - k0, lse2, dlt, lane,
+                            scale_log2);
         else
-          dq_chunk<D, false>(dqacc, qop, doop, sk[st], skt[st], sv[st], kb, qrow - k0, lse2,
-                             dlt, l32, hi, scale_log2);
+          dq_chunk<D, false>(dqacc, qop, doop, sk[st], sv[st], kb, qrow - k0, lse2, dlt, lane,
+                             scale_log2);
       }
     }
     if (t + 1 < n_tiles) {
-      kt.store_rm(sk[st ^ 1], tid);
-      kt.store_tr(skt[st ^ 1], tid);
-      vt.store_rm(sv[st ^ 1], tid);
+      kt.store(sk[st ^ 1], tid);
+      vt.store(sv[st ^ 1], tid);
     }
     __syncthreads();
   }

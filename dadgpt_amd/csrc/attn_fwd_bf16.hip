@@ -11,8 +11,9 @@
 //                               both query blocks
 //   online softmax in registers: each lane owns one query, so the row max is an in-lane max3
 //                               chain plus one exchange with the other lane half
-//   O^T[d][query] += V^T . P^T  A = V^T from the transposed LDS tile, B = P straight from the
-//                               score registers (bf16), no lane exchange
+//   O^T[d][query] += V^T . P^T  A = V^T read across the rows of the row-major V tile with
+//                               ds_read_b64_tr_b16, B = P straight from the score registers
+//                               (bf16), no lane exchange
 //
 // VALU per score, the forward's other bound at d_head 64: the scale is folded into the
 // exponent (one FMA: exp2(s*c - m)), the max takes half a v_max3 per score, the bf16 pack
@@ -23,9 +24,9 @@
 // the same factor, which the epilogue's division removes.
 //
 // Registers stay under 256 per lane (launch bound: 2 waves per SIMD), so a SIMD interleaves
-// one wave's softmax with the other's MFMAs. K and V^T tiles are double-buffered in LDS: the
-// next tile's global loads are in flight while the current tile is on the MFMA pipes; one
-// barrier per tile.
+// one wave's softmax with the other's MFMAs. K and V tiles are double-buffered in LDS (both
+// row-major, stored straight from the 16-byte global loads): the next tile's global loads are
+// in flight while the current tile is on the MFMA pipes; one barrier per tile.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "tiles.hpp"
@@ -44,8 +45,8 @@ template <int D, bool DIAG>
 __device__ __forceinline__ void fwd_chunk(f32x16 (&oacc)[2][D / 32], float (&mrun)[2],
                                           float (&lrun)[2], const bf16x8 (&qop)[2][D / 16],
                                           const bf16* lk, const bf16* lv, int kb,
-                                          int qrow_minus_c0, int l32, int hi,
-                                          float scale_log2) {
+                                          int qrow_minus_c0, int lane, float scale_log2) {
+  const int l32 = lane & 31, hi = lane >> 5;
   constexpr int DS = D / 16, DB = D / 32;
   // ---- S^T chunk = K[chunk] Q^T for both query blocks; each K operand read once ----
   f32x16 s[2] = {f32x16{}, f32x16{}};
@@ -108,10 +109,9 @@ __device__ __forceinline__ void fwd_chunk(f32x16 (&oacc)[2][D / 32], float (&mru
   // ---- O^T += V^T[:, chunk] P^T; each V^T operand read once for both query blocks ----
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
-    const int col = 32 * db + l32;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const bf16x8 a = lds_op(lv, tr_off(col, 4 * kb + 2 * j + hi));
+      const bf16x8 a = lds_tr_op<D>(lv, 32 * kb + 16 * j, 32 * db, lane);
       oacc[0][db] = mfma32(a, pb[0][j], oacc[0][db]);
       oacc[1][db] = mfma32(a, pb[1][j], oacc[1][db]);
     }
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void fwd_bf16_kernel(
   constexpr int DS = D / 16;  // 16-wide K-steps along D
   constexpr int DB = D / 32;  // 32-row blocks of O^T
   __shared__ __attribute__((aligned(16))) bf16 sk[2][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 svt[2][D * kTileRows];
+  __shared__ __attribute__((aligned(16))) bf16 sv[2][kTileRows * D];
 
   const int bh = blockIdx.x;
   const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
@@ -166,12 +166,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void fwd_bf16_kernel(
   float mrun[2] = {neg_inf(), neg_inf()};  // running max, scaled log2 units
   float lrun[2] = {0.f, 0.f};              // per lane half; halves summed in the epilogue
 
-  RowTile<D, NT> kt;
-  PairTile<D, NT> vt;
+  RowTile<D, NT> kt, vt;
   kt.load(kg, 0, S, tid);
   vt.load(vg, 0, S, tid);
-  kt.store_rm(sk[0], tid);
-  vt.store_tr(svt[0], tid);
+  kt.store(sk[0], tid);
+  vt.store(sv[0], tid);
   __syncthreads();
 
   for (int t = 0; t < n_tiles; ++t) {
@@ -188,16 +187,16 @@ __global__ __launch_bounds__(64 * kWaves, 2) void fwd_bf16_kernel(
         if (c0 > q0 + kQW - 1) continue;       // every key after every query of the wave
         const int rel = q0 + l32 - c0;
         if (c0 + 31 > q0)                      // some key after some query: mask
-          fwd_chunk<D, true>(oacc, mrun, lrun, qop, sk[st], svt[st], kb, rel, l32, hi,
+          fwd_chunk<D, true>(oacc, mrun, lrun, qop, sk[st], sv[st], kb, rel, lane,
                              scale_log2);
         else
-          fwd_chunk<D, false>(oacc, mrun, lrun, qop, sk[st], svt[st], kb, rel, l32, hi,
+          fwd_chunk<D, false>(oacc, mrun, lrun, qop, sk[st], sv[st], kb, rel, lane,
                               scale_log2);
       }
     }
     if (t + 1 < n_tiles) {
-      kt.store_rm(sk[st ^ 1], tid);
-      vt.store_tr(svt[st ^ 1], tid);
+      kt.store(sk[st ^ 1], tid);
+      vt.store(sv[st ^ 1], tid);
     }
     __syncthreads();
   }

@@ -1,10 +1,13 @@
-// Global -> register -> LDS staging of 64-row tiles of a [S, D] bf16 matrix, in two LDS
-// layouts:
-//   row-major  [64][D]   read as MFMA operands along D (16-byte chunks, XOR-swizzled by row)
-//   transposed [D][64]   read as MFMA operands along the 64 rows (keys or queries)
-// The transposed layout is built in registers: a thread holds the same 8-column chunk of two
-// adjacent rows and interleaves them into 2-row dwords, so each LDS write is 4 bytes and each
-// operand read is one 16-byte ds_read.
+// Global -> register -> LDS staging of 64-row tiles of a [S, D] bf16 matrix, and the two ways
+// the MFMA kernels read them back:
+//   row operands        one ds_read_b128: 8 consecutive columns of one row (along D)
+//   transposed operands two ds_read_b64_tr_b16: 8 consecutive rows of one column (along the
+//                       64 tile rows), so the tile never has to be stored transposed
+// Tiles are row-major [64][D] in LDS with the 16-byte chunks of each row XOR-swizzled by a
+// function of the row. The swizzle was chosen by enumerating the XOR maps of the row bits
+// against the exact lane patterns of the three accesses (sigma32-permuted row reads,
+// transposed reads, staging writes): with it none of them has a bank conflict, for either a
+// 32- or a 64-bank LDS.
 #pragma once
 
 #include "common.hpp"
@@ -13,100 +16,83 @@ namespace dadgpt {
 
 constexpr int kTileRows = 64;
 
-// Element offset of 16-byte chunk `chunk` (8 bf16) of row `row` in a row-major [64][D] tile.
+__device__ __forceinline__ constexpr int parity(int x) { return __builtin_popcount(x) & 1; }
+
+// Chunk swizzle of row `row` (D=64: 8 chunks per row, D=32: 4).
 template <int D>
-__device__ __forceinline__ int rm_off(int row, int chunk) {
-  constexpr int C = D / 8;
-  return row * D + ((chunk ^ (row & (C - 1))) << 3);
+__device__ __forceinline__ constexpr int swz(int row) {
+  if constexpr (D == 64)
+    return parity(row & 2) | (parity(row & 5) << 1) | (parity(row & 10) << 2);
+  else
+    return parity(row & 6) | (parity(row & 10) << 1);
 }
 
-// Element offset of chunk `chunk` (tile rows 8*chunk .. 8*chunk+7) of column `col` in a
-// transposed [D][64] tile. The swizzle keeps both the operand reads (32 consecutive columns,
-// one chunk) and the staging writes (8 columns x 8 chunks) spread over the LDS banks.
-__device__ __forceinline__ int tr_off(int col, int chunk) {
-  return col * kTileRows + ((chunk ^ ((col ^ (col >> 3)) & 7)) << 3);
+// Element offset of 16-byte chunk `chunk` (8 bf16) of row `row` in a [64][D] tile.
+template <int D>
+__device__ __forceinline__ int rm_off(int row, int chunk) {
+  return row * D + ((chunk ^ swz<D>(row)) << 3);
 }
 
 __device__ __forceinline__ bf16x8 lds_op(const bf16* lds, int off) {
   return *reinterpret_cast<const bf16x8*>(lds + off);
 }
 
-// Tile staged as 16-byte chunks: unit u -> row u / (D/8), chunk u % (D/8). Consecutive
-// threads read consecutive 16-byte pieces of a row (fully used 64-byte segments).
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) bf16 lds_bf16;
+
+// MFMA operand (A or B of v_mfma_f32_32x32x16_bf16) read across rows of a row-major tile T:
+// lane l receives T[row0 + 8*(l/32) + e][col0 + l%32] for e = 0..7, i.e. the operand
+// X[idx = l%32][k = 8*(l/32) + e] of X = T^T.
+//
+// ds_read_b64_tr_b16 works on 16-lane groups: if lane j of a group supplies the address of 4
+// consecutive bf16 M_j[0..3], lane i of the group receives M_{4e + i/4}[i % 4] for e = 0..3.
+// So lane j points at row row0 + 8*(g/2) + 4*half + (j%16)/4, columns
+// col0 + 16*(g%2) + 4*(j%4) .. +3 (g = j/16), once for rows +0..3 (half 0) and once for +4..7.
+template <int D>
+__device__ __forceinline__ bf16x8 lds_tr_op(const bf16* tile, int row0, int col0, int lane) {
+  const int g = lane >> 4;
+  const int col = col0 + 16 * (g & 1) + 4 * (lane & 3);
+  const lds_bf16* t = (const lds_bf16*)(tile);  // generic -> LDS address space
+  s16x4 v[2];
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int row = row0 + 8 * (g >> 1) + 4 * half + ((lane >> 2) & 3);
+    const int off = row * D + (((col >> 3) ^ swz<D>(row)) << 3) + (col & 7);
+    v[half] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + off));
+  }
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// A 64-row tile staged as 16-byte chunks: unit u -> row u / (D/8), chunk u % (D/8).
+// Consecutive threads read consecutive 16-byte pieces of a row (fully used 64-byte segments).
 template <int D, int NT>
 struct RowTile {
   static constexpr int C = D / 8;
   static constexpr int UNITS = kTileRows * C;
   static constexpr int PER = (UNITS + NT - 1) / NT;
+  static_assert(UNITS % NT == 0, "whole units per thread");
   u32x4 a[PER];
 
   __device__ __forceinline__ void load(const bf16* g, int row0, int S, int tid) {
+    const bf16* p = g + (size_t)row0 * D + (tid / C) * D + (tid % C) * 8;
+    if (row0 + kTileRows <= S) {  // whole tile in bounds (uniform branch)
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = tid + i * NT;
-      const int row = u / C, ch = u % C;
-      a[i] = u32x4{0, 0, 0, 0};
-      if (u < UNITS && row0 + row < S) a[i] = ld_g128u(g + (size_t)(row0 + row) * D + ch * 8);
-    }
-  }
-  __device__ __forceinline__ void store_rm(bf16* lds, int tid) const {
+      for (int i = 0; i < PER; ++i) a[i] = ld_g128u(p + (size_t)i * (NT / C) * D);
+    } else {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = tid + i * NT;
-      if (u < UNITS) *reinterpret_cast<u32x4*>(lds + rm_off<D>(u / C, u % C)) = a[i];
-    }
-  }
-};
-
-// Tile staged as row pairs: unit u -> rows 2*(u / (D/8)) and +1, chunk u % (D/8). Can be
-// stored row-major, transposed, or both from the same registers.
-template <int D, int NT>
-struct PairTile {
-  static constexpr int C = D / 8;
-  static constexpr int UNITS = (kTileRows / 2) * C;
-  static constexpr int PER = (UNITS + NT - 1) / NT;
-  u32x4 a[PER], b[PER];
-
-  __device__ __forceinline__ void load(const bf16* g, int row0, int S, int tid) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = tid + i * NT;
-      const int r = row0 + 2 * (u / C), ch = u % C;
-      a[i] = u32x4{0, 0, 0, 0};
-      b[i] = u32x4{0, 0, 0, 0};
-      if (u < UNITS) {
-        if (r < S) a[i] = ld_g128u(g + (size_t)r * D + ch * 8);
-        if (r + 1 < S) b[i] = ld_g128u(g + (size_t)(r + 1) * D + ch * 8);
+      for (int i = 0; i < PER; ++i) {
+        const int row = (tid + i * NT) / C;
+        a[i] = u32x4{0, 0, 0, 0};
+        if (row0 + row < S) a[i] = ld_g128u(p + (size_t)i * (NT / C) * D);
       }
     }
   }
-  __device__ __forceinline__ void store_rm(bf16* lds, int tid) const {
+  __device__ __forceinline__ void store(bf16* lds, int tid) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int u = tid + i * NT;
-      if (u < UNITS) {
-        const int p = u / C, ch = u % C;
-        *reinterpret_cast<u32x4*>(lds + rm_off<D>(2 * p, ch)) = a[i];
-        *reinterpret_cast<u32x4*>(lds + rm_off<D>(2 * p + 1, ch)) = b[i];
-      }
-    }
-  }
-  __device__ __forceinline__ void store_tr(bf16* lds, int tid) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = tid + i * NT;
-      if (u < UNITS) {
-        const int p = u / C, ch = u % C;
-        const int col0 = ch * 8, chunk = p >> 2, within = 2 * (p & 3);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t x = a[i][w], y = b[i][w];
-          const uint32_t even = (x & 0xffffu) | (y << 16);          // column col0 + 2w
-          const uint32_t odd = (x >> 16) | (y & 0xffff0000u);       // column col0 + 2w + 1
-          *reinterpret_cast<uint32_t*>(lds + tr_off(col0 + 2 * w, chunk) + within) = even;
-          *reinterpret_cast<uint32_t*>(lds + tr_off(col0 + 2 * w + 1, chunk) + within) = odd;
-        }
-      }
+      *reinterpret_cast<u32x4*>(lds + rm_off<D>(u / C, u % C)) = a[i];
     }
   }
 };
