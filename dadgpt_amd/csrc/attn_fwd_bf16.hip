@@ -2,13 +2,13 @@
 // fp32 natural-log logsumexp. Replaces the role of flash_fwd_kernel (cuda/attention.cu:17-73)
 // at bf16; the fp32 path is attn_f32.hip.
 //
-// Work decomposition: one workgroup = 4 waves x 64 queries of one (b,h) slice; it walks the
-// 64-key tiles up to its last query (causal tile skipping). Each wave owns 64 queries as two
+// Work decomposition: one workgroup = WAVES waves x NQB*32 queries of one (b,h) slice; it
+// walks the 64-key tiles up to its last query (causal tile skipping). Each wave owns NQB
 // 32-query MFMA blocks and handles each key tile as two 32-key chunks. Per chunk and wave, on
 // v_mfma_f32_32x32x16_bf16:
 //   S^T[key][query] = K . Q^T   A = K rows from LDS (rows loaded through sigma32), B = Q held
 //                               in registers for the whole kernel; one K operand read feeds
-//                               both query blocks
+//                               every query block of the wave
 //   online softmax in registers: each lane owns one query, so the row max is an in-lane max3
 //                               chain plus one exchange with the other lane half
 //   O^T[d][query] += V^T . P^T  A = V^T read across the rows of the row-major V tile with
@@ -18,15 +18,16 @@
 // VALU per score, the forward's other bound at d_head 64: the scale is folded into the
 // exponent (one FMA: exp2(s*c - m)), the max takes half a v_max3 per score, the bf16 pack
 // half a v_cvt_pk, and the row sum one fp32 add (in fp32, before the bf16 rounding, so the
-// saved logsumexp keeps fp32 accuracy). Rescaling is lazy: the running max m only moves when a row's new
-// maximum exceeds it by more than kRescale (log2 units), so the O accumulators are rescaled
+// saved logsumexp keeps fp32 accuracy). Rescaling is lazy: the running max m only moves when
+// a row's new maximum exceeds it by more than kRescale (log2 units), so the O accumulators are rescaled
 // on a few chunks per row instead of every chunk; P stays below 2^kRescale, and O and l carry
 // the same factor, which the epilogue's division removes.
 //
-// Registers stay under 256 per lane (launch bound: 2 waves per SIMD), so a SIMD interleaves
-// one wave's softmax with the other's MFMAs. K and V tiles are double-buffered in LDS (both
-// row-major, stored straight from the 16-byte global loads): the next tile's global loads are
-// in flight while the current tile is on the MFMA pipes; one barrier per tile.
+// The launch bound caps registers so that several waves share each SIMD, which interleaves
+// one wave's softmax with another's MFMAs and covers LDS latency. K and V tiles are
+// triple-buffered in LDS and staged by direct global->LDS loads (no registers, no LDS-store
+// instructions): tiles t+1 and t+2 are in flight while tile t is on the MFMA pipes; one
+// barrier per tile.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "tiles.hpp"
@@ -34,33 +35,49 @@
 namespace dadgpt {
 namespace {
 
-constexpr int kQW = 64;             // queries per wave
-constexpr int kWaves = 4;           // waves per workgroup
-constexpr float kRescale = 8.0f;    // lazy-rescale threshold, log2 units
+// Geometry: NQB 32-query blocks per wave, WAVES waves per workgroup, MINB workgroups per CU
+// (the register budget: 512 / (MINB * WAVES / 4) per lane). One wave with one query block and
+// 8 waves per workgroup keeps 4 waves on each SIMD to cover LDS and MFMA latencies; two query
+// blocks per wave halve the LDS reads per MFMA instead.
+#ifndef DADGPT_FWD_NQB
+#define DADGPT_FWD_NQB 1
+#endif
+#ifndef DADGPT_FWD_WAVES
+#define DADGPT_FWD_WAVES 4
+#endif
+#ifndef DADGPT_FWD_MINB
+#define DADGPT_FWD_MINB 3
+#endif
+constexpr int kNQB = DADGPT_FWD_NQB;
+constexpr int kQW = 32 * kNQB;            // queries per wave
+constexpr int kWaves = DADGPT_FWD_WAVES;  // waves per workgroup
+constexpr int kMinBlocks = DADGPT_FWD_MINB;
+constexpr float kRescale = 8.0f;          // lazy-rescale threshold, log2 units
 
-// One 32-key chunk (tile keys 32*kb ..) against the wave's 64 queries (two 32-query blocks).
-// Register r of lane half hi holds key c0 + 16*(r>>3) + 8*hi + (r&7); DIAG chunks mask keys
-// after the query.
-template <int D, bool DIAG>
-__device__ __forceinline__ void fwd_chunk(f32x16 (&oacc)[2][D / 32], float (&mrun)[2],
-                                          float (&lrun)[2], const bf16x8 (&qop)[2][D / 16],
+// One 32-key chunk (tile keys 32*kb ..) against the wave's NQB 32-query blocks. Register r of
+// lane half hi holds key c0 + 16*(r>>3) + 8*hi + (r&7); DIAG chunks mask keys after the query.
+template <int D, int NQB, bool DIAG>
+__device__ __forceinline__ void fwd_chunk(f32x16 (&oacc)[NQB][D / 32], float (&mrun)[NQB],
+                                          float (&lrun)[NQB], const bf16x8 (&qop)[NQB][D / 16],
                                           const bf16* lk, const bf16* lv, int kb,
                                           int qrow_minus_c0, int lane, float scale_log2) {
   const int l32 = lane & 31, hi = lane >> 5;
   constexpr int DS = D / 16, DB = D / 32;
-  // ---- S^T chunk = K[chunk] Q^T for both query blocks; each K operand read once ----
-  f32x16 s[2] = {f32x16{}, f32x16{}};
+  // ---- S^T chunk = K[chunk] Q^T for every query block; each K operand read once ----
+  f32x16 s[NQB];
+#pragma unroll
+  for (int i = 0; i < NQB; ++i) s[i] = f32x16{};
   const int krow = 32 * kb + sigma32(l32);
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) {
     const bf16x8 a = lds_op(lk, rm_off<D>(krow, 2 * ds + hi));
-    s[0] = mfma32(a, qop[0][ds], s[0]);
-    s[1] = mfma32(a, qop[1][ds], s[1]);
+#pragma unroll
+    for (int i = 0; i < NQB; ++i) s[i] = mfma32(a, qop[i][ds], s[i]);
   }
   // ---- online softmax, per query = per lane ----
-  bf16x8 pb[2][2];
+  bf16x8 pb[NQB][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < NQB; ++i) {
     // key offset within the chunk minus (query - c0): > 0 means masked
     const int rel = qrow_minus_c0 + 32 * i - 8 * hi;
     if (DIAG) {
@@ -112,25 +129,33 @@ __device__ __forceinline__ void fwd_chunk(f32x16 (&oacc)[2][D / 32], float (&mru
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const bf16x8 a = lds_tr_op<D>(lv, 32 * kb + 16 * j, 32 * db, lane);
-      oacc[0][db] = mfma32(a, pb[0][j], oacc[0][db]);
-      oacc[1][db] = mfma32(a, pb[1][j], oacc[1][db]);
+#pragma unroll
+      for (int i = 0; i < NQB; ++i) oacc[i][db] = mfma32(a, pb[i][j], oacc[i][db]);
     }
   }
 }
 
 template <int D>
-__global__ __launch_bounds__(64 * kWaves, 2) void fwd_bf16_kernel(
+__global__ __launch_bounds__(64 * kWaves, kMinBlocks)
+__attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_kernel(
     bf16* __restrict__ out, float* __restrict__ lse, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, int S, float scale_log2,
     int negate_q) {
   // scale_log2 = |scale| * log2(e); a negative scale is applied by negating Q (exact in bf16),
   // so the row max of the raw scores is the row max of the scaled ones.
-  constexpr int NT = 64 * kWaves;
   constexpr int QB = kQW * kWaves;
   constexpr int DS = D / 16;  // 16-wide K-steps along D
   constexpr int DB = D / 32;  // 32-row blocks of O^T
-  __shared__ __attribute__((aligned(16))) bf16 sk[2][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sv[2][kTileRows * D];
+  // K and V tiles, triple-buffered: tile t is read while t+1 and t+2 are in flight. Three
+  // separate arrays (not one indexed array) so that, with the tile loop unrolled by three,
+  // every LDS read names its buffer statically: the compiler then knows a pending direct
+  // load into another buffer does not alias it and inserts no wait for it.
+  __shared__ __attribute__((aligned(16))) bf16 sk0[kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 sk1[kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 sk2[kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 sv0[kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 sv1[kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 sv2[kTileRows * D];
 
   const int bh = blockIdx.x;
   const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
@@ -146,9 +171,9 @@ __global__ __launch_bounds__(64 * kWaves, 2) void fwd_bf16_kernel(
   const int n_tiles = wg_last / kTileRows + 1;
 
   // B operands of S^T: lane holds query q0 + 32i + l32, columns 16*ds + 8*hi + 0..7.
-  bf16x8 qop[2][DS];
+  bf16x8 qop[kNQB][DS];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < kNQB; ++i) {
     const int row = q0 + 32 * i + l32;
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
@@ -158,27 +183,41 @@ __global__ __launch_bounds__(64 * kWaves, 2) void fwd_bf16_kernel(
     }
   }
 
-  f32x16 oacc[2][DB];
+  f32x16 oacc[kNQB][DB];
+  float mrun[kNQB], lrun[kNQB];  // running max (scaled log2 units); per-half row sums
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kNQB; ++i) {
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[i][db] = f32x16{};
-  float mrun[2] = {neg_inf(), neg_inf()};  // running max, scaled log2 units
-  float lrun[2] = {0.f, 0.f};              // per lane half; halves summed in the epilogue
+    mrun[i] = neg_inf();
+    lrun[i] = 0.f;
+  }
 
-  RowTile<D, NT> kt, vt;
-  kt.load(kg, 0, S, tid);
-  vt.load(vg, 0, S, tid);
-  kt.store(sk[0], tid);
-  vt.store(sv[0], tid);
-  __syncthreads();
+  using Dma = DmaTile<D, kWaves>;
+  constexpr int NI = 2 * Dma::PER_WAVE;  // DMA instructions per wave per tile (K and V)
+  Dma::load(sk0, kg, 0, S, wave, lane);
+  Dma::load(sv0, vg, 0, S, wave, lane);
+  if (n_tiles > 1) {
+    Dma::load(sk1, kg, kTileRows, S, wave, lane);
+    Dma::load(sv1, vg, kTileRows, S, wave, lane);
+    wait_vm_lds<NI>();
+  } else {
+    wait_vm_lds<0>();
+  }
+  __builtin_amdgcn_s_barrier();
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int st = t & 1;
+  // One key tile: prefetch tile t+2 into (nk, nv) (it held tile t-1, released by the last
+  // barrier), compute tile t from (ck, cv), then wait for tile t+1 (only tile t+2's loads may
+  // still be in flight) and barrier, which also ends every wave's reads of tile t.
+  // `late` issues the prefetch after the compute instead: the first step of the unrolled loop
+  // uses it, because at the loop head the compiler cannot tell which buffer a pending direct
+  // load targets and waits for all of them before the first LDS read.
+  auto tile = [&](int t, const bf16* ck, const bf16* cv, bf16* nk, bf16* nv, bool late) {
     const int k0 = t * kTileRows;
-    if (t + 1 < n_tiles) {
-      kt.load(kg, k0 + kTileRows, S, tid);
-      vt.load(vg, k0 + kTileRows, S, tid);
+    const bool prefetch = t + 2 < n_tiles;
+    if (prefetch && !late) {
+      Dma::load(nk, kg, k0 + 2 * kTileRows, S, wave, lane);
+      Dma::load(nv, vg, k0 + 2 * kTileRows, S, wave, lane);
     }
     if (q0 < S) {
 #pragma unroll
@@ -187,23 +226,30 @@ __global__ __launch_bounds__(64 * kWaves, 2) void fwd_bf16_kernel(
         if (c0 > q0 + kQW - 1) continue;       // every key after every query of the wave
         const int rel = q0 + l32 - c0;
         if (c0 + 31 > q0)                      // some key after some query: mask
-          fwd_chunk<D, true>(oacc, mrun, lrun, qop, sk[st], sv[st], kb, rel, lane,
-                             scale_log2);
+          fwd_chunk<D, kNQB, true>(oacc, mrun, lrun, qop, ck, cv, kb, rel, lane, scale_log2);
         else
-          fwd_chunk<D, false>(oacc, mrun, lrun, qop, sk[st], sv[st], kb, rel, lane,
-                              scale_log2);
+          fwd_chunk<D, kNQB, false>(oacc, mrun, lrun, qop, ck, cv, kb, rel, lane, scale_log2);
       }
     }
-    if (t + 1 < n_tiles) {
-      kt.store(sk[st ^ 1], tid);
-      vt.store(sv[st ^ 1], tid);
+    if (prefetch && late) {
+      Dma::load(nk, kg, k0 + 2 * kTileRows, S, wave, lane);
+      Dma::load(nv, vg, k0 + 2 * kTileRows, S, wave, lane);
     }
-    __syncthreads();
+    if (prefetch)
+      wait_vm_lds<NI>();
+    else
+      wait_vm_lds<0>();
+    __builtin_amdgcn_s_barrier();
+  };
+  for (int t = 0; t < n_tiles; t += 3) {
+    tile(t, sk0, sv0, sk2, sv2, true);
+    if (t + 1 < n_tiles) tile(t + 1, sk1, sv1, sk0, sv0, false);
+    if (t + 2 < n_tiles) tile(t + 2, sk2, sv2, sk1, sv1, false);
   }
 
   // ---- epilogue: O = O^T / l, lse = ln2 * (m + log2 l) ----
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < kNQB; ++i) {
     const int qrow = q0 + 32 * i + l32;
     const float l = sum_halves(lrun[i]);
     const float inv = 1.0f / l;

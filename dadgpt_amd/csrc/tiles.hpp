@@ -66,15 +66,19 @@ __device__ __forceinline__ bf16x8 lds_tr_op(const bf16* tile, int row0, int col0
 
 // A 64-row tile staged as 16-byte chunks: unit u -> row u / (D/8), chunk u % (D/8).
 // Consecutive threads read consecutive 16-byte pieces of a row (fully used 64-byte segments).
+// With more threads than units (D=32 and 512 threads) the surplus threads stage nothing.
 template <int D, int NT>
 struct RowTile {
   static constexpr int C = D / 8;
   static constexpr int UNITS = kTileRows * C;
-  static constexpr int PER = (UNITS + NT - 1) / NT;
-  static_assert(UNITS % NT == 0, "whole units per thread");
+  static constexpr int PER = UNITS >= NT ? UNITS / NT : 1;
+  static_assert(UNITS % NT == 0 || NT % UNITS == 0, "units divide evenly over threads");
   u32x4 a[PER];
 
+  __device__ __forceinline__ static bool active(int tid) { return UNITS >= NT || tid < UNITS; }
+
   __device__ __forceinline__ void load(const bf16* g, int row0, int S, int tid) {
+    if (!active(tid)) return;
     const bf16* p = g + (size_t)row0 * D + (tid / C) * D + (tid % C) * 8;
     if (row0 + kTileRows <= S) {  // whole tile in bounds (uniform branch)
 #pragma unroll
@@ -89,6 +93,7 @@ struct RowTile {
     }
   }
   __device__ __forceinline__ void store(bf16* lds, int tid) const {
+    if (!active(tid)) return;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int u = tid + i * NT;
@@ -96,5 +101,41 @@ struct RowTile {
     }
   }
 };
+
+// Direct global -> LDS staging (global_load_lds_dwordx4): lane i of a wave-instruction writes
+// its 16 bytes to LDS at (instruction base + 16*i), so the swizzle is applied on the global
+// side: the lane that fills LDS slot (row, physical chunk c) reads logical chunk
+// c ^ swz(row). No registers hold the tile and the loads complete asynchronously into LDS,
+// which lets a kernel keep tiles in flight across barriers (vmcnt counts them). Rows past S
+// read row S-1 instead (in bounds; the kernels mask every key or query past S).
+template <int D, int WAVES>
+struct DmaTile {
+  static constexpr int C = D / 8;                       // 16-byte chunks per row
+  static constexpr int SLOTS = kTileRows * C;           // 16-byte slots per tile
+  static constexpr int PER_WAVE = SLOTS / (64 * WAVES); // wave-instructions per tile
+  static_assert(SLOTS % (64 * WAVES) == 0, "whole wave-instructions per tile");
+
+  __device__ __forceinline__ static void load(bf16* lds_tile, const bf16* g, int row0, int S,
+                                              int wave, int lane) {
+#pragma unroll
+    for (int n = 0; n < PER_WAVE; ++n) {
+      const int slot0 = (wave * PER_WAVE + n) * 64;
+      const int slot = slot0 + lane;
+      const int row = slot / C;
+      const int chunk = (slot % C) ^ swz<D>(row);
+      const int grow = min(row0 + row, S - 1);
+      __builtin_amdgcn_global_load_lds(g + (size_t)grow * D + chunk * 8, lds_tile + slot0 * 8,
+                                       16, 0, 0);
+    }
+  }
+};
+
+// s_waitcnt: vector-memory count <= N and every LDS operation done (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4 left at its maximum, lgkmcnt 11:8 = 0).
+template <int N>
+__device__ __forceinline__ void wait_vm_lds() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
 
 }  // namespace dadgpt
