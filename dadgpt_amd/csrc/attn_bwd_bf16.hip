@@ -13,9 +13,10 @@
 // tiles use the same sigma32 row permutation as the forward so that P and dS feed the next
 // MFMA as B operands from registers; the operands that must be read along the score dimension
 // (Q^T and dO^T in the dK/dV kernel, K^T in the dQ kernel) are read across the rows of the
-// row-major LDS tiles with ds_read_b64_tr_b16, so every tile is staged once, row-major. Masking is compiled only into the blocks that straddle the diagonal
-// (template DIAG), so the other blocks run branch-free. Registers stay under 256 per lane
-// (launch bound: 2 waves per SIMD) so each SIMD interleaves two waves.
+// row-major LDS tiles with ds_read_b64_tr_b16, so every tile is staged once, row-major.
+// Masking is compiled only into the blocks that straddle the diagonal (template DIAG), so the
+// other blocks run branch-free. The streamed tiles (Q and dO for dK/dV, K and V for dQ) are
+// triple-buffered in LDS through direct global->LDS loads, two tiles ahead of the compute.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "tiles.hpp"
@@ -24,6 +25,10 @@ namespace dadgpt {
 namespace {
 
 constexpr int kWaves = 4;
+#ifndef DADGPT_BWD_MINB
+#define DADGPT_BWD_MINB 2
+#endif
+constexpr int kMinBlocks = DADGPT_BWD_MINB;  // workgroups per CU the registers are sized for
 
 // ---------------------------------------------------------------- delta
 template <int D>
@@ -74,14 +79,16 @@ __device__ __forceinline__ void store_rows_bf16(bf16* dst, const f32x16 (&acc)[D
 constexpr int kKW = 32;  // keys per wave
 
 // One 32-query block (tile rows 32*qb ..) against the wave's 32 keys. Register 8j+e of lane
-// half hi holds tile query 32qb + 16j + 8hi + e.
-template <int D, bool DIAG>
+// half hi holds tile query 32qb + 16j + 8hi + e. slse holds the natural-log logsumexp of the
+// tile's queries (converted to log2 units here). MASK zeroes P for keys after the query and
+// for tile rows past S (rows_left = S - r0; those rows hold copies of row S-1).
+template <int D, bool MASK>
 __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dvacc)[D / 32],
                                            const bf16x8 (&kop)[D / 16],
                                            const bf16x8 (&vop)[D / 16], const bf16* sq,
                                            const bf16* sdo, const float* slse,
                                            const float* sdel, int qb, int key_minus_r0,
-                                           int lane, float scale_log2) {
+                                           int rows_left, int lane, float scale_log2) {
   constexpr int DS = D / 16, DB = D / 32;
   const int l32 = lane & 31, hi = lane >> 5;
   f32x16 s = f32x16{}, dp = f32x16{};
@@ -106,11 +113,11 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int e = 2 * e2 + h;
-        const float l2 = e < 4 ? la[e] : lb[e - 4];
+        const float l2 = (e < 4 ? la[e] : lb[e - 4]) * kLog2e;
         const float de = e < 4 ? da[e] : dbv[e - 4];
         float pe = fast_exp2(fmaf(s[8 * j + e], scale_log2, -l2));
-        // key > query: masked (key - r0 > tile query index)
-        if (DIAG) pe = key_minus_r0 > qt0 + e ? 0.f : pe;
+        // key > query (key - r0 > tile query index), or a row past S
+        if (MASK) pe = (key_minus_r0 > qt0 + e || qt0 + e >= rows_left) ? 0.f : pe;
         p[h] = pe;
         d[h] = pe * (dp[8 * j + e] - de);
       }
@@ -131,19 +138,27 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
   }
 }
 
+// Direct global->LDS load of the 64 fp32 row statistics (lse or delta) of one tile: lane i
+// writes row0 + i (rows past S read row S-1; the EDGE path masks them).
+__device__ __forceinline__ void dma_row_stats(float* lds, const float* g, int row0, int S,
+                                              int lane) {
+  dma_lds(g + min(row0 + lane, S - 1), lds, 4);
+}
+
 template <int D>
-__global__ __launch_bounds__(64 * kWaves, 2) void dkdv_bf16_kernel(
+__global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_bf16_kernel(
     bf16* __restrict__ dk, bf16* __restrict__ dv, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, float scale_log2,
     float scale) {
-  constexpr int NT = 64 * kWaves;
   constexpr int KB = kKW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
-  __shared__ __attribute__((aligned(16))) bf16 sq[2][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sdo[2][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) float slse[2][kTileRows];
-  __shared__ __attribute__((aligned(16))) float sdel[2][kTileRows];
+  // Q and dO tiles with their lse and delta rows, triple-buffered (constant buffer indices in
+  // the unrolled loop; see the forward kernel).
+  __shared__ __attribute__((aligned(16))) bf16 sq[3][kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 sdo[3][kTileRows * D];
+  __shared__ __attribute__((aligned(16))) float sl[3][kTileRows];
+  __shared__ __attribute__((aligned(16))) float sd[3][kTileRows];
 
   const int bh = blockIdx.x;
   const int kblk = blockIdx.y;  // key block 0 sees the most query tiles: dispatched first
@@ -177,50 +192,62 @@ __global__ __launch_bounds__(64 * kWaves, 2) void dkdv_bf16_kernel(
     dkacc[db] = f32x16{};
     dvacc[db] = f32x16{};
   }
+  // Land the operand loads before the first direct load: the compiler does not see those, so
+  // a wait it places later for these registers would also wait for every tile in flight.
+  wait_vm_lds<0>();
 
-  RowTile<D, NT> qt, dot;
-  float lse_r = 0.f, del_r = 0.f;
-  auto load_rows = [&](int row0) {
-    qt.load(qg, row0, S, tid);
-    dot.load(dog, row0, S, tid);
-    if (tid < kTileRows) {
-      const int r = row0 + tid;
-      // Padded query rows get lse = +inf so their recomputed P is exactly 0.
-      lse_r = r < S ? lseg[r] * kLog2e : __builtin_inff();
-      del_r = r < S ? delg[r] : 0.f;
+  // Direct loads per wave per tile: Q and dO, plus the lse row (wave 0) or delta row (wave 1).
+  using Dma = DmaTile<D, kWaves>;
+  constexpr int NI = 2 * Dma::PER_WAVE;
+  const bool stats_wave = wave < 2;
+  auto issue = [&](int t, bf16* nq, bf16* ndo, float* nl, float* nd) {
+    Dma::load(nq, qg, t * kTileRows, S, wave, lane);
+    Dma::load(ndo, dog, t * kTileRows, S, wave, lane);
+    if (wave == 0) dma_row_stats(nl, lseg, t * kTileRows, S, lane);
+    if (wave == 1) dma_row_stats(nd, delg, t * kTileRows, S, lane);
+  };
+  // wait until only one tile's loads (the most recent) may be outstanding, or none
+  auto wait_tiles = [&](bool one_pending) {
+    if (one_pending) {
+      if (stats_wave) wait_vm_lds<NI + 1>(); else wait_vm_lds<NI>();
+    } else {
+      wait_vm_lds<0>();
     }
   };
-  auto store_rows = [&](int st) {
-    qt.store(sq[st], tid);
-    dot.store(sdo[st], tid);
-    if (tid < kTileRows) {
-      slse[st][tid] = lse_r;
-      sdel[st][tid] = del_r;
-    }
-  };
-  load_rows(t_first * kTileRows);
-  store_rows(0);
-  __syncthreads();
+  issue(t_first, sq[0], sdo[0], sl[0], sd[0]);
+  if (t_first + 1 < t_end) issue(t_first + 1, sq[1], sdo[1], sl[1], sd[1]);
+  wait_tiles(t_first + 1 < t_end);
+  __builtin_amdgcn_s_barrier();
 
-  for (int t = t_first; t < t_end; ++t) {
-    const int st = (t - t_first) & 1;
+  // One query tile: prefetch tile t+2 (into the buffers of tile t-1, released by the last
+  // barrier), compute tile t, wait for tile t+1 and barrier.
+  auto tile = [&](int t, const bf16* cq, const bf16* cdo, const float* cl, const float* cd,
+                  bf16* nq, bf16* ndo, float* nl, float* nd) {
     const int r0 = t * kTileRows;
-    if (t + 1 < t_end) load_rows(r0 + kTileRows);
+    const bool prefetch = t + 2 < t_end;
+    if (prefetch) issue(t + 2, nq, ndo, nl, nd);
     if (kw0 < S && r0 + kTileRows - 1 >= kw0) {
+      const bool edge = r0 + kTileRows > S;
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         const int qlo = r0 + 32 * qb;  // first query of the block
         if (qlo + 31 < kw0) continue;   // every key of the wave is after every query
-        if (qlo < kw0 + kKW - 1)        // some key after some query: mask
-          dkdv_block<D, true>(dkacc, dvacc, kop, vop, sq[st], sdo[st], slse[st], sdel[st], qb,
-                              key - r0, lane, scale_log2);
+        // some key after some query, or rows past S: mask
+        if (edge || qlo < kw0 + kKW - 1)
+          dkdv_block<D, true>(dkacc, dvacc, kop, vop, cq, cdo, cl, cd, qb, key - r0, S - r0,
+                              lane, scale_log2);
         else
-          dkdv_block<D, false>(dkacc, dvacc, kop, vop, sq[st], sdo[st], slse[st], sdel[st], qb,
-                               key - r0, lane, scale_log2);
+          dkdv_block<D, false>(dkacc, dvacc, kop, vop, cq, cdo, cl, cd, qb, key - r0, S - r0,
+                               lane, scale_log2);
       }
     }
-    if (t + 1 < t_end) store_rows(st ^ 1);
-    __syncthreads();
+    wait_tiles(prefetch);
+    __builtin_amdgcn_s_barrier();
+  };
+  for (int t = t_first; t < t_end; t += 3) {
+    tile(t, sq[0], sdo[0], sl[0], sd[0], sq[2], sdo[2], sl[2], sd[2]);
+    if (t + 1 < t_end) tile(t + 1, sq[1], sdo[1], sl[1], sd[1], sq[0], sdo[0], sl[0], sd[0]);
+    if (t + 2 < t_end) tile(t + 2, sq[2], sdo[2], sl[2], sd[2], sq[1], sdo[1], sl[1], sd[1]);
   }
 
   if (key < S) {
@@ -275,15 +302,15 @@ __device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (
 }
 
 template <int D>
-__global__ __launch_bounds__(64 * kWaves, 2) void dq_bf16_kernel(
+__global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_bf16_kernel(
     bf16* __restrict__ dq, const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, const bf16* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta, int S, float scale_log2, float scale) {
-  constexpr int NT = 64 * kWaves;
   constexpr int QB = kQW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
-  __shared__ __attribute__((aligned(16))) bf16 sk[2][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sv[2][kTileRows * D];
+  // K and V tiles, triple-buffered (constant buffer indices; see the forward kernel).
+  __shared__ __attribute__((aligned(16))) bf16 sk[3][kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 sv[3][kTileRows * D];
 
   const int bh = blockIdx.x;
   const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
@@ -313,20 +340,30 @@ __global__ __launch_bounds__(64 * kWaves, 2) void dq_bf16_kernel(
   f32x16 dqacc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
+  // Land the operand loads before the first direct load (see the dK/dV kernel).
+  wait_vm_lds<0>();
 
-  RowTile<D, NT> kt, vt;
-  kt.load(kg, 0, S, tid);
-  vt.load(vg, 0, S, tid);
-  kt.store(sk[0], tid);
-  vt.store(sv[0], tid);
-  __syncthreads();
+  // Keys past S read row S-1; every chunk holding such keys is a DIAG chunk (the key is after
+  // every valid query), so they are masked.
+  using Dma = DmaTile<D, kWaves>;
+  constexpr int NI = 2 * Dma::PER_WAVE;
+  Dma::load(sk[0], kg, 0, S, wave, lane);
+  Dma::load(sv[0], vg, 0, S, wave, lane);
+  if (n_tiles > 1) {
+    Dma::load(sk[1], kg, kTileRows, S, wave, lane);
+    Dma::load(sv[1], vg, kTileRows, S, wave, lane);
+    wait_vm_lds<NI>();
+  } else {
+    wait_vm_lds<0>();
+  }
+  __builtin_amdgcn_s_barrier();
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int st = t & 1;
+  auto tile = [&](int t, const bf16* ck, const bf16* cv, bf16* nk, bf16* nv) {
     const int k0 = t * kTileRows;
-    if (t + 1 < n_tiles) {
-      kt.load(kg, k0 + kTileRows, S, tid);
-      vt.load(vg, k0 + kTileRows, S, tid);
+    const bool prefetch = t + 2 < n_tiles;
+    if (prefetch) {
+      Dma::load(nk, kg, k0 + 2 * kTileRows, S, wave, lane);
+      Dma::load(nv, vg, k0 + 2 * kTileRows, S, wave, lane);
     }
     if (q0 < S) {
 #pragma unroll
@@ -334,18 +371,23 @@ __global__ __launch_bounds__(64 * kWaves, 2) void dq_bf16_kernel(
         const int klo = k0 + 32 * kb;        // first key of the chunk
         if (klo > q0 + kQW - 1) continue;    // every key after every query of the wave
         if (klo + 31 > q0)                   // some key after some query: mask
-          dq_chunk<D, true>(dqacc, qop, doop, sk[st], sv[st], kb, qrow - k0, lse2, dlt, lane,
+          dq_chunk<D, true>(dqacc, qop, doop, ck, cv, kb, qrow - k0, lse2, dlt, lane,
                             scale_log2);
         else
-          dq_chunk<D, false>(dqacc, qop, doop, sk[st], sv[st], kb, qrow - k0, lse2, dlt, lane,
+          dq_chunk<D, false>(dqacc, qop, doop, ck, cv, kb, qrow - k0, lse2, dlt, lane,
                              scale_log2);
       }
     }
-    if (t + 1 < n_tiles) {
-      kt.store(sk[st ^ 1], tid);
-      vt.store(sv[st ^ 1], tid);
-    }
-    __syncthreads();
+    if (prefetch)
+      wait_vm_lds<NI>();
+    else
+      wait_vm_lds<0>();
+    __builtin_amdgcn_s_barrier();
+  };
+  for (int t = 0; t < n_tiles; t += 3) {
+    tile(t, sk[0], sv[0], sk[2], sv[2]);
+    if (t + 1 < n_tiles) tile(t + 1, sk[1], sv[1], sk[0], sv[0]);
+    if (t + 2 < n_tiles) tile(t + 2, sk[2], sv[2], sk[1], sv[1]);
   }
 
   if (qrow < S) store_rows_bf16<DB>(dq + base + (size_t)qrow * D, dqacc, scale, hi);

@@ -146,16 +146,12 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
   constexpr int QB = kQW * kWaves;
   constexpr int DS = D / 16;  // 16-wide K-steps along D
   constexpr int DB = D / 32;  // 32-row blocks of O^T
-  // K and V tiles, triple-buffered: tile t is read while t+1 and t+2 are in flight. Three
-  // separate arrays (not one indexed array) so that, with the tile loop unrolled by three,
-  // every LDS read names its buffer statically: the compiler then knows a pending direct
-  // load into another buffer does not alias it and inserts no wait for it.
-  __shared__ __attribute__((aligned(16))) bf16 sk0[kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sk1[kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sk2[kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sv0[kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sv1[kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sv2[kTileRows * D];
+  // K and V tiles, triple-buffered: tile t is read while t+1 and t+2 are in flight. With the
+  // tile loop unrolled by three every access names its buffer by a constant index, so the
+  // compiler addresses all three from one register and knows that a pending direct load into
+  // one buffer does not alias reads of another (it inserts no wait for it).
+  __shared__ __attribute__((aligned(16))) bf16 sk[3][kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 sv[3][kTileRows * D];
 
   const int bh = blockIdx.x;
   const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
@@ -193,13 +189,16 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
     lrun[i] = 0.f;
   }
 
+  // Land the Q loads before the first direct load: the compiler does not see those, so a
+  // wait it placed later for qop would also wait for every tile in flight.
+  wait_vm_lds<0>();
   using Dma = DmaTile<D, kWaves>;
   constexpr int NI = 2 * Dma::PER_WAVE;  // DMA instructions per wave per tile (K and V)
-  Dma::load(sk0, kg, 0, S, wave, lane);
-  Dma::load(sv0, vg, 0, S, wave, lane);
+  Dma::load(sk[0], kg, 0, S, wave, lane);
+  Dma::load(sv[0], vg, 0, S, wave, lane);
   if (n_tiles > 1) {
-    Dma::load(sk1, kg, kTileRows, S, wave, lane);
-    Dma::load(sv1, vg, kTileRows, S, wave, lane);
+    Dma::load(sk[1], kg, kTileRows, S, wave, lane);
+    Dma::load(sv[1], vg, kTileRows, S, wave, lane);
     wait_vm_lds<NI>();
   } else {
     wait_vm_lds<0>();
@@ -209,13 +208,10 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
   // One key tile: prefetch tile t+2 into (nk, nv) (it held tile t-1, released by the last
   // barrier), compute tile t from (ck, cv), then wait for tile t+1 (only tile t+2's loads may
   // still be in flight) and barrier, which also ends every wave's reads of tile t.
-  // `late` issues the prefetch after the compute instead: the first step of the unrolled loop
-  // uses it, because at the loop head the compiler cannot tell which buffer a pending direct
-  // load targets and waits for all of them before the first LDS read.
-  auto tile = [&](int t, const bf16* ck, const bf16* cv, bf16* nk, bf16* nv, bool late) {
+  auto tile = [&](int t, const bf16* ck, const bf16* cv, bf16* nk, bf16* nv) {
     const int k0 = t * kTileRows;
     const bool prefetch = t + 2 < n_tiles;
-    if (prefetch && !late) {
+    if (prefetch) {
       Dma::load(nk, kg, k0 + 2 * kTileRows, S, wave, lane);
       Dma::load(nv, vg, k0 + 2 * kTileRows, S, wave, lane);
     }
@@ -231,10 +227,6 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
           fwd_chunk<D, kNQB, false>(oacc, mrun, lrun, qop, ck, cv, kb, rel, lane, scale_log2);
       }
     }
-    if (prefetch && late) {
-      Dma::load(nk, kg, k0 + 2 * kTileRows, S, wave, lane);
-      Dma::load(nv, vg, k0 + 2 * kTileRows, S, wave, lane);
-    }
     if (prefetch)
       wait_vm_lds<NI>();
     else
@@ -242,9 +234,9 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
     __builtin_amdgcn_s_barrier();
   };
   for (int t = 0; t < n_tiles; t += 3) {
-    tile(t, sk0, sv0, sk2, sv2, true);
-    if (t + 1 < n_tiles) tile(t + 1, sk1, sv1, sk0, sv0, false);
-    if (t + 2 < n_tiles) tile(t + 2, sk2, sv2, sk1, sv1, false);
+    tile(t, sk[0], sv[0], sk[2], sv[2]);
+    if (t + 1 < n_tiles) tile(t + 1, sk[1], sv[1], sk[0], sv[0]);
+    if (t + 2 < n_tiles) tile(t + 2, sk[2], sv[2], sk[1], sv[1]);
   }
 
   // ---- epilogue: O = O^T / l, lse = ln2 * (m + log2 l) ----

@@ -103,11 +103,34 @@ struct RowTile {
 };
 
 // Direct global -> LDS staging (global_load_lds_dwordx4): lane i of a wave-instruction writes
-// its 16 bytes to LDS at (instruction base + 16*i), so the swizzle is applied on the global
-// side: the lane that fills LDS slot (row, physical chunk c) reads logical chunk
-// c ^ swz(row). No registers hold the tile and the loads complete asynchronously into LDS,
-// which lets a kernel keep tiles in flight across barriers (vmcnt counts them). Rows past S
-// read row S-1 instead (in bounds; the kernels mask every key or query past S).
+// its 16 bytes to LDS at (M0 + 16*i), so the swizzle is applied on the global side: the lane
+// that fills LDS slot (row, physical chunk c) reads logical chunk c ^ swz(row). No registers
+// hold the tile and the loads complete asynchronously into LDS, which lets a kernel keep
+// tiles in flight across barriers. Rows past S read row S-1 instead (in bounds; the kernels
+// mask every key or query past S).
+//
+// The instruction is issued from inline assembly, so the compiler does not see these loads:
+// with the builtin it inserts a wait for every pending direct load before each transposed
+// read (ds_read_b64_tr_b16 carries no alias information), which would serialise the
+// pipeline. Completion is therefore the caller's job: wait_vm_lds<N>() before the barrier
+// that publishes a tile. The compiler's own vector-memory waits stay correct because loads
+// complete in order, so unseen younger loads can only lengthen them. M0 is written here and
+// used by nothing else in these kernels.
+__device__ __forceinline__ void dma_lds(const void* gsrc, const void* lds_dst, int bytes) {
+  const uint32_t lds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst;
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds);  // wave-uniform destination
+  if (bytes == 16)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(base), "v"(gsrc)
+                 : "memory");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+                 :
+                 : "s"(base), "v"(gsrc)
+                 : "memory");
+}
+
 template <int D, int WAVES>
 struct DmaTile {
   static constexpr int C = D / 8;                       // 16-byte chunks per row
@@ -124,8 +147,7 @@ struct DmaTile {
       const int row = slot / C;
       const int chunk = (slot % C) ^ swz<D>(row);
       const int grow = min(row0 + row, S - 1);
-      __builtin_amdgcn_global_load_lds(g + (size_t)grow * D + chunk * 8, lds_tile + slot0 * 8,
-                                       16, 0, 0);
+      dma_lds(g + (size_t)grow * D + chunk * 8, lds_tile + slot0 * 8, 16);
     }
   }
 };
