@@ -58,6 +58,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-slices", type=int, default=24)
     p.add_argument("--profile-sample", action="store_true")
+    p.add_argument("--prewarm-seconds", type=float, default=2.0,
+                   help="untimed fwd+bwd steps before the warmup, so clocks have ramped")
     return p.parse_args()
 
 
@@ -221,6 +223,11 @@ def main():
         return
     stream = torch.cuda.current_stream()
 
+    t_end = time.perf_counter() + args.prewarm_seconds
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            wl.step()
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         wl.step()
     torch.cuda.synchronize()

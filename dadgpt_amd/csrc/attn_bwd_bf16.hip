@@ -25,10 +25,15 @@ namespace dadgpt {
 namespace {
 
 constexpr int kWaves = 4;
-#ifndef DADGPT_BWD_MINB
-#define DADGPT_BWD_MINB 2
+// Workgroups per CU the registers are sized for (4 waves each: 2 -> 256 VGPRs, 3 -> 168).
+#ifndef DADGPT_DKDV_MINB
+#define DADGPT_DKDV_MINB 2
 #endif
-constexpr int kMinBlocks = DADGPT_BWD_MINB;  // workgroups per CU the registers are sized for
+#ifndef DADGPT_DQ_MINB
+#define DADGPT_DQ_MINB 3
+#endif
+constexpr int kDkdvMinBlocks = DADGPT_DKDV_MINB;
+constexpr int kDqMinBlocks = DADGPT_DQ_MINB;
 
 // ---------------------------------------------------------------- delta
 template <int D>
@@ -146,7 +151,7 @@ __device__ __forceinline__ void dma_row_stats(float* lds, const float* g, int ro
 }
 
 template <int D>
-__global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_bf16_kernel(
+__global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
     bf16* __restrict__ dk, bf16* __restrict__ dv, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, float scale_log2,
@@ -302,7 +307,7 @@ __device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (
 }
 
 template <int D>
-__global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_bf16_kernel(
+__global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
     bf16* __restrict__ dq, const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, const bf16* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta, int S, float scale_log2, float scale) {

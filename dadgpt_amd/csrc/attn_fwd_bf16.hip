@@ -54,17 +54,14 @@ constexpr int kWaves = DADGPT_FWD_WAVES;  // waves per workgroup
 constexpr int kMinBlocks = DADGPT_FWD_MINB;
 constexpr float kRescale = 8.0f;          // lazy-rescale threshold, log2 units
 
-// One 32-key chunk (tile keys 32*kb ..) against the wave's NQB 32-query blocks. Register r of
-// lane half hi holds key c0 + 16*(r>>3) + 8*hi + (r&7); DIAG chunks mask keys after the query.
-template <int D, int NQB, bool DIAG>
-__device__ __forceinline__ void fwd_chunk(f32x16 (&oacc)[NQB][D / 32], float (&mrun)[NQB],
-                                          float (&lrun)[NQB], const bf16x8 (&qop)[NQB][D / 16],
-                                          const bf16* lk, const bf16* lv, int kb,
-                                          int qrow_minus_c0, int lane, float scale_log2) {
+// S^T for one 32-key chunk (tile keys 32*kb ..) against the wave's NQB 32-query blocks:
+// s[i] = K[chunk] Q_i^T. Register r of lane half hi holds key 32kb + 16*(r>>3) + 8*hi + (r&7)
+// (K rows are read through sigma32); each K operand read feeds every query block.
+template <int D, int NQB>
+__device__ __forceinline__ void fwd_scores(f32x16 (&s)[NQB], const bf16x8 (&qop)[NQB][D / 16],
+                                           const bf16* lk, int kb, int lane) {
   const int l32 = lane & 31, hi = lane >> 5;
-  constexpr int DS = D / 16, DB = D / 32;
-  // ---- S^T chunk = K[chunk] Q^T for every query block; each K operand read once ----
-  f32x16 s[NQB];
+  constexpr int DS = D / 16;
 #pragma unroll
   for (int i = 0; i < NQB; ++i) s[i] = f32x16{};
   const int krow = 32 * kb + sigma32(l32);
@@ -74,6 +71,17 @@ __device__ __forceinline__ void fwd_chunk(f32x16 (&oacc)[NQB][D / 32], float (&m
 #pragma unroll
     for (int i = 0; i < NQB; ++i) s[i] = mfma32(a, qop[i][ds], s[i]);
   }
+}
+
+// Online softmax of one chunk's scores and O^T += V^T[:, chunk] P^T. DIAG chunks mask keys
+// after the query.
+template <int D, int NQB, bool DIAG>
+__device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[NQB][D / 32],
+                                               float (&mrun)[NQB], float (&lrun)[NQB],
+                                               const bf16* lv, int kb, int qrow_minus_c0,
+                                               int lane, float scale_log2) {
+  const int hi = lane >> 5;
+  constexpr int DB = D / 32;
   // ---- online softmax, per query = per lane ----
   bf16x8 pb[NQB][2];
 #pragma unroll
@@ -123,7 +131,7 @@ __device__ __forceinline__ void fwd_chunk(f32x16 (&oacc)[NQB][D / 32], float (&m
     }
     lrun[i] = ls;
   }
-  // ---- O^T += V^T[:, chunk] P^T; each V^T operand read once for both query blocks ----
+  // ---- O^T += V^T[:, chunk] P^T; each V^T operand read once for every query block ----
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -215,16 +223,26 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
       Dma::load(nk, kg, k0 + 2 * kTileRows, S, wave, lane);
       Dma::load(nv, vg, k0 + 2 * kTileRows, S, wave, lane);
     }
-    if (q0 < S) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int c0 = k0 + 32 * kb;           // first key of the chunk
-        if (c0 > q0 + kQW - 1) continue;       // every key after every query of the wave
-        const int rel = q0 + l32 - c0;
-        if (c0 + 31 > q0)                      // some key after some query: mask
-          fwd_chunk<D, kNQB, true>(oacc, mrun, lrun, qop, ck, cv, kb, rel, lane, scale_log2);
+    // Both chunks' score MFMAs are issued before the first chunk's softmax, so the second
+    // chunk's MFMAs run while the first chunk's softmax is on the VALU.
+    if (q0 < S && k0 <= q0 + kQW - 1) {  // some key of the tile at or before a query
+      const bool live1 = k0 + 32 <= q0 + kQW - 1;  // likewise for chunk 1
+      f32x16 s0[kNQB], s1[kNQB];
+      fwd_scores<D, kNQB>(s0, qop, ck, 0, lane);
+      if (live1) fwd_scores<D, kNQB>(s1, qop, ck, 1, lane);
+      if (k0 + 31 > q0)  // some key after some query: mask
+        fwd_softmax_pv<D, kNQB, true>(s0, oacc, mrun, lrun, cv, 0, q0 + l32 - k0, lane,
+                                      scale_log2);
+      else
+        fwd_softmax_pv<D, kNQB, false>(s0, oacc, mrun, lrun, cv, 0, q0 + l32 - k0, lane,
+                                       scale_log2);
+      if (live1) {
+        if (k0 + 63 > q0)
+          fwd_softmax_pv<D, kNQB, true>(s1, oacc, mrun, lrun, cv, 1, q0 + l32 - k0 - 32, lane,
+                                        scale_log2);
         else
-          fwd_chunk<D, kNQB, false>(oacc, mrun, lrun, qop, ck, cv, kb, rel, lane, scale_log2);
+          fwd_softmax_pv<D, kNQB, false>(s1, oacc, mrun, lrun, cv, 1, q0 + l32 - k0 - 32,
+                                         lane, scale_log2);
       }
     }
     if (prefetch)
