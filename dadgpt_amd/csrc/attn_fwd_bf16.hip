@@ -54,23 +54,37 @@ constexpr int kWaves = DADGPT_FWD_WAVES;  // waves per workgroup
 constexpr int kMinBlocks = DADGPT_FWD_MINB;
 constexpr float kRescale = 8.0f;          // lazy-rescale threshold, log2 units
 
-// S^T for one 32-key chunk (tile keys 32*kb ..) against the wave's NQB 32-query blocks:
-// s[i] = K[chunk] Q_i^T. Register r of lane half hi holds key 32kb + 16*(r>>3) + 8*hi + (r&7)
-// (K rows are read through sigma32); each K operand read feeds every query block.
-template <int D, int NQB>
-__device__ __forceinline__ void fwd_scores(f32x16 (&s)[NQB], const bf16x8 (&qop)[NQB][D / 16],
-                                           const bf16* lk, int kb, int lane) {
+// K operands of one 32-key chunk (tile keys 32*kb ..): A operands of S^T = K Q^T, K rows read
+// through sigma32 so that register r of lane half hi holds key 32kb + 16*(r>>3) + 8*hi + (r&7).
+template <int D>
+__device__ __forceinline__ void fwd_k_ops(bf16x8 (&ka)[D / 16], const bf16* lk, int kb,
+                                          int lane) {
   const int l32 = lane & 31, hi = lane >> 5;
-  constexpr int DS = D / 16;
-#pragma unroll
-  for (int i = 0; i < NQB; ++i) s[i] = f32x16{};
   const int krow = 32 * kb + sigma32(l32);
 #pragma unroll
-  for (int ds = 0; ds < DS; ++ds) {
-    const bf16x8 a = lds_op(lk, rm_off<D>(krow, 2 * ds + hi));
+  for (int ds = 0; ds < D / 16; ++ds) ka[ds] = lds_op(lk, rm_off<D>(krow, 2 * ds + hi));
+}
+
+// s[i] = K[chunk] Q_i^T for the wave's NQB query blocks; each K operand feeds every block.
+template <int D, int NQB>
+__device__ __forceinline__ void fwd_scores(f32x16 (&s)[NQB], const bf16x8 (&qop)[NQB][D / 16],
+                                           const bf16x8 (&ka)[D / 16]) {
 #pragma unroll
-    for (int i = 0; i < NQB; ++i) s[i] = mfma32(a, qop[i][ds], s[i]);
-  }
+  for (int i = 0; i < NQB; ++i) s[i] = f32x16{};
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds)
+#pragma unroll
+    for (int i = 0; i < NQB; ++i) s[i] = mfma32(ka[ds], qop[i][ds], s[i]);
+}
+
+// V^T operands of one chunk (A of O^T += V^T P^T), read across the rows of the V tile.
+template <int D>
+__device__ __forceinline__ void fwd_v_ops(bf16x8 (&va)[D / 32][2], const bf16* lv, int kb,
+                                          int lane) {
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) va[db][j] = lds_tr_op<D>(lv, 32 * kb + 16 * j, 32 * db, lane);
 }
 
 // Online softmax of one chunk's scores and O^T += V^T[:, chunk] P^T. DIAG chunks mask keys
@@ -78,7 +92,7 @@ __device__ __forceinline__ void fwd_scores(f32x16 (&s)[NQB], const bf16x8 (&qop)
 template <int D, int NQB, bool DIAG>
 __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[NQB][D / 32],
                                                float (&mrun)[NQB], float (&lrun)[NQB],
-                                               const bf16* lv, int kb, int qrow_minus_c0,
+                                               const bf16x8 (&va)[D / 32][2], int qrow_minus_c0,
                                                int lane, float scale_log2) {
   const int hi = lane >> 5;
   constexpr int DB = D / 32;
@@ -133,14 +147,11 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[
   }
   // ---- O^T += V^T[:, chunk] P^T; each V^T operand read once for every query block ----
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
+  for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const bf16x8 a = lds_tr_op<D>(lv, 32 * kb + 16 * j, 32 * db, lane);
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int i = 0; i < NQB; ++i) oacc[i][db] = mfma32(a, pb[i][j], oacc[i][db]);
-    }
-  }
+      for (int i = 0; i < NQB; ++i) oacc[i][db] = mfma32(va[db][j], pb[i][j], oacc[i][db]);
 }
 
 template <int D>
@@ -223,26 +234,33 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
       Dma::load(nk, kg, k0 + 2 * kTileRows, S, wave, lane);
       Dma::load(nv, vg, k0 + 2 * kTileRows, S, wave, lane);
     }
-    // Both chunks' score MFMAs are issued before the first chunk's softmax, so the second
-    // chunk's MFMAs run while the first chunk's softmax is on the VALU.
+    // Issue order is pinned with scheduling barriers: all K operand reads, then both chunks'
+    // score MFMAs, then each chunk's V^T reads ahead of its softmax, so no MFMA waits on an
+    // LDS read issued just before it and the second chunk's MFMAs run under the first
+    // chunk's softmax.
     if (q0 < S && k0 <= q0 + kQW - 1) {  // some key of the tile at or before a query
       const bool live1 = k0 + 32 <= q0 + kQW - 1;  // likewise for chunk 1
+      bf16x8 ka0[DS], ka1[DS], va[DB][2];
       f32x16 s0[kNQB], s1[kNQB];
-      fwd_scores<D, kNQB>(s0, qop, ck, 0, lane);
-      if (live1) fwd_scores<D, kNQB>(s1, qop, ck, 1, lane);
+      fwd_k_ops<D>(ka0, ck, 0, lane);
+      if (live1) fwd_k_ops<D>(ka1, ck, 1, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      fwd_scores<D, kNQB>(s0, qop, ka0);
+      if (live1) fwd_scores<D, kNQB>(s1, qop, ka1);
+      fwd_v_ops<D>(va, cv, 0, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      const int rel0 = q0 + l32 - k0;
       if (k0 + 31 > q0)  // some key after some query: mask
-        fwd_softmax_pv<D, kNQB, true>(s0, oacc, mrun, lrun, cv, 0, q0 + l32 - k0, lane,
-                                      scale_log2);
+        fwd_softmax_pv<D, kNQB, true>(s0, oacc, mrun, lrun, va, rel0, lane, scale_log2);
       else
-        fwd_softmax_pv<D, kNQB, false>(s0, oacc, mrun, lrun, cv, 0, q0 + l32 - k0, lane,
-                                       scale_log2);
+        fwd_softmax_pv<D, kNQB, false>(s0, oacc, mrun, lrun, va, rel0, lane, scale_log2);
       if (live1) {
+        fwd_v_ops<D>(va, cv, 1, lane);
+        __builtin_amdgcn_sched_barrier(0);
         if (k0 + 63 > q0)
-          fwd_softmax_pv<D, kNQB, true>(s1, oacc, mrun, lrun, cv, 1, q0 + l32 - k0 - 32, lane,
-                                        scale_log2);
+          fwd_softmax_pv<D, kNQB, true>(s1, oacc, mrun, lrun, va, rel0 - 32, lane, scale_log2);
         else
-          fwd_softmax_pv<D, kNQB, false>(s1, oacc, mrun, lrun, cv, 1, q0 + l32 - k0 - 32,
-                                         lane, scale_log2);
+          fwd_softmax_pv<D, kNQB, false>(s1, oacc, mrun, lrun, va, rel0 - 32, lane, scale_log2);
       }
     }
     if (prefetch)
