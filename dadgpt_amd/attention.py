@@ -206,11 +206,12 @@ def decode_workspace_bytes(n_seq: int, n_heads: int, max_len: int, d_head: int) 
 
 def decode_workspace(n_seq, n_heads, max_len, d_head, device="cuda"):
     """The workspace decode_attention needs for this cache shape, or None when it needs
-    none (max_len fits one workgroup span)."""
+    none (max_len fits one workgroup chunk). It is zero-filled, as the library requires
+    before first use (its arrival counters start at zero; every call leaves them there)."""
     nbytes = decode_workspace_bytes(n_seq, n_heads, max_len, d_head)
     if nbytes == 0:
         return None
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)
 
 
 def decode_attention(out, q, k_cache, v_cache, lens, n_seq, n_heads, max_len, d_head, scale,

@@ -6,32 +6,42 @@
 // Cache layout [n_seq, H, max_len, D] (for n_seq = 1 this is the reference's per-layer
 // [H, max_len, d_head] cache, src/model.cpp:659-675); only the first lens[s] rows are read.
 //
-// One workgroup of 16 waves covers a span of 16*KW keys of one (sequence, head): wave w owns
-// keys [span0 + w*KW, span0 + (w+1)*KW). Every 16-byte load instruction of a wave covers whole
-// key rows (for bf16 D=64: 8 lanes x 16 B per row, 8 rows per instruction, a contiguous 1 KiB),
-// and all K and V loads of a wave are issued before any arithmetic, so a workgroup keeps its
-// whole span in flight. The 16 waves merge (max, sum, o) in LDS with the logsumexp rule.
+// Work split. A cache (one sequence and head) is cut into chunks of C = 8*KW keys, one 8-wave
+// workgroup per chunk; wave w owns keys [chunk*C + w*KW, chunk*C + (w+1)*KW). Every 16-byte
+// load instruction of a wave covers whole key rows (bf16 D=64: 8 lanes x 16 B per row, 8 rows
+// per instruction, a contiguous 1 KiB), all K and V loads of a wave are issued before any
+// arithmetic, and they carry the non-temporal hint (the cache is streamed once). The 8 waves
+// merge (max, sum, o) in LDS with the logsumexp rule. Chunks are small enough that the work
+// of a long cache spreads over several CUs: one CU streaming a whole 1024-key cache alone was
+// the tail of the launch.
 //
-// Spans are 1024 keys (bf16) or 512 keys (fp32). When max_len fits one span, the workgroup
-// writes the output directly: one kernel, no workspace, no inter-workgroup communication. A
-// longer cache splits into n_split spans: each workgroup writes an fp32 partial
-// (max, sum, unnormalised o) and a second kernel merges them. The kernel boundary orders the
-// two; no device-scope fence is used (on this part an agent-scope release writes back the
-// whole L2, because the L2s of the 8 XCDs are not coherent with each other).
+// The grid runs over caches fastest, so consecutive workgroups (dealt round-robin to the 8
+// XCDs) hold the same chunk index of different caches, and the chunks past a short cache's
+// length (which exit at once) do not pile up on one XCD.
+//
+// A cache that fits one chunk is written directly. A longer one merges inside the same kernel:
+// each chunk publishes an fp32 partial (max in log2 units, sum, unnormalised o) and counts
+// itself on a per-cache counter; the chunk that arrives last merges all partials, writes the
+// output and rearms the counter to zero. The partials and the counter move only through
+// agent-scope relaxed accesses (stores, loads and the atomic with the device-scope cache bit),
+// each coherent across the XCDs on its own, and the stores are complete (s_waitcnt vmcnt(0))
+// before the counter is incremented. No agent-scope fence is used: on this part a release
+// fence writes back the whole L2 (the L2s of the 8 XCDs are not coherent with each other),
+// which made the first fence-based version of this kernel 17x slower.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace dadgpt {
 namespace {
 
-constexpr int kWaves = 16;
+constexpr int kWaves = 8;         // waves per workgroup (one chunk)
+constexpr int kLoadsPerWave = 8;  // 16-byte loads per lane and tensor
 
 template <typename T>
 struct Elem;
 template <>
 struct Elem<bf16> {
   static constexpr int kPer16B = 8;
-  static constexpr int kKeysPerWave = 64;
   static __device__ __forceinline__ void unpack(const u32x4& w, float* f) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -44,7 +54,6 @@ struct Elem<bf16> {
 template <>
 struct Elem<float> {
   static constexpr int kPer16B = 4;
-  static constexpr int kKeysPerWave = 32;
   static __device__ __forceinline__ void unpack(const u32x4& w, float* f) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(w[i]);
@@ -52,37 +61,68 @@ struct Elem<float> {
   static __device__ __forceinline__ float from(float x) { return x; }
 };
 
-template <typename T>
-constexpr int span_keys() {
-  return kWaves * Elem<T>::kKeysPerWave;
+// Keys per wave: kLoadsPerWave wave-wide loads of 64 x 16 B, each covering whole key rows.
+// bf16: 64 keys (D=64) or 128 (D=32); fp32: 32 or 64.
+template <typename T, int D>
+__host__ __device__ constexpr int keys_per_wave() {
+  return kLoadsPerWave * 64 / (D / Elem<T>::kPer16B);
+}
+template <typename T, int D>
+__host__ __device__ constexpr int chunk_keys() {
+  return kWaves * keys_per_wave<T, D>();
 }
 
 __device__ __forceinline__ int clamp_len(int L, int max_len) {
   return L < 0 ? 0 : (L > max_len ? max_len : L);
 }
 
-// part: [n_seq*H][n_split][D+2] fp32 (max in log2 units, sum, o[D]); used when n_split > 1.
+// Cache rows are read once: non-temporal loads.
+__device__ __forceinline__ u32x4 ld_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// Agent-scope relaxed accesses: each is coherent across the XCDs by itself.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Workspace of a split decode: fp32 partials [n_seq*H][n_chunk][D+2], then (256-byte
+// aligned) one arrival counter per (sequence, head).
+size_t counter_offset(int n_seq, int H, int n_chunk, int D) {
+  const size_t part = sizeof(float) * (size_t)n_seq * H * n_chunk * (D + 2);
+  return (part + 255) & ~(size_t)255;
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
     T* __restrict__ out, const T* __restrict__ q, const T* __restrict__ kc,
     const T* __restrict__ vc, const int* __restrict__ lens, int H, int max_len,
-    float scale_log2, float* __restrict__ part, int n_split) {
+    float scale_log2, float* __restrict__ part, unsigned* __restrict__ counter, int n_chunk) {
   constexpr int EPL = Elem<T>::kPer16B;       // elements per 16-byte load
-  constexpr int KW = Elem<T>::kKeysPerWave;   // keys per wave
+  constexpr int KW = keys_per_wave<T, D>();   // keys per wave
+  constexpr int C = chunk_keys<T, D>();       // keys per workgroup
   constexpr int LPR = D / EPL;                // lanes per key row
   constexpr int KPL = 64 / LPR;               // key rows per wave-wide load
-  constexpr int NLD = KW / KPL;               // loads per wave, per tensor
+  constexpr int NLD = kLoadsPerWave;          // loads per wave, per tensor
   __shared__ float sm_o[kWaves][D];
   __shared__ float sm_m[kWaves], sm_l[kWaves];
+  __shared__ int sm_last;
 
-  const int seq = blockIdx.z, head = blockIdx.y, split = blockIdx.x;
+  const int seq = blockIdx.x / H, head = blockIdx.x % H, chunk = blockIdx.y;
   const int L = clamp_len(lens[seq], max_len);
+  const int nch = (L + C - 1) / C;
+  // Chunks past the length do nothing; chunk 0 of an empty cache still writes the zero output.
+  if (chunk >= (nch > 1 ? nch : 1)) return;
+
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sub = lane % LPR, grp = lane / LPR;
   const size_t hrow = (size_t)seq * H + head;
   const T* kh = kc + hrow * max_len * D + sub * EPL;
   const T* vh = vc + hrow * max_len * D + sub * EPL;
-  const int key0 = split * span_keys<T>() + wave * KW;
+  const int key0 = chunk * C + wave * KW;
 
   float mx = neg_inf(), lsum = 0.f;
   float o[EPL];
@@ -96,12 +136,12 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int key = min(key0 + i * KPL + grp, L - 1);
-      kr[i] = ld_g128u(kh + (size_t)key * D);
+      kr[i] = ld_stream(kh + (size_t)key * D);
     }
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int key = min(key0 + i * KPL + grp, L - 1);
-      vr[i] = ld_g128u(vh + (size_t)key * D);
+      vr[i] = ld_stream(vh + (size_t)key * D);
     }
     float qf[EPL];
     Elem<T>::unpack(ld_g128u(q + hrow * D + sub * EPL), qf);
@@ -153,8 +193,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
   __syncthreads();
 
   // merge the waves (threads 0..D-1 own one output column each)
+  float wm = neg_inf(), wl = 0.f, wo = 0.f;
   if (tid < D) {
-    float wm = neg_inf(), wl = 0.f, wo = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) wm = fmaxf(wm, sm_m[w]);
 #pragma unroll
@@ -163,57 +203,70 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
       wl += sm_l[w] * f;
       wo += sm_o[w][tid] * f;
     }
-    if (n_split == 1) {
-      out[hrow * D + tid] = Elem<T>::from(wl > 0.f ? wo / wl : 0.f);
-    } else {
-      float* my = part + (hrow * n_split + split) * (D + 2);
-      my[2 + tid] = wo;
-      if (tid == 0) {
-        my[0] = wm;
-        my[1] = wl;
-      }
+  }
+  if (nch <= 1) {  // the whole cache is this chunk
+    if (tid < D) out[hrow * D + tid] = Elem<T>::from(wl > 0.f ? wo / wl : 0.f);
+    return;
+  }
+
+  // Split cache: publish this chunk's partial; the last chunk to arrive merges all of them.
+  float* ph = part + hrow * n_chunk * (D + 2);
+  if (tid < D) {
+    float* my = ph + chunk * (D + 2);
+    st_agent(my + 2 + tid, wo);
+    if (tid == 0) {
+      st_agent(my, wm);
+      st_agent(my + 1, wl);
     }
   }
-}
-
-// One wave per (sequence, head): logsumexp merge of the n_split partials.
-template <typename T, int D>
-__global__ __launch_bounds__(256) void decode_merge_kernel(T* __restrict__ out,
-                                                           const float* __restrict__ part,
-                                                           int rows, int n_split) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  const float* ph = part + (size_t)row * n_split * (D + 2);
-  float gm = neg_inf();
-  for (int w = 0; w < n_split; ++w) gm = fmaxf(gm, ph[w * (D + 2)]);
-  float gl = 0.f, go = 0.f;
-  for (int w = 0; w < n_split; ++w) {
-    const float* pw = ph + w * (D + 2);
-    const float f = pw[0] == neg_inf() ? 0.f : fast_exp2(pw[0] - gm);
-    gl += pw[1] * f;
-    if (lane < D) go += pw[2 + lane] * f;
+  // This thread's stores are complete at the device coherence point (the asm is also a
+  // compiler barrier for them); the barrier then covers the whole workgroup's.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned before = __hip_atomic_fetch_add(counter + hrow, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    sm_last = before == (unsigned)(nch - 1);
   }
-  if (lane < D) out[(size_t)row * D + lane] = Elem<T>::from(gl > 0.f ? go / gl : 0.f);
+  __syncthreads();
+  if (!sm_last) return;
+
+  if (tid < D) {
+    float gm = neg_inf();
+    for (int c = 0; c < nch; ++c) gm = fmaxf(gm, ld_agent(ph + c * (D + 2)));
+    float gl = 0.f, go = 0.f;
+    for (int c = 0; c < nch; ++c) {  // every chunk < nch holds a valid key: finite max
+      const float* pc = ph + c * (D + 2);
+      const float f = fast_exp2(ld_agent(pc) - gm);
+      gl += ld_agent(pc + 1) * f;
+      go += ld_agent(pc + 2 + tid) * f;
+    }
+    out[hrow * D + tid] = Elem<T>::from(go / gl);
+  }
+  // All nch arrivals of this call are in: rearm the counter for the next call.
+  if (tid == 0)
+    __hip_atomic_store(counter + hrow, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <typename T>
-int n_split_for(int max_len) {
-  return (max_len + span_keys<T>() - 1) / span_keys<T>();
+template <typename T, int D>
+int n_chunk_for(int max_len) {
+  return (max_len + chunk_keys<T, D>() - 1) / chunk_keys<T, D>();
 }
 
 template <typename T, int D>
 hipError_t launch_decode_d(T* out, const T* q, const T* kc, const T* vc, const int* lens,
                            int n_seq, int H, int max_len, float scale, void* workspace,
                            hipStream_t stream) {
-  const int ns = n_split_for<T>(max_len);
-  float* part = static_cast<float*>(workspace);
-  decode_kernel<T, D><<<dim3(ns, H, n_seq), 64 * kWaves, 0, stream>>>(
-      out, q, kc, vc, lens, H, max_len, scale * kLog2e, part, ns);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || ns == 1) return e;
-  const int rows = n_seq * H;
-  decode_merge_kernel<T, D><<<(rows + 3) / 4, 256, 0, stream>>>(out, part, rows, ns);
+  const int nc = n_chunk_for<T, D>(max_len);
+  float* part = nullptr;
+  unsigned* counter = nullptr;
+  if (nc > 1) {
+    part = static_cast<float*>(workspace);
+    counter = reinterpret_cast<unsigned*>(static_cast<char*>(workspace) +
+                                          counter_offset(n_seq, H, nc, D));
+  }
+  decode_kernel<T, D><<<dim3(n_seq * H, nc), 64 * kWaves, 0, stream>>>(
+      out, q, kc, vc, lens, H, max_len, scale * kLog2e, part, counter, nc);
   return hipGetLastError();
 }
 
@@ -233,11 +286,11 @@ hipError_t launch_decode_t(T* out, const T* q, const T* kc, const T* vc, const i
 }  // namespace
 
 size_t decode_workspace_bytes(int n_seq, int H, int max_len, int D) {
-  // fp32 spans are shorter, so the fp32 split count bounds the bf16 one: the size returned
+  // fp32 chunks are shorter, so the fp32 chunk count bounds the bf16 one: the size returned
   // serves both element types.
-  const int ns = n_split_for<float>(max_len);
-  if (ns == 1) return 0;
-  return sizeof(float) * (size_t)n_seq * H * ns * (D + 2);
+  const int nc = D == 64 ? n_chunk_for<float, 64>(max_len) : n_chunk_for<float, 32>(max_len);
+  if (nc == 1) return 0;
+  return counter_offset(n_seq, H, nc, D) + sizeof(unsigned) * (size_t)n_seq * H;
 }
 
 hipError_t launch_decode_bf16(bf16* out, const bf16* q, const bf16* k_cache,

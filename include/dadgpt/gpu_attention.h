@@ -104,10 +104,13 @@ int dadgpt_flash_attention_backward_bf16_phase(int phase, uint16_t* dq, uint16_t
                                                int S, int d_head, float scale, void* stream);
 
 /* Bytes of decode workspace for a cache shape, valid for both element types. It is 0 when
- * max_len fits one workgroup span (512 keys fp32, 1024 keys bf16): then no workspace is
- * needed and NULL may be passed. Longer caches are split into spans whose fp32 partials go to
- * the workspace and are merged by a second kernel. The workspace needs no initialisation;
- * calls that share a workspace must not overlap in time. */
+ * max_len fits one workgroup chunk (256 keys fp32 and 512 bf16 at d_head 64; 512 and 1024 at
+ * d_head 32): then no workspace is needed and NULL may be passed. Longer caches are split
+ * into chunks whose fp32 partials and per-(sequence, head) arrival counters live in the
+ * workspace; the last chunk of each cache merges them inside the same kernel.
+ * The workspace must be ZERO-FILLED before its first use (hipMemset once, at allocation);
+ * every call leaves the counters at zero again. Calls that share a workspace must not overlap
+ * in time. */
 size_t dadgpt_decode_workspace_bytes(int n_seq, int n_heads, int max_len, int d_head);
 
 /* KV-cache decode attention (replaces the per-head composition in src/model.cpp:758-790:

@@ -92,14 +92,20 @@ def test_backward_phase_validation():
 
 
 def expected_ws(n, h, max_len, d):
-    """fp32 partials (max, sum, o[d]) per 512-key span when the cache needs more than one
-    span (fp32 spans are 512 keys, bf16 spans 1024: the fp32 count serves both)."""
-    spans = (max_len + 511) // 512
-    return 0 if spans == 1 else 4 * n * h * spans * (d + 2)
+    """fp32 partials (max, sum, o[d]) per chunk, padded to 256 bytes, then one uint32 arrival
+    counter per (sequence, head), when the cache needs more than one chunk. fp32 chunks (256
+    keys at d=64, 512 at d=32) are the shorter ones, so their count serves both types."""
+    chunk = 256 if d == 64 else 512
+    n_chunk = (max_len + chunk - 1) // chunk
+    if n_chunk == 1:
+        return 0
+    part = 4 * n * h * n_chunk * (d + 2)
+    return (part + 255) // 256 * 256 + 4 * n * h
 
 
 @pytest.mark.parametrize("n,h,L,d", [(32, 12, 1024, 64), (1, 1, 1, 32), (3, 5, 257, 64),
-                                     (2, 3, 512, 64), (2, 3, 513, 32), (4, 12, 4096, 64)])
+                                     (2, 3, 256, 64), (2, 3, 512, 32), (2, 3, 513, 32),
+                                     (4, 12, 4096, 64)])
 def test_decode_workspace_bytes(n, h, L, d):
     assert A.decode_workspace_bytes(n, h, L, d) == expected_ws(n, h, L, d)
 

@@ -350,9 +350,9 @@ def test_decode_length_clamping(gpu):
 
 @pytest.mark.parametrize("dtype,L", [(torch.bfloat16, 2500), (torch.float32, 1300)])
 def test_decode_split_spans(gpu, dtype, L):
-    """Caches longer than one workgroup span go through the partial + merge kernels."""
+    """Caches longer than one workgroup chunk publish partials that the last chunk merges."""
     n, H, D = 5, 3, 64
-    case(f"decode split spans {dtype} max_len={L}")
+    case(f"decode split chunks {dtype} max_len={L}")
     bf = dtype == torch.bfloat16
     qn, kc, vc, lens = synth.decode_inputs(n, H, L, D, seed=105, bf16=bf)
     lens[:4] = [L, 1, 1024, 1025]
@@ -364,6 +364,32 @@ def test_decode_split_spans(gpu, dtype, L):
     assert torch.equal(out, out2)
     assert max_abs(host(out), oracle.decode(qn, kc, vc, lens, 0.125)) <= (TOL_DEC if bf else
                                                                           TOL_F32)
+
+
+def ws_counters(ws, n, H, L, D):
+    """The arrival counters at the end of a decode workspace (n*H uint32)."""
+    return ws[ws.numel() - 4 * n * H:].view(torch.int32)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float32, 64),
+                                     (torch.bfloat16, 32)])
+def test_decode_workspace_reuse(gpu, dtype, D):
+    """One workspace across calls with changing lengths: every call matches the oracle and
+    leaves the arrival counters at zero (the last chunk of each cache rearms its counter)."""
+    n, H, L = 6, 4, 3000
+    case(f"decode workspace reuse {dtype} D={D}")
+    bf = dtype == torch.bfloat16
+    qn, kc, vc, _ = synth.decode_inputs(n, H, L, D, seed=106 + D, bf16=bf)
+    ws = A.decode_workspace(n, H, L, D)
+    rng = np.random.default_rng(7)
+    tol = TOL_DEC if bf else TOL_F32
+    for it in range(6):
+        lens = rng.integers(0, L + 1, n).astype(np.int32)
+        lens[it % n] = L  # always one cache of every chunk
+        out, _ = run_decode(qn, kc, vc, lens, 0.125, dtype, ws=ws)
+        torch.cuda.synchronize()
+        assert max_abs(host(out), oracle.decode(qn, kc, vc, lens, 0.125)) <= tol, f"call {it}"
+        assert int(ws_counters(ws, n, H, L, D).abs().sum()) == 0, f"counters after call {it}"
 
 
 def test_decode_matches_forward_rows(gpu):
