@@ -206,7 +206,7 @@ int dadgpt_decode_attention_bf16(uint16_t* out, const uint16_t* q, const uint16_
     return st;
   return from_hip(dadgpt::launch_decode_bf16(B(out), B(q), B(k_cache), B(v_cache), lens, n_seq,
                                              n_heads, max_len, d_head, scale, workspace,
-                                             as_stream(stream)),
+                                             workspace_bytes, as_stream(stream)),
                   fn);
 }
 
@@ -219,7 +219,7 @@ int dadgpt_decode_attention_f32(float* out, const float* q, const float* k_cache
                             workspace_bytes, {out, q, k_cache, v_cache, lens}))
     return st;
   return from_hip(dadgpt::launch_decode_f32(out, q, k_cache, v_cache, lens, n_seq, n_heads,
-                                            max_len, d_head, scale, workspace,
+                                            max_len, d_head, scale, workspace, workspace_bytes,
                                             as_stream(stream)),
                   fn);
 }

@@ -89,11 +89,16 @@ __device__ __forceinline__ float ld_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Workspace of a split decode: fp32 partials [n_seq*H][n_chunk][D+2], then (256-byte
-// aligned) one arrival counter per (sequence, head).
-size_t counter_offset(int n_seq, int H, int n_chunk, int D) {
-  const size_t part = sizeof(float) * (size_t)n_seq * H * n_chunk * (D + 2);
-  return (part + 255) & ~(size_t)255;
+// Workspace of a split decode: one uint32 arrival counter per (sequence, head) from the start
+// (the region rounded up to 256 bytes), and the fp32 partials [n_seq*H][n_chunk][D+2] packed
+// against the END of the caller's buffer. A buffer sized for the largest shape it serves thus
+// never has a later call's partials over any counter of a call of another shape, and the
+// counters, rearmed by every call, stay zero between calls.
+size_t counter_bytes(int n_seq, int H) {
+  return (sizeof(unsigned) * (size_t)n_seq * H + 255) & ~(size_t)255;
+}
+size_t partial_bytes(int n_seq, int H, int n_chunk, int D) {
+  return sizeof(float) * (size_t)n_seq * H * n_chunk * (D + 2);
 }
 
 template <typename T, int D>
@@ -256,14 +261,15 @@ int n_chunk_for(int max_len) {
 template <typename T, int D>
 hipError_t launch_decode_d(T* out, const T* q, const T* kc, const T* vc, const int* lens,
                            int n_seq, int H, int max_len, float scale, void* workspace,
-                           hipStream_t stream) {
+                           size_t workspace_bytes, hipStream_t stream) {
   const int nc = n_chunk_for<T, D>(max_len);
   float* part = nullptr;
   unsigned* counter = nullptr;
   if (nc > 1) {
-    part = static_cast<float*>(workspace);
-    counter = reinterpret_cast<unsigned*>(static_cast<char*>(workspace) +
-                                          counter_offset(n_seq, H, nc, D));
+    // the caller checked workspace_bytes >= decode_workspace_bytes(), which bounds both regions
+    const size_t at = (workspace_bytes - partial_bytes(n_seq, H, nc, D)) & ~(size_t)15;
+    counter = static_cast<unsigned*>(workspace);
+    part = reinterpret_cast<float*>(static_cast<char*>(workspace) + at);
   }
   decode_kernel<T, D><<<dim3(n_seq * H, nc), 64 * kWaves, 0, stream>>>(
       out, q, kc, vc, lens, H, max_len, scale * kLog2e, part, counter, nc);
@@ -273,13 +279,13 @@ hipError_t launch_decode_d(T* out, const T* q, const T* kc, const T* vc, const i
 template <typename T>
 hipError_t launch_decode_t(T* out, const T* q, const T* kc, const T* vc, const int* lens,
                            int n_seq, int H, int max_len, int D, float scale, void* workspace,
-                           hipStream_t stream) {
+                           size_t workspace_bytes, hipStream_t stream) {
   if (D == 64)
     return launch_decode_d<T, 64>(out, q, kc, vc, lens, n_seq, H, max_len, scale, workspace,
-                                  stream);
+                                  workspace_bytes, stream);
   if (D == 32)
     return launch_decode_d<T, 32>(out, q, kc, vc, lens, n_seq, H, max_len, scale, workspace,
-                                  stream);
+                                  workspace_bytes, stream);
   return hipErrorInvalidValue;
 }
 
@@ -290,23 +296,23 @@ size_t decode_workspace_bytes(int n_seq, int H, int max_len, int D) {
   // serves both element types.
   const int nc = D == 64 ? n_chunk_for<float, 64>(max_len) : n_chunk_for<float, 32>(max_len);
   if (nc == 1) return 0;
-  return counter_offset(n_seq, H, nc, D) + sizeof(unsigned) * (size_t)n_seq * H;
+  return counter_bytes(n_seq, H) + partial_bytes(n_seq, H, nc, D);
 }
 
 hipError_t launch_decode_bf16(bf16* out, const bf16* q, const bf16* k_cache,
                               const bf16* v_cache, const int* lens, int n_seq, int H,
                               int max_len, int D, float scale, void* workspace,
-                              hipStream_t stream) {
+                              size_t workspace_bytes, hipStream_t stream) {
   return launch_decode_t<bf16>(out, q, k_cache, v_cache, lens, n_seq, H, max_len, D, scale,
-                               workspace, stream);
+                               workspace, workspace_bytes, stream);
 }
 
 hipError_t launch_decode_f32(float* out, const float* q, const float* k_cache,
                              const float* v_cache, const int* lens, int n_seq, int H,
                              int max_len, int D, float scale, void* workspace,
-                             hipStream_t stream) {
+                             size_t workspace_bytes, hipStream_t stream) {
   return launch_decode_t<float>(out, q, k_cache, v_cache, lens, n_seq, H, max_len, D, scale,
-                                workspace, stream);
+                                workspace, workspace_bytes, stream);
 }
 
 }  // namespace dadgpt

@@ -32,17 +32,18 @@ hipError_t launch_bwd_f32(float* dq, float* dk, float* dv, float* delta, const f
                           const float* v, int BH, int S, int D, float scale,
                           hipStream_t stream);
 
-// Decode over ragged KV caches [n_seq,H,max_len,D]. A cache longer than one workgroup span
-// (1024 keys bf16, 512 fp32) is split into spans whose fp32 partials go to the workspace and
-// are merged by a second kernel; decode_workspace_bytes is 0 when no split is needed.
+// Decode over ragged KV caches [n_seq,H,max_len,D]. A cache longer than one workgroup chunk
+// (512 keys bf16, 256 fp32 at D=64) is split into chunks merged inside the kernel through the
+// workspace: arrival counters at its start, fp32 partials packed against its end (its full
+// size, workspace_bytes, places them). decode_workspace_bytes is 0 when no split is needed.
 size_t decode_workspace_bytes(int n_seq, int H, int max_len, int D);
 hipError_t launch_decode_bf16(bf16* out, const bf16* q, const bf16* k_cache,
                               const bf16* v_cache, const int* lens, int n_seq, int H,
                               int max_len, int D, float scale, void* workspace,
-                              hipStream_t stream);
+                              size_t workspace_bytes, hipStream_t stream);
 hipError_t launch_decode_f32(float* out, const float* q, const float* k_cache,
                              const float* v_cache, const int* lens, int n_seq, int H,
                              int max_len, int D, float scale, void* workspace,
-                             hipStream_t stream);
+                             size_t workspace_bytes, hipStream_t stream);
 
 }  // namespace dadgpt

@@ -106,11 +106,12 @@ int dadgpt_flash_attention_backward_bf16_phase(int phase, uint16_t* dq, uint16_t
 /* Bytes of decode workspace for a cache shape, valid for both element types. It is 0 when
  * max_len fits one workgroup chunk (256 keys fp32 and 512 bf16 at d_head 64; 512 and 1024 at
  * d_head 32): then no workspace is needed and NULL may be passed. Longer caches are split
- * into chunks whose fp32 partials and per-(sequence, head) arrival counters live in the
- * workspace; the last chunk of each cache merges them inside the same kernel.
- * The workspace must be ZERO-FILLED before its first use (hipMemset once, at allocation);
- * every call leaves the counters at zero again. Calls that share a workspace must not overlap
- * in time. */
+ * into chunks merged inside the same kernel by the last chunk of each cache, through the
+ * workspace: per-(sequence, head) arrival counters at its start, fp32 partials packed against
+ * its end. Contract: size it for the largest (n_seq, n_heads, max_len, d_head) it will serve,
+ * ZERO-FILL it once (hipMemset at allocation), and pass its full size as workspace_bytes on
+ * every call; each call leaves the counters at zero again, so calls of any shape up to the
+ * sizing one can share it. Calls that share a workspace must not overlap in time. */
 size_t dadgpt_decode_workspace_bytes(int n_seq, int n_heads, int max_len, int d_head);
 
 /* KV-cache decode attention (replaces the per-head composition in src/model.cpp:758-790:

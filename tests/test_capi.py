@@ -92,15 +92,15 @@ def test_backward_phase_validation():
 
 
 def expected_ws(n, h, max_len, d):
-    """fp32 partials (max, sum, o[d]) per chunk, padded to 256 bytes, then one uint32 arrival
-    counter per (sequence, head), when the cache needs more than one chunk. fp32 chunks (256
-    keys at d=64, 512 at d=32) are the shorter ones, so their count serves both types."""
+    """One uint32 arrival counter per (sequence, head), the region padded to 256 bytes, then
+    fp32 partials (max, sum, o[d]) per chunk, when the cache needs more than one chunk. fp32
+    chunks (256 keys at d=64, 512 at d=32) are the shorter ones, so their count serves both
+    element types."""
     chunk = 256 if d == 64 else 512
     n_chunk = (max_len + chunk - 1) // chunk
     if n_chunk == 1:
         return 0
-    part = 4 * n * h * n_chunk * (d + 2)
-    return (part + 255) // 256 * 256 + 4 * n * h
+    return (4 * n * h + 255) // 256 * 256 + 4 * n * h * n_chunk * (d + 2)
 
 
 @pytest.mark.parametrize("n,h,L,d", [(32, 12, 1024, 64), (1, 1, 1, 32), (3, 5, 257, 64),

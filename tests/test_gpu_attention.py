@@ -366,16 +366,17 @@ def test_decode_split_spans(gpu, dtype, L):
                                                                           TOL_F32)
 
 
-def ws_counters(ws, n, H, L, D):
-    """The arrival counters at the end of a decode workspace (n*H uint32)."""
-    return ws[ws.numel() - 4 * n * H:].view(torch.int32)
+def ws_counters(ws, n, H):
+    """The arrival counters at the start of a decode workspace (n*H uint32)."""
+    return ws[:4 * n * H].view(torch.int32)
 
 
 @pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float32, 64),
                                      (torch.bfloat16, 32)])
 def test_decode_workspace_reuse(gpu, dtype, D):
-    """One workspace across calls with changing lengths: every call matches the oracle and
-    leaves the arrival counters at zero (the last chunk of each cache rearms its counter)."""
+    """One workspace (sized for 6 sequences) across calls with changing lengths and changing
+    sequence counts: every call matches the oracle and leaves the arrival counters at zero
+    (the last chunk of each cache rearms its counter; partials never land on counters)."""
     n, H, L = 6, 4, 3000
     case(f"decode workspace reuse {dtype} D={D}")
     bf = dtype == torch.bfloat16
@@ -383,13 +384,14 @@ def test_decode_workspace_reuse(gpu, dtype, D):
     ws = A.decode_workspace(n, H, L, D)
     rng = np.random.default_rng(7)
     tol = TOL_DEC if bf else TOL_F32
-    for it in range(6):
-        lens = rng.integers(0, L + 1, n).astype(np.int32)
-        lens[it % n] = L  # always one cache of every chunk
-        out, _ = run_decode(qn, kc, vc, lens, 0.125, dtype, ws=ws)
+    for it, m in enumerate([6, 2, 6, 3, 1, 6]):
+        lens = rng.integers(0, L + 1, m).astype(np.int32)
+        lens[it % m] = L  # always one cache of every chunk
+        out, _ = run_decode(qn[:m], kc[:m], vc[:m], lens, 0.125, dtype, ws=ws)
         torch.cuda.synchronize()
-        assert max_abs(host(out), oracle.decode(qn, kc, vc, lens, 0.125)) <= tol, f"call {it}"
-        assert int(ws_counters(ws, n, H, L, D).abs().sum()) == 0, f"counters after call {it}"
+        ref = oracle.decode(qn[:m], kc[:m], vc[:m], lens, 0.125)
+        assert max_abs(host(out), ref) <= tol, f"call {it} (n_seq {m})"
+        assert int(ws_counters(ws, n, H).abs().sum()) == 0, f"counters after call {it}"
 
 
 def test_decode_matches_forward_rows(gpu):
