@@ -1,0 +1,76 @@
+// Internal interface of libdadgpt_gen: error reporting, the GEMM entry point and the launch
+// functions of the model's elementwise kernels (gpt2_ops.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+struct dadgpt_blas;
+
+namespace dadgpt::gen {
+
+typedef __bf16 bf16;
+
+// Records a printf-style message as this thread's last error and returns `status`.
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// DADGPT_OK, or DADGPT_ERR_HIP with the HIP error's name recorded.
+int check_hip(hipError_t e, const char* what);
+
+// Row-major out[M,N] (fp32) = a[M,K] x b[K,N] (or x b[N,K]^T when trans_b); bf16 operands.
+int gemm(dadgpt_blas* h, float* out, const bf16* a, const bf16* b, int M, int K, int N,
+         bool trans_b, hipStream_t stream);
+
+// ---- kernels (gpt2_ops.hip); every launcher returns hipGetLastError() ----
+
+// p[i] = bf16(std * N(0,1)) from a counter-based splitmix64/Box-Muller stream of `seed`.
+hipError_t init_normal(bf16* p, size_t n, uint64_t seed, float stddev, hipStream_t s);
+hipError_t fill(bf16* p, size_t n, float value, hipStream_t s);
+
+// Rows r = b*S + s of x [n*S, d] fp32 = wte[tok[r]] + wpe[pos0[b] + s].
+hipError_t embed(float* x, const int* tok, const int* pos0, const bf16* wte, const bf16* wpe,
+                 int n, int S, int d, hipStream_t s);
+
+// out[r] = bf16(LayerNorm(x[r]) * w + b), eps 1e-5 (two-pass mean and variance, fp32).
+hipError_t layernorm(bf16* out, const float* x, const bf16* w, const bf16* b, int rows, int d,
+                     hipStream_t s);
+
+// qkv [n*S, 3d] fp32 (+ bias bqkv [3d] fp32): q -> qh [n*H, S, dh]; k, v -> kh, vh
+// [n*H, S, dh] when kh is not null; k, v of the rows s < nvalid[b] -> caches
+// [n_cap, H, max_len, dh] at position pos0[b] + s. T is bf16 or float.
+template <typename T>
+hipError_t qkv_split(T* qh, T* kh, T* vh, T* kcache, T* vcache, const float* qkv,
+                     const float* bqkv, const int* pos0, const int* nvalid, int n, int S, int H,
+                     int dh, int max_len, hipStream_t s);
+
+// out [n*S, d] bf16 <- heads [n*H, S, dh] (T).
+template <typename T>
+hipError_t merge_heads(bf16* out, const T* heads, int n, int S, int H, int dh, hipStream_t s);
+
+// out[i] = bf16(in[i]).
+hipError_t to_bf16(bf16* out, const float* in, size_t count, hipStream_t s);
+
+// x[r, c] += y[r, c] + bias[c] (fp32 x and y, bf16 bias).
+hipError_t bias_residual(float* x, const float* y, const bf16* bias, int rows, int cols,
+                         hipStream_t s);
+
+// out[r, c] = bf16(gelu_tanh(y[r, c] + bias[c])).
+hipError_t bias_gelu(bf16* out, const float* y, const bf16* bias, int rows, int cols,
+                     hipStream_t s);
+
+// out[b] = x[b*S + len[b] - 1] (rows of d floats).
+hipError_t gather_last(float* out, const float* x, const int* len, int n, int S, int d,
+                       hipStream_t s);
+
+// Greedy pick per row of logits [n, V]: the first maximum (as std::max_element), its margin
+// over the runner-up; writes tokens[step*n + b], margins[step*n + b], and advances the
+// decode state: tok[b] = pick, pos[b] += advance, cache_len[b] = pos[b] + 1.
+hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
+                          const float* logits, int n, int V, int step, int advance,
+                          hipStream_t s);
+
+// bqkv [3d] fp32 <- (bq, bk, bv) bf16.
+hipError_t pack_bias(float* bqkv, const bf16* bq, const bf16* bk, const bf16* bv, int d,
+                     hipStream_t s);
+
+}  // namespace dadgpt::gen

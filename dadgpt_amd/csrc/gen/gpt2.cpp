@@ -1,0 +1,546 @@
+// Batched GPT-2 prefill and greedy decode over the MI355X attention path (the generation stack
+// of src/generate.cpp:94-139 and src/model.cpp:659-851, re-planned for a batch of ragged
+// prompts). Per layer and step the work is: LayerNorm -> fused QKV GEMM (hipBLASLt) -> QKV
+// split with the KV-cache append -> attention (flash forward over the padded batch for the
+// prefill; one ragged decode launch for all sequences per decode step) -> Wo GEMM -> bias +
+// residual -> LayerNorm -> fc1 GEMM -> bias + GELU -> fc2 GEMM -> bias + residual. Every
+// launch is stream-ordered on the model's stream; the host synchronises once per call (or per
+// step when the caller asks for every step's logits).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "dadgpt/gpt2_generate.h"
+#include "dadgpt/gpu_attention.h"
+#include "dadgpt/gpu_matmul.h"
+#include "gen_internal.hpp"
+
+namespace dadgpt::gen {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int fail(int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return DADGPT_OK;
+  return fail(DADGPT_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+namespace {
+
+// Offsets of the reference's parameter arena (src/model.cpp:17-56).
+struct Offsets {
+  size_t tok_emb = 0, pos_emb = 0;
+  struct Layer {
+    size_t ln1_w, ln1_b, Wq, bq, Wk, bk, Wv, bv, Wo, bo, ln2_w, ln2_b, fc1_w, fc1_b, fc2_w,
+        fc2_b;
+  };
+  std::vector<Layer> layers;
+  size_t lnf_w = 0, lnf_b = 0, total = 0;
+};
+
+Offsets offsets_of(const dadgpt_gpt2_config& c) {
+  Offsets o;
+  size_t at = 0;
+  auto take = [&](size_t n) {
+    const size_t here = at;
+    at += n;
+    return here;
+  };
+  const size_t d = c.d_model, dd = d * d, dff = (size_t)c.d_ff;
+  o.tok_emb = take((size_t)c.vocab_size * d);
+  o.pos_emb = take((size_t)c.ctx_len * d);
+  o.layers.resize(c.n_layers);
+  for (auto& L : o.layers) {
+    L.ln1_w = take(d);
+    L.ln1_b = take(d);
+    L.Wq = take(dd);
+    L.bq = take(d);
+    L.Wk = take(dd);
+    L.bk = take(d);
+    L.Wv = take(dd);
+    L.bv = take(d);
+    L.Wo = take(dd);
+    L.bo = take(d);
+    L.ln2_w = take(d);
+    L.ln2_b = take(d);
+    L.fc1_w = take(d * dff);
+    L.fc1_b = take(dff);
+    L.fc2_w = take(dff * d);
+    L.fc2_b = take(d);
+  }
+  o.lnf_w = take(d);
+  o.lnf_b = take(d);
+  o.total = at;
+  return o;
+}
+
+bool config_ok(const dadgpt_gpt2_config* c) {
+  if (!c || c->d_model < 1 || c->n_layers < 1 || c->n_heads < 1 || c->d_ff < 1 ||
+      c->ctx_len < 1 || c->vocab_size < 2)
+    return false;
+  if (c->d_model % c->n_heads) return false;
+  const int dh = c->d_model / c->n_heads;
+  return dh == 32 || dh == 64;
+}
+
+uint64_t mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+}  // namespace
+
+}  // namespace dadgpt::gen
+
+using namespace dadgpt::gen;
+using dadgpt::gen::bf16;
+
+struct dadgpt_gpt2 {
+  dadgpt_gpt2_config c{};
+  Offsets off;
+  const bf16* params = nullptr;
+  int max_batch = 0;
+  bool fp32 = false;
+  int dh = 0;
+  size_t esz = 2;  // bytes per attention element (Q/K/V, caches, attention output)
+  dadgpt_blas* blas = nullptr;
+  hipStream_t stream = nullptr;
+  std::vector<void*> allocs;
+
+  std::vector<bf16*> wqkv;   // per layer [d, 3d]
+  std::vector<float*> bqkv;  // per layer [3d]
+  std::vector<void*> kc, vc;  // per layer [max_batch, H, ctx, dh]
+
+  float *x = nullptr, *qkv = nullptr, *y = nullptr, *f = nullptr, *xl = nullptr;
+  float *logits = nullptr, *lse = nullptr;
+  bf16 *h = nullptr, *a = nullptr, *g = nullptr;
+  void *qh = nullptr, *kh = nullptr, *vh = nullptr, *ao = nullptr;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  int *tok_in = nullptr, *pos0 = nullptr, *nvalid = nullptr, *ones = nullptr, *lens = nullptr;
+  int *cur_tok = nullptr, *cur_pos = nullptr, *cache_len = nullptr;
+  int* out_tok = nullptr;
+  float* out_margin = nullptr;
+  size_t out_cap = 0;
+  std::vector<hipEvent_t> events;
+
+  const bf16* P(size_t offset) const { return params + offset; }
+
+  int alloc(void** p, size_t bytes, const char* what) {
+    if (hipMalloc(p, bytes < 16 ? 16 : bytes) != hipSuccess)
+      return fail(DADGPT_ERR_HIP, "dadgpt_gpt2_create: hipMalloc of %zu bytes (%s) failed", bytes,
+                  what);
+    allocs.push_back(*p);
+    return DADGPT_OK;
+  }
+  template <typename T>
+  int alloc_n(T** p, size_t count, const char* what) {
+    return alloc(reinterpret_cast<void**>(p), count * sizeof(T), what);
+  }
+};
+
+namespace {
+
+int attention_prefill(dadgpt_gpt2* m, int n, int S, float scale) {
+  const int BH = n * m->c.n_heads;
+  if (m->fp32)
+    return dadgpt_flash_attention_forward_async((float*)m->ao, m->lse, (const float*)m->qh,
+                                                (const float*)m->kh, (const float*)m->vh, BH, S,
+                                                m->dh, scale, m->stream);
+  return dadgpt_flash_attention_forward_bf16((uint16_t*)m->ao, m->lse, (const uint16_t*)m->qh,
+                                             (const uint16_t*)m->kh, (const uint16_t*)m->vh, BH,
+                                             S, m->dh, scale, m->stream);
+}
+
+int attention_decode(dadgpt_gpt2* m, int layer, int n, float scale) {
+  const int H = m->c.n_heads, L = m->c.ctx_len;
+  if (m->fp32)
+    return dadgpt_decode_attention_f32((float*)m->ao, (const float*)m->qh,
+                                       (const float*)m->kc[layer], (const float*)m->vc[layer],
+                                       m->cache_len, n, H, L, m->dh, scale, m->ws, m->ws_bytes,
+                                       m->stream);
+  return dadgpt_decode_attention_bf16((uint16_t*)m->ao, (const uint16_t*)m->qh,
+                                      (const uint16_t*)m->kc[layer],
+                                      (const uint16_t*)m->vc[layer], m->cache_len, n, H, L,
+                                      m->dh, scale, m->ws, m->ws_bytes, m->stream);
+}
+
+// The attention error of the C ABI is recorded by libdadgpt_attn; carry it over.
+int attn_fail(int st, const char* what) {
+  return fail(st, "%s: %s", what, dadgpt_last_error());
+}
+
+#define TRY(expr)                          \
+  do {                                     \
+    if (int st_ = (expr)) return st_;      \
+  } while (0)
+#define TRY_HIP(expr, what) TRY(check_hip((expr), (what)))
+
+// One transformer block over `rows` rows (n sequences of S rows each). prefill: the rows are
+// prompt positions 0..S-1 (K/V appended for s < len); otherwise one token per sequence at
+// cur_pos. attn_ev: optional pair of events around the attention launch.
+int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev) {
+  const auto& c = m->c;
+  const auto& L = m->off.layers[l];
+  const int d = c.d_model, H = c.n_heads, dh = m->dh, rows = n * S;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(dh));  // src/model.cpp:389
+  hipStream_t s = m->stream;
+
+  TRY_HIP(layernorm(m->h, m->x, m->P(L.ln1_w), m->P(L.ln1_b), rows, d, s), "layernorm");
+  TRY(gemm(m->blas, m->qkv, m->h, m->wqkv[l], rows, d, 3 * d, false, s));
+  const bf16* attn_in = m->a;
+  if (prefill) {
+    if (m->fp32)
+      TRY_HIP(qkv_split<float>((float*)m->qh, (float*)m->kh, (float*)m->vh, (float*)m->kc[l],
+                               (float*)m->vc[l], m->qkv, m->bqkv[l], m->pos0, m->nvalid, n, S, H,
+                               dh, c.ctx_len, s),
+              "qkv_split");
+    else
+      TRY_HIP(qkv_split<bf16>((bf16*)m->qh, (bf16*)m->kh, (bf16*)m->vh, (bf16*)m->kc[l],
+                              (bf16*)m->vc[l], m->qkv, m->bqkv[l], m->pos0, m->nvalid, n, S, H,
+                              dh, c.ctx_len, s),
+              "qkv_split");
+    if (int st = attention_prefill(m, n, S, scale)) return attn_fail(st, "prefill attention");
+    if (m->fp32)
+      TRY_HIP(merge_heads<float>(m->a, (const float*)m->ao, n, S, H, dh, s), "merge_heads");
+    else
+      TRY_HIP(merge_heads<bf16>(m->a, (const bf16*)m->ao, n, S, H, dh, s), "merge_heads");
+  } else {
+    if (m->fp32)
+      TRY_HIP(qkv_split<float>((float*)m->qh, nullptr, nullptr, (float*)m->kc[l],
+                               (float*)m->vc[l], m->qkv, m->bqkv[l], m->cur_pos, m->ones, n, 1,
+                               H, dh, c.ctx_len, s),
+              "qkv_split");
+    else
+      TRY_HIP(qkv_split<bf16>((bf16*)m->qh, nullptr, nullptr, (bf16*)m->kc[l], (bf16*)m->vc[l],
+                              m->qkv, m->bqkv[l], m->cur_pos, m->ones, n, 1, H, dh, c.ctx_len,
+                              s),
+              "qkv_split");
+    if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[0], s), "hipEventRecord");
+    if (int st = attention_decode(m, l, n, scale)) return attn_fail(st, "decode attention");
+    if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[1], s), "hipEventRecord");
+    // decode output [n, H, dh] is already the [n, d] row layout
+    if (m->fp32)
+      TRY_HIP(to_bf16(m->a, (const float*)m->ao, (size_t)n * d, s), "to_bf16");
+    else
+      attn_in = (const bf16*)m->ao;
+  }
+  TRY(gemm(m->blas, m->y, attn_in, m->P(L.Wo), rows, d, d, false, s));
+  TRY_HIP(bias_residual(m->x, m->y, m->P(L.bo), rows, d, s), "bias_residual");
+  TRY_HIP(layernorm(m->h, m->x, m->P(L.ln2_w), m->P(L.ln2_b), rows, d, s), "layernorm");
+  TRY(gemm(m->blas, m->f, m->h, m->P(L.fc1_w), rows, d, c.d_ff, false, s));
+  TRY_HIP(bias_gelu(m->g, m->f, m->P(L.fc1_b), rows, c.d_ff, s), "bias_gelu");
+  TRY(gemm(m->blas, m->y, m->g, m->P(L.fc2_w), rows, c.d_ff, d, false, s));
+  TRY_HIP(bias_residual(m->x, m->y, m->P(L.fc2_b), rows, d, s), "bias_residual");
+  return DADGPT_OK;
+}
+
+// Final LayerNorm of n rows at xs, weight-tied logits, greedy pick of step `step`.
+int head(dadgpt_gpt2* m, const float* xs, int n, int step) {
+  const auto& c = m->c;
+  hipStream_t s = m->stream;
+  TRY_HIP(layernorm(m->h, xs, m->P(m->off.lnf_w), m->P(m->off.lnf_b), n, c.d_model, s),
+          "layernorm");
+  TRY(gemm(m->blas, m->logits, m->h, m->P(m->off.tok_emb), n, c.d_model, c.vocab_size, true, s));
+  TRY_HIP(argmax_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
+                         m->logits, n, c.vocab_size, step, 1, s),
+          "argmax_advance");
+  return DADGPT_OK;
+}
+
+int copy_logits(dadgpt_gpt2* m, float* host, int n, int step) {
+  const size_t count = (size_t)n * m->c.vocab_size;
+  TRY_HIP(hipMemcpyAsync(host + (size_t)step * count, m->logits, count * sizeof(float),
+                         hipMemcpyDeviceToHost, m->stream),
+          "hipMemcpyAsync(logits)");
+  TRY_HIP(hipStreamSynchronize(m->stream), "hipStreamSynchronize");
+  return DADGPT_OK;
+}
+
+int ensure_events(dadgpt_gpt2* m, size_t count) {
+  while (m->events.size() < count) {
+    hipEvent_t e;
+    TRY_HIP(hipEventCreate(&e), "hipEventCreate");
+    m->events.push_back(e);
+  }
+  return DADGPT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dadgpt_gen_last_error(void) { return g_last_error.c_str(); }
+
+size_t dadgpt_gpt2_param_count(const dadgpt_gpt2_config* config) {
+  return config_ok(config) ? offsets_of(*config).total : 0;
+}
+
+int dadgpt_gpt2_init_params(uint16_t* params, const dadgpt_gpt2_config* config, uint64_t seed,
+                            void* stream) {
+  if (!params || !config_ok(config))
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "dadgpt_gpt2_init_params: bad arguments");
+  const auto& c = *config;
+  const Offsets o = offsets_of(c);
+  bf16* p = reinterpret_cast<bf16*>(params);
+  hipStream_t s = (hipStream_t)stream;
+  const float sd = 0.02f;
+  const float res_sd = sd / std::sqrt(2.0f * static_cast<float>(c.n_layers));  // model.cpp:139
+  const size_t d = c.d_model, dd = d * d, dff = (size_t)c.d_ff * d;
+  uint64_t tensor = 0;
+  auto normal = [&](size_t off, size_t count, float stddev) {
+    return check_hip(init_normal(p + off, count, mix64(seed ^ mix64(++tensor)), stddev, s),
+                     "init_normal");
+  };
+  auto constant = [&](size_t off, size_t count, float v) {
+    return check_hip(fill(p + off, count, v, s), "fill");
+  };
+  TRY(constant(0, o.total, 0.0f));  // biases
+  TRY(normal(o.tok_emb, (size_t)c.vocab_size * d, sd));
+  TRY(normal(o.pos_emb, (size_t)c.ctx_len * d, sd));
+  for (const auto& L : o.layers) {
+    TRY(constant(L.ln1_w, d, 1.0f));
+    TRY(constant(L.ln2_w, d, 1.0f));
+    TRY(normal(L.Wq, dd, sd));
+    TRY(normal(L.Wk, dd, sd));
+    TRY(normal(L.Wv, dd, sd));
+    TRY(normal(L.Wo, dd, res_sd));
+    TRY(normal(L.fc1_w, dff, sd));
+    TRY(normal(L.fc2_w, dff, res_sd));
+  }
+  TRY(constant(o.lnf_w, d, 1.0f));
+  return DADGPT_OK;
+}
+
+void dadgpt_gpt2_destroy(dadgpt_gpt2* m) {
+  if (!m) return;
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  for (hipEvent_t e : m->events) (void)hipEventDestroy(e);
+  for (void* p : m->allocs) (void)hipFree(p);
+  if (m->blas) dadgpt_blas_destroy(m->blas);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  delete m;
+}
+
+int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params, int max_batch,
+                       int attn_fp32, dadgpt_gpt2** out) {
+  if (!out || !params || !config_ok(config) || max_batch < 1)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                "dadgpt_gpt2_create: bad arguments (d_head must be 32 or 64, max_batch >= 1)");
+  *out = nullptr;
+  auto* m = new dadgpt_gpt2();
+  m->c = *config;
+  m->off = offsets_of(m->c);
+  m->params = reinterpret_cast<const bf16*>(params);
+  m->max_batch = max_batch;
+  m->fp32 = attn_fp32 != 0;
+  m->dh = m->c.d_model / m->c.n_heads;
+  m->esz = m->fp32 ? sizeof(float) : sizeof(bf16);
+  const auto& c = m->c;
+  const size_t d = c.d_model, rows = (size_t)max_batch * c.ctx_len;
+  auto bail = [&](int st) {
+    dadgpt_gpt2_destroy(m);
+    return st;
+  };
+  if (hipStreamCreate(&m->stream) != hipSuccess)
+    return bail(fail(DADGPT_ERR_HIP, "dadgpt_gpt2_create: hipStreamCreate failed"));
+  if (int st = dadgpt_blas_create(&m->blas)) return bail(st);
+
+  // fused QKV weights [d, 3d] (Wq | Wk | Wv along the output dimension) and fp32 biases
+  m->wqkv.resize(c.n_layers);
+  m->bqkv.resize(c.n_layers);
+  m->kc.resize(c.n_layers);
+  m->vc.resize(c.n_layers);
+  const size_t cache = (size_t)max_batch * c.n_heads * c.ctx_len * m->dh * m->esz;
+  for (int l = 0; l < c.n_layers; ++l) {
+    const auto& L = m->off.layers[l];
+    if (int st = m->alloc_n(&m->wqkv[l], d * 3 * d, "wqkv")) return bail(st);
+    if (int st = m->alloc_n(&m->bqkv[l], 3 * d, "bqkv")) return bail(st);
+    const size_t wbytes = d * sizeof(bf16);
+    const size_t src[3] = {L.Wq, L.Wk, L.Wv};
+    for (int j = 0; j < 3; ++j)
+      if (hipMemcpy2DAsync(m->wqkv[l] + j * d, 3 * wbytes, m->P(src[j]), wbytes, wbytes, d,
+                           hipMemcpyDeviceToDevice, m->stream) != hipSuccess)
+        return bail(fail(DADGPT_ERR_HIP, "dadgpt_gpt2_create: QKV weight repack failed"));
+    if (int st = check_hip(pack_bias(m->bqkv[l], m->P(L.bq), m->P(L.bk), m->P(L.bv), (int)d,
+                                     m->stream),
+                           "pack_bias"))
+      return bail(st);
+    if (int st = m->alloc(&m->kc[l], cache, "k cache")) return bail(st);
+    if (int st = m->alloc(&m->vc[l], cache, "v cache")) return bail(st);
+  }
+  const size_t ab = m->esz;
+  int st = DADGPT_OK;
+  if ((st = m->alloc_n(&m->x, rows * d, "x")) || (st = m->alloc_n(&m->qkv, rows * 3 * d, "qkv")) ||
+      (st = m->alloc_n(&m->y, rows * d, "y")) ||
+      (st = m->alloc_n(&m->f, rows * c.d_ff, "fc1 out")) ||
+      (st = m->alloc_n(&m->xl, (size_t)max_batch * d, "last rows")) ||
+      (st = m->alloc_n(&m->logits, (size_t)max_batch * c.vocab_size, "logits")) ||
+      (st = m->alloc_n(&m->lse, rows * c.n_heads, "lse")) ||
+      (st = m->alloc_n(&m->h, rows * d, "ln out")) || (st = m->alloc_n(&m->a, rows * d, "attn in")) ||
+      (st = m->alloc_n(&m->g, rows * c.d_ff, "gelu out")) ||
+      (st = m->alloc(&m->qh, rows * d * ab, "q heads")) ||
+      (st = m->alloc(&m->kh, rows * d * ab, "k heads")) ||
+      (st = m->alloc(&m->vh, rows * d * ab, "v heads")) ||
+      (st = m->alloc(&m->ao, rows * d * ab, "attn out")) ||
+      (st = m->alloc_n(&m->tok_in, rows, "tokens")) ||
+      (st = m->alloc_n(&m->pos0, max_batch, "pos0")) ||
+      (st = m->alloc_n(&m->nvalid, max_batch, "nvalid")) ||
+      (st = m->alloc_n(&m->ones, max_batch, "ones")) ||
+      (st = m->alloc_n(&m->lens, max_batch, "lens")) ||
+      (st = m->alloc_n(&m->cur_tok, max_batch, "cur_tok")) ||
+      (st = m->alloc_n(&m->cur_pos, max_batch, "cur_pos")) ||
+      (st = m->alloc_n(&m->cache_len, max_batch, "cache_len")))
+    return bail(st);
+  m->ws_bytes = dadgpt_decode_workspace_bytes(max_batch, c.n_heads, c.ctx_len, m->dh);
+  if (m->ws_bytes) {
+    if ((st = m->alloc(&m->ws, m->ws_bytes, "decode workspace"))) return bail(st);
+    if (hipMemsetAsync(m->ws, 0, m->ws_bytes, m->stream) != hipSuccess)
+      return bail(fail(DADGPT_ERR_HIP, "dadgpt_gpt2_create: workspace clear failed"));
+  }
+  std::vector<int> ones(max_batch, 1), zeros(max_batch, 0);
+  if (hipMemcpyAsync(m->ones, ones.data(), max_batch * sizeof(int), hipMemcpyHostToDevice,
+                     m->stream) != hipSuccess ||
+      hipMemcpyAsync(m->pos0, zeros.data(), max_batch * sizeof(int), hipMemcpyHostToDevice,
+                     m->stream) != hipSuccess ||
+      hipStreamSynchronize(m->stream) != hipSuccess)
+    return bail(fail(DADGPT_ERR_HIP, "dadgpt_gpt2_create: initial copies failed"));
+  *out = m;
+  return DADGPT_OK;
+}
+
+int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* prompt_lens,
+                         int n, int prompt_stride, int new_tokens, int32_t* tokens,
+                         float* margins, float* logits, dadgpt_gpt2_timing* timing) {
+  const char* fn = "dadgpt_gpt2_generate";
+  if (!m || !prompts || !prompt_lens || !tokens)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: null argument", fn);
+  const auto& c = m->c;
+  if (n < 1 || n > m->max_batch || new_tokens < 1)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: n=%d (max_batch %d), new_tokens=%d", fn, n,
+                m->max_batch, new_tokens);
+  int S = 0;
+  for (int b = 0; b < n; ++b) {
+    const int len = prompt_lens[b];
+    if (len < 1 || len > prompt_stride || len + new_tokens > c.ctx_len)
+      return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                  "%s: prompt %d has %d tokens (stride %d); prompt + %d new tokens must fit "
+                  "the context of %d",
+                  fn, b, len, prompt_stride, new_tokens, c.ctx_len);
+    for (int t = 0; t < len; ++t) {
+      const int tok = prompts[(size_t)b * prompt_stride + t];
+      if (tok < 0 || tok >= c.vocab_size)
+        return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: token %d of prompt %d is %d (vocab %d)",
+                    fn, t, b, tok, c.vocab_size);
+    }
+    S = len > S ? len : S;
+  }
+  hipStream_t s = m->stream;
+  const size_t outs = (size_t)new_tokens * n;
+  if (outs > m->out_cap) {
+    if (m->out_tok) {
+      (void)hipStreamSynchronize(s);
+      (void)hipFree(m->out_tok);
+      (void)hipFree(m->out_margin);
+      m->out_tok = nullptr;
+      m->out_margin = nullptr;
+      m->out_cap = 0;
+    }
+    if (hipMalloc(&m->out_tok, outs * sizeof(int)) != hipSuccess ||
+        hipMalloc(&m->out_margin, outs * sizeof(float)) != hipSuccess)
+      return fail(DADGPT_ERR_HIP, "%s: hipMalloc of the outputs failed", fn);
+    m->out_cap = outs;
+  }
+
+  // padded prompt rows, lengths, and the position before the first generated token
+  std::vector<int> tok((size_t)n * S, 0), len(prompt_lens, prompt_lens + n), pos(n);
+  for (int b = 0; b < n; ++b) {
+    for (int t = 0; t < len[b]; ++t) tok[(size_t)b * S + t] = prompts[(size_t)b * prompt_stride + t];
+    pos[b] = len[b] - 1;
+  }
+  TRY_HIP(hipMemcpyAsync(m->tok_in, tok.data(), tok.size() * sizeof(int), hipMemcpyHostToDevice, s),
+          "hipMemcpyAsync(tokens)");
+  TRY_HIP(hipMemcpyAsync(m->nvalid, len.data(), n * sizeof(int), hipMemcpyHostToDevice, s),
+          "hipMemcpyAsync(lens)");
+  TRY_HIP(hipMemcpyAsync(m->lens, len.data(), n * sizeof(int), hipMemcpyHostToDevice, s),
+          "hipMemcpyAsync(lens)");
+  TRY_HIP(hipMemcpyAsync(m->cur_pos, pos.data(), n * sizeof(int), hipMemcpyHostToDevice, s),
+          "hipMemcpyAsync(pos)");
+
+  const int steps = new_tokens - 1;
+  const bool timed = timing != nullptr;
+  if (timed) TRY(ensure_events(m, 3 + 2 * (size_t)steps * c.n_layers));
+  hipEvent_t* ev = m->events.data();
+  if (timed) TRY_HIP(hipEventRecord(ev[0], s), "hipEventRecord");
+
+  // ---- prefill: the padded batch [n, S], then the pick after each prompt ----
+  TRY_HIP(embed(m->x, m->tok_in, m->pos0, m->P(m->off.tok_emb), m->P(m->off.pos_emb), n, S,
+                c.d_model, s),
+          "embed");
+  for (int l = 0; l < c.n_layers; ++l) TRY(block(m, l, n, S, true, nullptr));
+  TRY_HIP(gather_last(m->xl, m->x, m->lens, n, S, c.d_model, s), "gather_last");
+  TRY(head(m, m->xl, n, 0));
+  if (timed) TRY_HIP(hipEventRecord(ev[1], s), "hipEventRecord");
+  if (logits) TRY(copy_logits(m, logits, n, 0));
+
+  // ---- decode: feed token t-1 at its position, pick token t ----
+  for (int t = 1; t <= steps; ++t) {
+    TRY_HIP(embed(m->x, m->cur_tok, m->cur_pos, m->P(m->off.tok_emb), m->P(m->off.pos_emb), n,
+                  1, c.d_model, s),
+            "embed");
+    for (int l = 0; l < c.n_layers; ++l)
+      TRY(block(m, l, n, 1, false,
+                timed ? ev + 3 + 2 * ((size_t)(t - 1) * c.n_layers + l) : nullptr));
+    TRY(head(m, m->x, n, t));
+    if (logits) TRY(copy_logits(m, logits, n, t));
+  }
+  if (timed) TRY_HIP(hipEventRecord(ev[2], s), "hipEventRecord");
+
+  std::vector<int> tk(outs);
+  std::vector<float> mg(outs);
+  TRY_HIP(hipMemcpyAsync(tk.data(), m->out_tok, outs * sizeof(int), hipMemcpyDeviceToHost, s),
+          "hipMemcpyAsync(tokens)");
+  TRY_HIP(hipMemcpyAsync(mg.data(), m->out_margin, outs * sizeof(float), hipMemcpyDeviceToHost,
+                         s),
+          "hipMemcpyAsync(margins)");
+  TRY_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+  for (int b = 0; b < n; ++b)
+    for (int t = 0; t < new_tokens; ++t) {
+      tokens[(size_t)b * new_tokens + t] = tk[(size_t)t * n + b];
+      if (margins) margins[(size_t)b * new_tokens + t] = mg[(size_t)t * n + b];
+    }
+  if (timed) {
+    float ms = 0.f;
+    timing->decode_steps = steps;
+    TRY_HIP(hipEventElapsedTime(&ms, ev[0], ev[1]), "hipEventElapsedTime");
+    timing->prefill_ms = ms;
+    TRY_HIP(hipEventElapsedTime(&ms, ev[1], ev[2]), "hipEventElapsedTime");
+    timing->decode_ms = logits ? NAN : ms;  // per-step host copies would be counted
+    double attn = 0.0;
+    for (size_t i = 0; i < (size_t)steps * c.n_layers; ++i) {
+      TRY_HIP(hipEventElapsedTime(&ms, ev[3 + 2 * i], ev[4 + 2 * i]), "hipEventElapsedTime");
+      attn += ms;
+    }
+    timing->decode_attn_ms = (float)attn;
+  }
+  return DADGPT_OK;
+}
+
+}  // extern "C"

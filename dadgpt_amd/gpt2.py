@@ -1,0 +1,224 @@
+"""Python mirror of libdadgpt_gen: bf16 hipBLASLt projections and batched GPT-2 generation.
+
+The C ABI is declared in include/dadgpt/gpt2_generate.h and include/dadgpt/gpu_matmul.h.
+It replaces the reference's generation stack (src/generate.cpp:94-139 generate_tokens with
+greedy sample_token, src/model.cpp:659-851 KV cache, cached forward and prefill) and its
+cuBLAS projection wrappers (cuda/gpu_ops.cu:94-112). Like the attention wrappers, every call
+raises on failure and there is no fallback: a missing library raises ``LibraryNotBuilt``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import torch
+
+from . import attention as _attn
+
+GEN_PATH = os.path.join(_attn.HERE, "lib", "libdadgpt_gen.so")
+
+# The reference's named architectures (src/model.cpp:221-234); vocab as GPT-2's tokenizer.
+PRESETS = {
+    "tiny": dict(d_model=128, n_layers=2, n_heads=4, d_ff=512, ctx_len=64, vocab_size=512),
+    "small": dict(d_model=512, n_layers=8, n_heads=8, d_ff=2048, ctx_len=128, vocab_size=512),
+    "gpt2-124m": dict(d_model=768, n_layers=12, n_heads=12, d_ff=3072, ctx_len=1024,
+                      vocab_size=50257),
+}
+
+GEN_SYMBOLS = (
+    "dadgpt_gen_last_error",
+    "dadgpt_blas_create",
+    "dadgpt_blas_destroy",
+    "dadgpt_matmul_bf16",
+    "dadgpt_matmul_transposed_b_bf16",
+    "dadgpt_gpt2_param_count",
+    "dadgpt_gpt2_init_params",
+    "dadgpt_gpt2_create",
+    "dadgpt_gpt2_destroy",
+    "dadgpt_gpt2_generate",
+)
+
+
+class Config(ctypes.Structure):
+    _fields_ = [(k, ctypes.c_int) for k in
+                ("d_model", "n_layers", "n_heads", "d_ff", "ctx_len", "vocab_size")]
+
+    @classmethod
+    def of(cls, cfg) -> "Config":
+        if isinstance(cfg, Config):
+            return cfg
+        if isinstance(cfg, str):
+            cfg = PRESETS[cfg]
+        return cls(**cfg)
+
+    def as_dict(self) -> dict:
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+class Timing(ctypes.Structure):
+    _fields_ = [("prefill_ms", ctypes.c_float), ("decode_ms", ctypes.c_float),
+                ("decode_attn_ms", ctypes.c_float), ("decode_steps", ctypes.c_int)]
+
+
+_gen = None
+
+
+def gen_lib():
+    """The loaded generation library (after the attention library it links against)."""
+    global _gen
+    if _gen is not None:
+        return _gen
+    _attn.lib()
+    if not os.path.exists(GEN_PATH):
+        raise _attn.LibraryNotBuilt(f"{GEN_PATH} is not built; run __graft_entry__.build()")
+    try:
+        L = ctypes.CDLL(GEN_PATH)
+    except OSError as e:  # pragma: no cover - depends on the machine
+        raise _attn.LibraryNotBuilt(f"cannot load {GEN_PATH}: {e}") from e
+    vp, i, f, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    cfgp = ctypes.POINTER(Config)
+    L.dadgpt_gen_last_error.restype = ctypes.c_char_p
+    L.dadgpt_gen_last_error.argtypes = []
+    L.dadgpt_blas_create.argtypes = [ctypes.POINTER(vp)]
+    L.dadgpt_blas_destroy.argtypes = [vp]
+    L.dadgpt_blas_destroy.restype = None
+    L.dadgpt_matmul_bf16.argtypes = [vp, vp, vp, vp, i, i, i, vp]
+    L.dadgpt_matmul_transposed_b_bf16.argtypes = [vp, vp, vp, vp, i, i, i, vp]
+    L.dadgpt_gpt2_param_count.argtypes = [cfgp]
+    L.dadgpt_gpt2_param_count.restype = sz
+    L.dadgpt_gpt2_init_params.argtypes = [vp, cfgp, ctypes.c_uint64, vp]
+    L.dadgpt_gpt2_create.argtypes = [cfgp, vp, i, i, ctypes.POINTER(vp)]
+    L.dadgpt_gpt2_destroy.argtypes = [vp]
+    L.dadgpt_gpt2_destroy.restype = None
+    L.dadgpt_gpt2_generate.argtypes = [vp, vp, vp, i, i, i, vp, vp, vp, ctypes.POINTER(Timing)]
+    for name in GEN_SYMBOLS:
+        if name not in ("dadgpt_gen_last_error", "dadgpt_blas_destroy", "dadgpt_gpt2_destroy",
+                        "dadgpt_gpt2_param_count"):
+            getattr(L, name).restype = i
+    _gen = L
+    return L
+
+
+def last_error() -> str:
+    return gen_lib().dadgpt_gen_last_error().decode()
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise _attn.AttentionError(status, last_error())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+# ------------------------------------------------------------------------------ GEMMs
+
+class Blas:
+    """An opaque hipBLASLt handle (the reference's cublasHandle_t, src/model.cpp:236)."""
+
+    def __init__(self):
+        self._h = ctypes.c_void_p()
+        _check(gen_lib().dadgpt_blas_create(ctypes.byref(self._h)))
+
+    def close(self):
+        if self._h:
+            gen_lib().dadgpt_blas_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    __del__ = close
+
+    def _mm(self, fn, a, b, M, K, N):
+        for t, nm in ((a, "a"), (b, "b")):
+            if t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous():
+                raise ValueError(f"{nm} must be a contiguous bfloat16 device tensor")
+        out = torch.empty(M, N, dtype=torch.float32, device=a.device)
+        _check(fn(self._h, out.data_ptr(), a.data_ptr(), b.data_ptr(), M, K, N, _stream()))
+        return out
+
+    def matmul(self, a, b):
+        """gpu_matmul (cuda/gpu_ops.cu:94-98): a [M,K] @ b [K,N] -> fp32 [M,N]."""
+        (M, K), (K2, N) = a.shape, b.shape
+        if K != K2:
+            raise ValueError("inner dimensions differ")
+        return self._mm(gen_lib().dadgpt_matmul_bf16, a, b, M, K, N)
+
+    def matmul_transposed_b(self, a, b):
+        """gpu_matmul_transposed_b (cuda/gpu_ops.cu:108-112): a [M,K] @ b[N,K]^T -> [M,N]."""
+        (M, K), (N, K2) = a.shape, b.shape
+        if K != K2:
+            raise ValueError("inner dimensions differ")
+        return self._mm(gen_lib().dadgpt_matmul_transposed_b_bf16, a, b, M, K, N)
+
+
+# ------------------------------------------------------------------------ the model
+
+def param_count(cfg) -> int:
+    c = Config.of(cfg)
+    return int(gen_lib().dadgpt_gpt2_param_count(ctypes.byref(c)))
+
+
+def init_params(cfg, seed: int, device="cuda") -> torch.Tensor:
+    """A device bf16 parameter arena with the reference's GPT-2 initialisation
+    (src/model.cpp:121-166), from a seeded counter-based stream."""
+    c = Config.of(cfg)
+    n = param_count(c)
+    if n == 0:
+        raise ValueError(f"invalid config {c.as_dict()}")
+    params = torch.empty(n, dtype=torch.bfloat16, device=device)
+    _check(gen_lib().dadgpt_gpt2_init_params(params.data_ptr(), ctypes.byref(c), seed,
+                                             _stream()))
+    return params
+
+
+class GPT2:
+    """Batched greedy generation over a bf16 parameter arena (kept referenced here)."""
+
+    def __init__(self, cfg, params: torch.Tensor, max_batch: int, attn_fp32: bool = False):
+        self.cfg = Config.of(cfg)
+        if params.dtype != torch.bfloat16 or not params.is_cuda:
+            raise ValueError("params must be a bfloat16 device tensor")
+        if params.numel() != param_count(self.cfg):
+            raise ValueError("params has the wrong size for this config")
+        self.params = params
+        self.max_batch = max_batch
+        self._m = ctypes.c_void_p()
+        torch.cuda.synchronize()  # the arena may still be being written on torch's stream
+        _check(gen_lib().dadgpt_gpt2_create(ctypes.byref(self.cfg), params.data_ptr(), max_batch,
+                                            int(attn_fp32), ctypes.byref(self._m)))
+
+    def close(self):
+        if self._m:
+            gen_lib().dadgpt_gpt2_destroy(self._m)
+            self._m = ctypes.c_void_p()
+
+    __del__ = close
+
+    def generate(self, prompts, new_tokens: int, logits: bool = False, timing: bool = False):
+        """prompts: list of 1-D int sequences. Returns a dict with tokens [n, new_tokens]
+        int32, margins [n, new_tokens] float32, and optionally logits
+        [new_tokens, n, vocab] float32 and timing (ms)."""
+        n = len(prompts)
+        lens = np.array([len(p) for p in prompts], np.int32)
+        stride = int(lens.max())
+        pad = np.zeros((n, stride), np.int32)
+        for b, p in enumerate(prompts):
+            pad[b, :len(p)] = np.asarray(p, np.int32)
+        toks = np.zeros((n, new_tokens), np.int32)
+        margins = np.zeros((n, new_tokens), np.float32)
+        lg = np.zeros((new_tokens, n, self.cfg.vocab_size), np.float32) if logits else None
+        tm = Timing()
+        torch.cuda.synchronize()
+        _check(gen_lib().dadgpt_gpt2_generate(
+            self._m, pad.ctypes.data, lens.ctypes.data, n, stride, new_tokens, toks.ctypes.data,
+            margins.ctypes.data, None if lg is None else lg.ctypes.data,
+            ctypes.byref(tm) if timing else None))
+        out = {"tokens": toks, "margins": margins}
+        if lg is not None:
+            out["logits"] = lg
+        if timing:
+            out["timing"] = {"prefill_ms": tm.prefill_ms, "decode_ms": tm.decode_ms,
+                             "decode_attn_ms": tm.decode_attn_ms,
+                             "decode_steps": tm.decode_steps}
+        return out

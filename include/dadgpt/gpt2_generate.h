@@ -1,0 +1,83 @@
+/*
+ * libdadgpt_gen.so — batched GPT-2 generation on the MI355X attention path.
+ *
+ * Replaces, for a batch of ragged prompts, the reference's generation stack:
+ *   generate_tokens / sample_token (greedy)   src/generate.cpp:16-37, 94-139
+ *   model_prefill                             src/model.cpp:827-851
+ *   model_forward_cached                      src/model.cpp:687-825
+ *   KVCache, kv_cache_alloc                   src/model.hpp:140-152, src/model.cpp:659-685
+ * The reference decodes one sequence at a time with 2*H cache memcpys and 2*H cuBLAS GEMVs per
+ * layer and token. Here the prompts of a batch prefill together (one flash-attention launch per
+ * layer over the padded batch, the KV append fused into the QKV split), and every decode step
+ * runs one ragged decode-attention launch per layer for the whole batch. Projections are bf16
+ * hipBLASLt GEMMs (<dadgpt/gpu_matmul.h>); the residual stream, LayerNorm statistics and
+ * logits are fp32. Attention runs in bf16 (default) or in fp32 (attn_fp32 = 1: fp32 Q/K/V,
+ * fp32 caches, the fp32 kernels) with everything else identical.
+ *
+ * Status codes are those of <dadgpt/gpu_attention.h>; dadgpt_gen_last_error() describes the
+ * last failure on the calling thread.
+ */
+#ifndef DADGPT_GPT2_GENERATE_H
+#define DADGPT_GPT2_GENERATE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The reference's ModelConfig (src/model.hpp:10-20) without batch_size.
+ * GPT-2 124M: d_model 768, n_layers 12, n_heads 12, d_ff 3072, ctx_len 1024, vocab 50257. */
+typedef struct dadgpt_gpt2_config {
+  int d_model, n_layers, n_heads, d_ff, ctx_len, vocab_size;
+} dadgpt_gpt2_config;
+
+typedef struct dadgpt_gpt2 dadgpt_gpt2;
+
+typedef struct dadgpt_gpt2_timing {
+  float prefill_ms;      /* the batched prefill, through the first greedy pick */
+  float decode_ms;       /* all decode steps */
+  float decode_attn_ms;  /* the decode-attention launches inside those steps */
+  int decode_steps;
+} dadgpt_gpt2_timing;
+
+/* Parameter count (bf16 elements) of the reference's parameter arena, in its order
+ * (src/model.cpp:17-56): tok_emb [V,d], pos_emb [ctx,d], then per layer ln1_w, ln1_b,
+ * Wq [d,d], bq, Wk, bk, Wv, bv, Wo, bo, ln2_w, ln2_b, fc1_w [d,d_ff], fc1_b, fc2_w [d_ff,d],
+ * fc2_b; then lnf_w, lnf_b. Weights are row-major [in, out]. 0 for an invalid config. */
+size_t dadgpt_gpt2_param_count(const dadgpt_gpt2_config* config);
+
+/* The reference's initialisation (src/model.cpp:121-166) into a device arena of
+ * dadgpt_gpt2_param_count elements: weights N(0, 0.02); Wo and fc2_w N(0, 0.02/sqrt(2L));
+ * biases 0; LayerNorm weights 1. The normals come from a counter-based splitmix64 +
+ * Box-Muller stream of `seed` (one sub-stream per tensor), rounded to bf16. */
+int dadgpt_gpt2_init_params(uint16_t* params, const dadgpt_gpt2_config* config, uint64_t seed,
+                            void* stream);
+
+/* A model over a caller-owned device parameter arena (kept by pointer: it must outlive the
+ * model). Allocates the fused QKV weights, the KV caches [max_batch, H, ctx_len, d_head] per
+ * layer, activations for max_batch x ctx_len rows, and a hipBLASLt handle. d_head must be 32
+ * or 64. */
+int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params, int max_batch,
+                       int attn_fp32, dadgpt_gpt2** out);
+void dadgpt_gpt2_destroy(dadgpt_gpt2* model);
+
+/* Greedy generation for n <= max_batch prompts (host arrays):
+ *   prompts [n, prompt_stride] int32 token ids, row b holding prompt_lens[b] >= 1 tokens;
+ *   every prompt_lens[b] + new_tokens <= ctx_len (the reference stops at the context, and
+ *   truncating a long prompt, src/generate.cpp:100-110, is the caller's choice).
+ * Outputs (host): tokens [n, new_tokens]; margins [n, new_tokens] or NULL (top-1 minus
+ * top-2 logit of each pick); logits [new_tokens, n, vocab] or NULL (every step's logits: for
+ * tests, it synchronises per step); timing or NULL.
+ * Token t of row b is the first maximum of the logits after the prompt and tokens 0..t-1
+ * (std::max_element, src/generate.cpp:34-37). No stop token: exactly new_tokens per row. */
+int dadgpt_gpt2_generate(dadgpt_gpt2* model, const int32_t* prompts, const int32_t* prompt_lens,
+                         int n, int prompt_stride, int new_tokens, int32_t* tokens,
+                         float* margins, float* logits, dadgpt_gpt2_timing* timing);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DADGPT_GPT2_GENERATE_H */

@@ -14,6 +14,10 @@ Two libraries, both built by ``oracle/Makefile``:
   where ``/root/reference`` was available at build time (and on GPU boxes the tree was sent to).
 
 Numpy in, numpy out; float32 arrays for the f32 functions, float64 for the f64 twins.
+
+``gpt2_oracle`` (numpy) restates the GPT-2 forward of the generation path; ``ref_gpt2_forward``
+composes the reference's own CPU operators (``src/tensor_ops.cpp``, from ``_ref``) in
+``model_forward``'s order to pin it.
 """
 from __future__ import annotations
 
@@ -246,3 +250,101 @@ def ref_decode(q, k_cache, v_cache, lens, scale):
     _check(R.ref_decode_f32(_f(out), _f(q), _f(k_cache), _f(v_cache), lens.ctypes.data_as(_ip),
                             n, H, max_len, D, scale), "ref decode")
     return out
+
+
+# ---- the reference's own CPU tensor operators (src/tensor_ops.cpp, C++ linkage) ----
+
+_REF_OPS = {
+    "matmul": ("_Z6matmulPfPKfS1_iii", [_fp, _fp, _fp, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "matmul_tb": ("_Z19matmul_transposed_bPfPKfS1_iii",
+                  [_fp, _fp, _fp, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "layernorm": ("_Z9layernormPfPKfS1_S1_iif",
+                  [_fp, _fp, _fp, _fp, ctypes.c_int, ctypes.c_int, ctypes.c_float]),
+    "gelu": ("_Z4geluPfPKfi", [_fp, _fp, ctypes.c_int]),
+    "embedding": ("_Z16embedding_lookupPfPKtPKfii",
+                  [_fp, ctypes.POINTER(ctypes.c_uint16), _fp, ctypes.c_int, ctypes.c_int]),
+    "add": ("_Z11add_vectorsPfPKfS1_i", [_fp, _fp, _fp, ctypes.c_int]),
+}
+
+
+def ref_op(name):
+    """A reference CPU operator from oracle/_ref (raises when not built)."""
+    R = ref_lib()
+    if R is None:
+        raise RuntimeError("oracle/_ref/libref_attn.so is not built")
+    sym, argtypes = _REF_OPS[name]
+    fn = getattr(R, sym)
+    fn.argtypes = argtypes
+    fn.restype = None
+    return fn
+
+
+def ref_layernorm(x, w, b, eps=1e-5):
+    x, w, b = _c32(x), _c32(w), _c32(b)
+    out = np.empty_like(x)
+    ref_op("layernorm")(_f(out), _f(x), _f(w), _f(b), x.shape[0], x.shape[1], eps)
+    return out
+
+
+def ref_gelu(x):
+    x = _c32(x)
+    out = np.empty_like(x)
+    ref_op("gelu")(_f(out), _f(x), x.size)
+    return out
+
+
+def ref_matmul(a, b):
+    a, b = _c32(a), _c32(b)
+    out = np.empty((a.shape[0], b.shape[1]), np.float32)
+    ref_op("matmul")(_f(out), _f(a), _f(b), a.shape[0], a.shape[1], b.shape[1])
+    return out
+
+
+def ref_matmul_tb(a, b):
+    a, b = _c32(a), _c32(b)
+    out = np.empty((a.shape[0], b.shape[0]), np.float32)
+    ref_op("matmul_tb")(_f(out), _f(a), _f(b), a.shape[0], a.shape[1], b.shape[0])
+    return out
+
+
+def ref_gpt2_forward(params, cfg, tokens):
+    """Logits [S, V] of one sequence, composed from the reference's own CPU operators in the
+    order of model_forward (src/model.cpp:334-475, batch 1); attention is the reference's
+    materialized composition (ref_attn_fwd). Bias adds and the head split/merge are index
+    work done in numpy."""
+    from . import gpt2_oracle
+
+    P = gpt2_oracle.unpack(_c32(params), cfg)
+    d, H, L = cfg["d_model"], cfg["n_heads"], cfg["n_layers"]
+    dh = d // H
+    toks = np.ascontiguousarray(tokens, dtype=np.uint16)
+    S = len(toks)
+    emb = np.empty((S, d), np.float32)
+    ref_op("embedding")(_f(emb), toks.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)),
+                        _f(_c32(P["tok_emb"])), S, d)
+    x = np.empty_like(emb)
+    pos = _c32(P["pos_emb"][:S])
+    ref_op("add")(_f(x), _f(emb), _f(pos), S * d)
+    scale = np.float32(1.0) / np.sqrt(np.float32(dh))
+
+    def add(a, b):
+        a, b = _c32(a), _c32(b)
+        out = np.empty_like(a)
+        ref_op("add")(_f(out), _f(a), _f(b), a.size)
+        return out
+
+    for l in range(L):
+        g = lambda nm: P[f"{l}.{nm}"]
+        h = ref_layernorm(x, g("ln1_w"), g("ln1_b"))
+        q = ref_matmul(h, g("Wq")) + g("bq")
+        k = ref_matmul(h, g("Wk")) + g("bk")
+        v = ref_matmul(h, g("Wv")) + g("bv")
+        split = lambda t: np.ascontiguousarray(t.reshape(S, H, dh).transpose(1, 0, 2))
+        a = ref_attn_fwd(split(q), split(k), split(v), float(scale))
+        a = np.ascontiguousarray(a.transpose(1, 0, 2).reshape(S, d))
+        x = add(x, ref_matmul(a, g("Wo")) + g("bo"))
+        h = ref_layernorm(x, g("ln2_w"), g("ln2_b"))
+        f = ref_gelu(ref_matmul(h, g("fc1_w")) + g("fc1_b"))
+        x = add(x, ref_matmul(f, g("fc2_w")) + g("fc2_b"))
+    h = ref_layernorm(x, P["lnf_w"], P["lnf_b"])
+    return ref_matmul_tb(h, P["tok_emb"])
