@@ -11,7 +11,11 @@ The same line carries each kernel's time and roofline fraction, the KV-decode HB
 the 256 MB MALL cannot hold them), the roofline of the dominant kernel, and the reference's
 CPU path timed on a bounded sample on this host.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+Config 5 (GPT-2 124M architecture, random init, 16 prompts of U[16,256] random tokens,
+batched prefill + 128 greedy tokens) is reported under components.generate_cfg5: tokens/s,
+the decode-attention time share, and the comparison with fp32 attention.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-generate]
     python bench.py --profile-sample     # each kernel --reps times + a copy of known size,
                                          # for rocprofv3 --pmc runs; prints no bench line
 """
@@ -58,6 +62,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-slices", type=int, default=24)
     p.add_argument("--profile-sample", action="store_true")
+    p.add_argument("--no-generate", action="store_true", help="skip the config 5 leg")
     p.add_argument("--prewarm-seconds", type=float, default=2.0,
                    help="untimed fwd+bwd steps before the warmup, so clocks have ramped")
     return p.parse_args()
@@ -204,6 +209,71 @@ def profile_sample(wl, reps):
           f"{COPY_BYTES} B copy", flush=True)
 
 
+GEN_N, GEN_NEW, GEN_SEED = 16, 128, 0x5EED
+
+
+def generate_cfg5():
+    """Config 5: GPT-2 124M architecture, random init (the reference's init rules,
+    src/model.cpp:121-166), 16 prompts of U[16,256] random tokens, batched prefill into the KV
+    cache, 128 greedy tokens each; then the same with fp32 attention."""
+    import numpy as np
+    import torch
+
+    from dadgpt_amd import gpt2, synth
+
+    cfg = gpt2.PRESETS["gpt2-124m"]
+    lens = synth.uniform_int(16, 256, GEN_N, GEN_SEED ^ 0x10)
+    prompts = [list(synth.uniform_int(0, cfg["vocab_size"] - 1, int(n), GEN_SEED + 0x100 + i))
+               for i, n in enumerate(lens)]
+    params = gpt2.init_params(cfg, GEN_SEED)
+    m16 = gpt2.GPT2(cfg, params, GEN_N, attn_fp32=False)
+    m16.generate(prompts, 8)  # builds the hipBLASLt plans and captures the decode step
+    runs = [m16.generate(prompts, GEN_NEW, timing=True) for _ in range(3)]
+    best = min(runs, key=lambda r: r["timing"]["prefill_ms"] + r["timing"]["decode_ms"])
+    t = best["timing"]
+    # the attention launches timed one by one need the eager step (no events inside a graph)
+    m16.set_graphs(False)
+    eager = m16.generate(prompts, GEN_NEW, timing=True)["timing"]
+    m16.close()
+    m32 = gpt2.GPT2(cfg, params, GEN_N, attn_fp32=True)
+    ref = m32.generate(prompts, GEN_NEW, timing=True)
+    m32.close()
+    del params
+    torch.cuda.synchronize()
+    a, b = best["tokens"], ref["tokens"]
+    div = [int(np.nonzero(ra != rb)[0][0]) if (ra != rb).any() else GEN_NEW
+           for ra, rb in zip(a, b)]
+    div_margins = [float(ref["margins"][r, d]) for r, d in enumerate(div) if d < GEN_NEW]
+    total_ms = t["prefill_ms"] + t["decode_ms"]
+    out = {
+        "config": "GPT-2 124M arch (d768 L12 H12 ff3072 ctx1024 V50257), random init, 16 "
+                  "prompts len U[16,256], 128 greedy tokens, bf16 attention + bf16 hipBLASLt "
+                  "projections, fp32 residual",
+        "tokens": int(GEN_N * GEN_NEW),
+        "tokens_per_s": round(GEN_N * GEN_NEW / (total_ms * 1e-3), 1),
+        "decode_tokens_per_s": round(GEN_N * t["decode_steps"] / (t["decode_ms"] * 1e-3), 1),
+        "prefill_ms": round(t["prefill_ms"], 3),
+        "decode_ms": round(t["decode_ms"], 3),
+        "decode_ms_per_step": round(t["decode_ms"] / t["decode_steps"], 4),
+        "decode_graph": True,
+        "eager_decode_ms": round(eager["decode_ms"], 3),
+        "decode_attn_ms": round(eager["decode_attn_ms"], 3),
+        "attn_share_of_decode": round(eager["decode_attn_ms"] / t["decode_ms"], 4),
+        "fp32_attention": {
+            "tokens_per_s": round(GEN_N * GEN_NEW / ((ref["timing"]["prefill_ms"] +
+                                                      ref["timing"]["decode_ms"]) * 1e-3), 1),
+            "identical_tokens": float((a == b).mean()),
+            "rows_identical": int(sum(d == GEN_NEW for d in div)),
+            "first_divergence_per_row": div,
+            "fp32_margin_at_divergence_max": max(div_margins) if div_margins else None,
+            "min_margin_fp32": float(ref["margins"].min()),
+            "min_margin_bf16": float(best["margins"].min()),
+        },
+    }
+    print(f"[bench] generate cfg5 {json.dumps(out)}", file=sys.stderr, flush=True)
+    return out
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -296,6 +366,9 @@ def main():
                        "eager_us_per_launch": round(eager_dec_ms * 1e3, 3),
                        "cache_copies": wl.ncopy, "hbm_bytes_per_launch": traffic.get("decode"),
                        "config": "32 seqs, H12, D64, bf16 cache [32,12,1024,64], lens U[1,1024]"}
+
+    if not args.no_generate:
+        comps["generate_cfg5"] = generate_cfg5()
 
     dom = max(("fwd", "bwd_dq", "bwd_dkdv"), key=lambda n: kern_ms[n])
     ach = KERNEL_FLOPS[dom] / (kern_ms[dom] * 1e-3) / 1e12

@@ -3,14 +3,18 @@
 // matrix X^T (C rows, R cols, leading dimension C), so
 //   out[M,N] = a[M,K] b[K,N]    is  out^T[N,M] = b^T[N,K] a^T[K,M]    (both operands as stored)
 //   out[M,N] = a[M,K] b[N,K]^T  is  out^T[N,M] = (b^T)^T[N,K] a^T[K,M] (first operand transposed)
-// One plan (descriptors, layouts, the heuristic's first algorithm) is built per distinct shape
-// and reused; the 32 MiB workspace is allocated once per handle.
+// One plan (descriptors, layouts, an algorithm) is built per distinct shape and reused; the
+// 32 MiB workspace is allocated once per handle. The first call of a shape (outside stream
+// capture) times up to 16 of the heuristic's candidates on the call's own operands and keeps
+// the fastest: for the skinny decode shapes (M = batch) the heuristic's first choice was up to
+// several times slower than the best candidate.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdio>
 #include <map>
 #include <tuple>
+#include <vector>
 
 #include "dadgpt/gpu_attention.h"
 #include "dadgpt/gpu_matmul.h"
@@ -24,6 +28,8 @@ struct dadgpt_blas {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, ld = nullptr;
     hipblasLtMatmulAlgo_t algo{};
+    std::vector<hipblasLtMatmulAlgo_t> candidates;
+    bool tuned = false;
   };
   std::map<std::tuple<int, int, int, int>, Plan> plans;  // (M, N, K, transposed_b)
 };
@@ -33,6 +39,7 @@ namespace dadgpt::gen {
 namespace {
 
 constexpr size_t kWorkspaceBytes = 32u << 20;
+constexpr int kCandidates = 16;
 
 int lt_fail(hipblasStatus_t s, const char* what) {
   return fail(DADGPT_ERR_HIP, "%s: hipBLASLt status %d", what, (int)s);
@@ -72,16 +79,55 @@ int plan_for(dadgpt_blas* h, int M, int N, int K, bool trans_b, dadgpt_blas::Pla
   const uint64_t ws = h->workspace_bytes;
   hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
                                         sizeof(ws));
-  hipblasLtMatmulHeuristicResult_t res[4];
+  hipblasLtMatmulHeuristicResult_t res[kCandidates];
   int n = 0;
-  s = hipblasLtMatmulAlgoGetHeuristic(h->lt, p.desc, p.la, p.lb, p.ld, p.ld, pref, 4, res, &n);
+  s = hipblasLtMatmulAlgoGetHeuristic(h->lt, p.desc, p.la, p.lb, p.ld, p.ld, pref, kCandidates,
+                                      res, &n);
   hipblasLtMatmulPreferenceDestroy(pref);
   if (s != HIPBLAS_STATUS_SUCCESS || n < 1)
     return fail(DADGPT_ERR_HIP, "hipBLASLt has no algorithm for M=%d N=%d K=%d%s (status %d)",
                 M, N, K, trans_b ? " (b transposed)" : "", (int)s);
   p.algo = res[0].algo;
+  for (int i = 0; i < n; ++i)
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS) p.candidates.push_back(res[i].algo);
   *out = &(h->plans[key] = p);
   return DADGPT_OK;
+}
+
+// Times each candidate of a fresh plan on the call's operands (the output is rewritten by the
+// call that follows) and keeps the fastest. Skipped while the stream is being captured.
+void tune(dadgpt_blas* h, dadgpt_blas::Plan* p, float* out, const void* a, const void* b,
+          hipStream_t stream) {
+  p->tuned = true;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (p->candidates.size() < 2 || hipStreamIsCapturing(stream, &cap) != hipSuccess ||
+      cap != hipStreamCaptureStatusNone)
+    return;
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess) return;
+  if (hipEventCreate(&e1) != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return;
+  }
+  const float alpha = 1.0f, beta = 0.0f;
+  float best = 1e30f;
+  for (const auto& algo : p->candidates) {
+    auto run = [&] {
+      return hipblasLtMatmul(h->lt, p->desc, &alpha, b, p->la, a, p->lb, &beta, out, p->ld, out,
+                             p->ld, &algo, h->workspace, h->workspace_bytes, stream);
+    };
+    if (run() != HIPBLAS_STATUS_SUCCESS) continue;
+    bool ok = hipEventRecord(e0, stream) == hipSuccess;
+    for (int r = 0; r < 3 && ok; ++r) ok = run() == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipEventRecord(e1, stream) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+    float ms = 0.f;
+    if (ok && hipEventElapsedTime(&ms, e0, e1) == hipSuccess && ms < best) {
+      best = ms;
+      p->algo = algo;
+    }
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
 }
 
 int matmul(dadgpt_blas* h, float* out, const uint16_t* a, const uint16_t* b, int M, int K, int N,
@@ -91,6 +137,7 @@ int matmul(dadgpt_blas* h, float* out, const uint16_t* a, const uint16_t* b, int
     return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: M=%d K=%d N=%d must be positive", fn, M, K, N);
   dadgpt_blas::Plan* p = nullptr;
   if (int st = plan_for(h, M, N, K, trans_b, &p)) return st;
+  if (!p->tuned) tune(h, p, out, a, b, (hipStream_t)stream);
   const float alpha = 1.0f, beta = 0.0f;
   const hipblasStatus_t s =
       hipblasLtMatmul(h->lt, p->desc, &alpha, b, p->la, a, p->lb, &beta, out, p->ld, out, p->ld,

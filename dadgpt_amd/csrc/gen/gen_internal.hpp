@@ -31,9 +31,11 @@ hipError_t fill(bf16* p, size_t n, float value, hipStream_t s);
 hipError_t embed(float* x, const int* tok, const int* pos0, const bf16* wte, const bf16* wpe,
                  int n, int S, int d, hipStream_t s);
 
-// out[r] = bf16(LayerNorm(x[r]) * w + b), eps 1e-5 (two-pass mean and variance, fp32).
-hipError_t layernorm(bf16* out, const float* x, const bf16* w, const bf16* b, int rows, int d,
-                     hipStream_t s);
+// Per row (d <= 2048): if y, x[r] += y[r] + bias (the residual add of a projection); then,
+// if w, out[r] = bf16(LayerNorm(x[r]) * w + b) with eps 1e-5 (two-pass mean and variance,
+// fp32).
+hipError_t residual_layernorm(float* x, const float* y, const bf16* bias, bf16* out,
+                              const bf16* w, const bf16* b, int rows, int d, hipStream_t s);
 
 // qkv [n*S, 3d] fp32 (+ bias bqkv [3d] fp32): q -> qh [n*H, S, dh]; k, v -> kh, vh
 // [n*H, S, dh] when kh is not null; k, v of the rows s < nvalid[b] -> caches
@@ -50,10 +52,6 @@ hipError_t merge_heads(bf16* out, const T* heads, int n, int S, int H, int dh, h
 // out[i] = bf16(in[i]).
 hipError_t to_bf16(bf16* out, const float* in, size_t count, hipStream_t s);
 
-// x[r, c] += y[r, c] + bias[c] (fp32 x and y, bf16 bias).
-hipError_t bias_residual(float* x, const float* y, const bf16* bias, int rows, int cols,
-                         hipStream_t s);
-
 // out[r, c] = bf16(gelu_tanh(y[r, c] + bias[c])).
 hipError_t bias_gelu(bf16* out, const float* y, const bf16* bias, int rows, int cols,
                      hipStream_t s);
@@ -62,12 +60,16 @@ hipError_t bias_gelu(bf16* out, const float* y, const bf16* bias, int rows, int 
 hipError_t gather_last(float* out, const float* x, const int* len, int n, int S, int d,
                        hipStream_t s);
 
-// Greedy pick per row of logits [n, V]: the first maximum (as std::max_element), its margin
-// over the runner-up; writes tokens[step*n + b], margins[step*n + b], and advances the
-// decode state: tok[b] = pick, pos[b] += advance, cache_len[b] = pos[b] + 1.
+// Greedy pick per row of logits [n, V]: the first maximum (as std::max_element) and its
+// margin over the runner-up, stored at step = pos[b] - (prompt_len[b] - 1) in tokens
+// [step*n + b] and margins; then the decode state advances: tok[b] = pick, pos[b] += 1,
+// cache_len[b] = pos[b] + 1.
+// Two launches: 32 blocks per row reduce slices into candidates (scratch of
+// pick_scratch_floats(n) floats), then one wave per row merges them.
+size_t pick_scratch_floats(int n);
 hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
-                          const float* logits, int n, int V, int step, int advance,
-                          hipStream_t s);
+                          const int* prompt_len, const float* logits, float* scratch, int n,
+                          int V, hipStream_t s);
 
 // bqkv [3d] fp32 <- (bq, bk, bv) bf16.
 hipError_t pack_bias(float* bqkv, const bf16* bq, const bf16* bk, const bf16* bv, int d,

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -129,17 +130,18 @@ struct dadgpt_gpt2 {
   std::vector<void*> kc, vc;  // per layer [max_batch, H, ctx, dh]
 
   float *x = nullptr, *qkv = nullptr, *y = nullptr, *f = nullptr, *xl = nullptr;
-  float *logits = nullptr, *lse = nullptr;
+  float *logits = nullptr, *lse = nullptr, *pick = nullptr;
   bf16 *h = nullptr, *a = nullptr, *g = nullptr;
   void *qh = nullptr, *kh = nullptr, *vh = nullptr, *ao = nullptr;
   void* ws = nullptr;
   size_t ws_bytes = 0;
   int *tok_in = nullptr, *pos0 = nullptr, *nvalid = nullptr, *ones = nullptr, *lens = nullptr;
   int *cur_tok = nullptr, *cur_pos = nullptr, *cache_len = nullptr;
-  int* out_tok = nullptr;
+  int* out_tok = nullptr;       // [ctx_len, max_batch]: every step any call can take
   float* out_margin = nullptr;
-  size_t out_cap = 0;
   std::vector<hipEvent_t> events;
+  bool use_graphs = true;
+  std::map<int, hipGraphExec_t> graphs;  // captured decode step per batch size
 
   const bf16* P(size_t offset) const { return params + offset; }
 
@@ -203,7 +205,7 @@ int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev
   const float scale = 1.0f / std::sqrt(static_cast<float>(dh));  // src/model.cpp:389
   hipStream_t s = m->stream;
 
-  TRY_HIP(layernorm(m->h, m->x, m->P(L.ln1_w), m->P(L.ln1_b), rows, d, s), "layernorm");
+  // m->h holds LayerNorm 1 of x (written by whichever kernel last updated x)
   TRY(gemm(m->blas, m->qkv, m->h, m->wqkv[l], rows, d, 3 * d, false, s));
   const bf16* attn_in = m->a;
   if (prefill) {
@@ -243,25 +245,85 @@ int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev
       attn_in = (const bf16*)m->ao;
   }
   TRY(gemm(m->blas, m->y, attn_in, m->P(L.Wo), rows, d, d, false, s));
-  TRY_HIP(bias_residual(m->x, m->y, m->P(L.bo), rows, d, s), "bias_residual");
-  TRY_HIP(layernorm(m->h, m->x, m->P(L.ln2_w), m->P(L.ln2_b), rows, d, s), "layernorm");
+  TRY_HIP(residual_layernorm(m->x, m->y, m->P(L.bo), m->h, m->P(L.ln2_w), m->P(L.ln2_b), rows,
+                             d, s),
+          "residual_layernorm");
   TRY(gemm(m->blas, m->f, m->h, m->P(L.fc1_w), rows, d, c.d_ff, false, s));
   TRY_HIP(bias_gelu(m->g, m->f, m->P(L.fc1_b), rows, c.d_ff, s), "bias_gelu");
   TRY(gemm(m->blas, m->y, m->g, m->P(L.fc2_w), rows, c.d_ff, d, false, s));
-  TRY_HIP(bias_residual(m->x, m->y, m->P(L.fc2_b), rows, d, s), "bias_residual");
+  // the residual add, fused with the next LayerNorm: layer l+1's LayerNorm 1, or after the
+  // last layer the final LayerNorm (decode; the prefill normalises only the gathered rows)
+  const bf16 *nw = nullptr, *nb = nullptr;
+  if (l + 1 < c.n_layers) {
+    nw = m->P(m->off.layers[l + 1].ln1_w);
+    nb = m->P(m->off.layers[l + 1].ln1_b);
+  } else if (!prefill) {
+    nw = m->P(m->off.lnf_w);
+    nb = m->P(m->off.lnf_b);
+  }
+  TRY_HIP(residual_layernorm(m->x, m->y, m->P(L.fc2_b), m->h, nw, nb, rows, d, s),
+          "residual_layernorm");
   return DADGPT_OK;
 }
 
-// Final LayerNorm of n rows at xs, weight-tied logits, greedy pick of step `step`.
-int head(dadgpt_gpt2* m, const float* xs, int n, int step) {
+// LayerNorm 1 of layer 0 over freshly embedded rows.
+int first_layernorm(dadgpt_gpt2* m, int rows) {
+  const auto& L0 = m->off.layers[0];
+  return check_hip(residual_layernorm(m->x, nullptr, nullptr, m->h, m->P(L0.ln1_w),
+                                      m->P(L0.ln1_b), rows, m->c.d_model, m->stream),
+                   "residual_layernorm");
+}
+
+// Weight-tied logits of the n final-LayerNorm rows in m->h, greedy pick (stored at the step
+// the device state implies).
+int head(dadgpt_gpt2* m, int n) {
   const auto& c = m->c;
   hipStream_t s = m->stream;
-  TRY_HIP(layernorm(m->h, xs, m->P(m->off.lnf_w), m->P(m->off.lnf_b), n, c.d_model, s),
-          "layernorm");
   TRY(gemm(m->blas, m->logits, m->h, m->P(m->off.tok_emb), n, c.d_model, c.vocab_size, true, s));
   TRY_HIP(argmax_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
-                         m->logits, n, c.vocab_size, step, 1, s),
+                         m->lens, m->logits, m->pick, n, c.vocab_size, s),
           "argmax_advance");
+  return DADGPT_OK;
+}
+
+// One decode step for n sequences: embed each sequence's last token at its position, the
+// blocks, the head. Everything it reads and advances is device state, so a captured copy
+// replays for every step.
+int decode_step(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
+  const auto& c = m->c;
+  TRY_HIP(embed(m->x, m->cur_tok, m->cur_pos, m->P(m->off.tok_emb), m->P(m->off.pos_emb), n, 1,
+                c.d_model, m->stream),
+          "embed");
+  TRY(first_layernorm(m, n));
+  for (int l = 0; l < c.n_layers; ++l)
+    TRY(block(m, l, n, 1, false, attn_ev ? attn_ev + 2 * l : nullptr));
+  return head(m, n);
+}
+
+// The captured decode step for batch size n (captured on first use; hipBLASLt plans must
+// already exist, so the caller runs one eager step first).
+int step_graph(dadgpt_gpt2* m, int n, hipGraphExec_t* out) {
+  auto it = m->graphs.find(n);
+  if (it != m->graphs.end()) {
+    *out = it->second;
+    return DADGPT_OK;
+  }
+  hipGraph_t graph = nullptr;
+  TRY_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal),
+          "hipStreamBeginCapture");
+  const int st = decode_step(m, n, nullptr);
+  const hipError_t e = hipStreamEndCapture(m->stream, &graph);
+  if (st) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return st;
+  }
+  TRY_HIP(e, "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  TRY_HIP(ei, "hipGraphInstantiate");
+  m->graphs[n] = exec;
+  *out = exec;
   return DADGPT_OK;
 }
 
@@ -333,6 +395,7 @@ void dadgpt_gpt2_destroy(dadgpt_gpt2* m) {
   if (!m) return;
   if (m->stream) (void)hipStreamSynchronize(m->stream);
   for (hipEvent_t e : m->events) (void)hipEventDestroy(e);
+  for (auto& [n, g] : m->graphs) (void)hipGraphExecDestroy(g);
   for (void* p : m->allocs) (void)hipFree(p);
   if (m->blas) dadgpt_blas_destroy(m->blas);
   if (m->stream) (void)hipStreamDestroy(m->stream);
@@ -341,9 +404,10 @@ void dadgpt_gpt2_destroy(dadgpt_gpt2* m) {
 
 int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params, int max_batch,
                        int attn_fp32, dadgpt_gpt2** out) {
-  if (!out || !params || !config_ok(config) || max_batch < 1)
+  if (!out || !params || !config_ok(config) || max_batch < 1 || config->d_model > 2048)
     return fail(DADGPT_ERR_INVALID_ARGUMENT,
-                "dadgpt_gpt2_create: bad arguments (d_head must be 32 or 64, max_batch >= 1)");
+                "dadgpt_gpt2_create: bad arguments (d_head must be 32 or 64, d_model <= 2048, "
+                "max_batch >= 1)");
   *out = nullptr;
   auto* m = new dadgpt_gpt2();
   m->c = *config;
@@ -393,6 +457,7 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       (st = m->alloc_n(&m->f, rows * c.d_ff, "fc1 out")) ||
       (st = m->alloc_n(&m->xl, (size_t)max_batch * d, "last rows")) ||
       (st = m->alloc_n(&m->logits, (size_t)max_batch * c.vocab_size, "logits")) ||
+      (st = m->alloc_n(&m->pick, pick_scratch_floats(max_batch), "pick scratch")) ||
       (st = m->alloc_n(&m->lse, rows * c.n_heads, "lse")) ||
       (st = m->alloc_n(&m->h, rows * d, "ln out")) || (st = m->alloc_n(&m->a, rows * d, "attn in")) ||
       (st = m->alloc_n(&m->g, rows * c.d_ff, "gelu out")) ||
@@ -407,7 +472,9 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       (st = m->alloc_n(&m->lens, max_batch, "lens")) ||
       (st = m->alloc_n(&m->cur_tok, max_batch, "cur_tok")) ||
       (st = m->alloc_n(&m->cur_pos, max_batch, "cur_pos")) ||
-      (st = m->alloc_n(&m->cache_len, max_batch, "cache_len")))
+      (st = m->alloc_n(&m->cache_len, max_batch, "cache_len")) ||
+      (st = m->alloc_n(&m->out_tok, rows, "tokens out")) ||
+      (st = m->alloc_n(&m->out_margin, rows, "margins out")))
     return bail(st);
   m->ws_bytes = dadgpt_decode_workspace_bytes(max_batch, c.n_heads, c.ctx_len, m->dh);
   if (m->ws_bytes) {
@@ -423,6 +490,12 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       hipStreamSynchronize(m->stream) != hipSuccess)
     return bail(fail(DADGPT_ERR_HIP, "dadgpt_gpt2_create: initial copies failed"));
   *out = m;
+  return DADGPT_OK;
+}
+
+int dadgpt_gpt2_set_graphs(dadgpt_gpt2* m, int enable) {
+  if (!m) return fail(DADGPT_ERR_INVALID_ARGUMENT, "dadgpt_gpt2_set_graphs: null model");
+  m->use_graphs = enable != 0;
   return DADGPT_OK;
 }
 
@@ -453,21 +526,7 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
     S = len > S ? len : S;
   }
   hipStream_t s = m->stream;
-  const size_t outs = (size_t)new_tokens * n;
-  if (outs > m->out_cap) {
-    if (m->out_tok) {
-      (void)hipStreamSynchronize(s);
-      (void)hipFree(m->out_tok);
-      (void)hipFree(m->out_margin);
-      m->out_tok = nullptr;
-      m->out_margin = nullptr;
-      m->out_cap = 0;
-    }
-    if (hipMalloc(&m->out_tok, outs * sizeof(int)) != hipSuccess ||
-        hipMalloc(&m->out_margin, outs * sizeof(float)) != hipSuccess)
-      return fail(DADGPT_ERR_HIP, "%s: hipMalloc of the outputs failed", fn);
-    m->out_cap = outs;
-  }
+  const size_t outs = (size_t)new_tokens * n;  // <= ctx_len * max_batch, the buffers' size
 
   // padded prompt rows, lengths, and the position before the first generated token
   std::vector<int> tok((size_t)n * S, 0), len(prompt_lens, prompt_lens + n), pos(n);
@@ -486,7 +545,7 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
 
   const int steps = new_tokens - 1;
   const bool timed = timing != nullptr;
-  if (timed) TRY(ensure_events(m, 3 + 2 * (size_t)steps * c.n_layers));
+  if (timed) TRY(ensure_events(m, 3 + (m->use_graphs ? 0 : 2 * (size_t)steps * c.n_layers)));
   hipEvent_t* ev = m->events.data();
   if (timed) TRY_HIP(hipEventRecord(ev[0], s), "hipEventRecord");
 
@@ -494,21 +553,28 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
   TRY_HIP(embed(m->x, m->tok_in, m->pos0, m->P(m->off.tok_emb), m->P(m->off.pos_emb), n, S,
                 c.d_model, s),
           "embed");
+  TRY(first_layernorm(m, n * S));
   for (int l = 0; l < c.n_layers; ++l) TRY(block(m, l, n, S, true, nullptr));
   TRY_HIP(gather_last(m->xl, m->x, m->lens, n, S, c.d_model, s), "gather_last");
-  TRY(head(m, m->xl, n, 0));
+  TRY_HIP(residual_layernorm(m->xl, nullptr, nullptr, m->h, m->P(m->off.lnf_w),
+                             m->P(m->off.lnf_b), n, c.d_model, s),
+          "residual_layernorm");
+  TRY(head(m, n));
   if (timed) TRY_HIP(hipEventRecord(ev[1], s), "hipEventRecord");
   if (logits) TRY(copy_logits(m, logits, n, 0));
 
   // ---- decode: feed token t-1 at its position, pick token t ----
+  // With graphs, step 1 runs eagerly (it builds any missing hipBLASLt plan) and every later
+  // step replays the captured step. Without graphs, timing brackets each attention launch.
+  const bool attn_events = timed && !m->use_graphs;
   for (int t = 1; t <= steps; ++t) {
-    TRY_HIP(embed(m->x, m->cur_tok, m->cur_pos, m->P(m->off.tok_emb), m->P(m->off.pos_emb), n,
-                  1, c.d_model, s),
-            "embed");
-    for (int l = 0; l < c.n_layers; ++l)
-      TRY(block(m, l, n, 1, false,
-                timed ? ev + 3 + 2 * ((size_t)(t - 1) * c.n_layers + l) : nullptr));
-    TRY(head(m, m->x, n, t));
+    if (m->use_graphs && t > 1) {
+      hipGraphExec_t g = nullptr;
+      TRY(step_graph(m, n, &g));
+      TRY_HIP(hipGraphLaunch(g, s), "hipGraphLaunch");
+    } else {
+      TRY(decode_step(m, n, attn_events ? ev + 3 + 2 * (size_t)(t - 1) * c.n_layers : nullptr));
+    }
     if (logits) TRY(copy_logits(m, logits, n, t));
   }
   if (timed) TRY_HIP(hipEventRecord(ev[2], s), "hipEventRecord");
@@ -534,11 +600,11 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
     TRY_HIP(hipEventElapsedTime(&ms, ev[1], ev[2]), "hipEventElapsedTime");
     timing->decode_ms = logits ? NAN : ms;  // per-step host copies would be counted
     double attn = 0.0;
-    for (size_t i = 0; i < (size_t)steps * c.n_layers; ++i) {
+    for (size_t i = 0; attn_events && i < (size_t)steps * c.n_layers; ++i) {
       TRY_HIP(hipEventElapsedTime(&ms, ev[3 + 2 * i], ev[4 + 2 * i]), "hipEventElapsedTime");
       attn += ms;
     }
-    timing->decode_attn_ms = (float)attn;
+    timing->decode_attn_ms = attn_events ? (float)attn : -1.0f;
   }
   return DADGPT_OK;
 }

@@ -55,25 +55,58 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// One wave per row, four rows per block.
-__global__ __launch_bounds__(256) void layernorm_kernel(bf16* out, const float* x,
-                                                        const bf16* w, const bf16* b, int rows,
-                                                        int d) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  const float* xr = x + (size_t)row * d;
+// Sum over the 256 threads of a block (4 waves): wave shuffles, then the 4 partials via LDS.
+__device__ __forceinline__ float block_sum(float v, float* sm) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();  // sm may still be read from a previous reduction
+  if (lane == 0) sm[wave] = v;
+  __syncthreads();
+  return sm[0] + sm[1] + sm[2] + sm[3];
+}
+
+constexpr int kLnMaxPerThread = 8;  // d <= 2048
+
+// One row per 256-thread block, the row held in registers: optionally x += y + bias (the
+// residual add of the previous projection), then out = bf16(LayerNorm(x) * w + b) with
+// eps 1e-5 and two-pass mean and variance in fp32 (src/tensor_ops.cpp:57-84). w == nullptr:
+// residual only.
+__global__ __launch_bounds__(256) void residual_layernorm_kernel(float* x, const float* y,
+                                                                 const bf16* bias, bf16* out,
+                                                                 const bf16* w, const bf16* b,
+                                                                 int d) {
+  __shared__ float sm[4];
+  float* xr = x + (size_t)blockIdx.x * d;
+  float v[kLnMaxPerThread];
   float sum = 0.f;
-  for (int c = lane; c < d; c += 64) sum += xr[c];
-  const float mean = wave_sum(sum) / (float)d;
-  float sq = 0.f;
-  for (int c = lane; c < d; c += 64) {
-    const float diff = xr[c] - mean;
-    sq += diff * diff;
+#pragma unroll
+  for (int i = 0; i < kLnMaxPerThread; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    v[i] = 0.f;
+    if (c < d) {
+      v[i] = xr[c];
+      if (y) {
+        v[i] += y[(size_t)blockIdx.x * d + c] + (float)bias[c];
+        xr[c] = v[i];
+      }
+      sum += v[i];
+    }
   }
-  const float inv_std = 1.0f / sqrtf(wave_sum(sq) / (float)d + 1e-5f);
-  bf16* orow = out + (size_t)row * d;
-  for (int c = lane; c < d; c += 64)
-    orow[c] = static_cast<bf16>((xr[c] - mean) * inv_std * (float)w[c] + (float)b[c]);
+  if (!w) return;
+  const float mean = block_sum(sum, sm) / (float)d;
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < kLnMaxPerThread; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c < d) sq += (v[i] - mean) * (v[i] - mean);
+  }
+  const float inv_std = 1.0f / sqrtf(block_sum(sq, sm) / (float)d + 1e-5f);
+  bf16* orow = out + (size_t)blockIdx.x * d;
+#pragma unroll
+  for (int i = 0; i < kLnMaxPerThread; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c < d) orow[c] = static_cast<bf16>((v[i] - mean) * inv_std * (float)w[c] + (float)b[c]);
+  }
 }
 
 template <typename T>
@@ -118,14 +151,6 @@ __global__ void to_bf16_kernel(bf16* out, const float* in, size_t count) {
     out[i] = static_cast<bf16>(in[i]);
 }
 
-__global__ void bias_residual_kernel(float* x, const float* y, const bf16* bias, int rows,
-                                     int cols) {
-  const size_t n = (size_t)rows * cols;
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-       i += (size_t)gridDim.x * blockDim.x)
-    x[i] += y[i] + (float)bias[i % cols];
-}
-
 // GELU, tanh form (cuda/gpu_ops.cu:250-256, src/tensor_ops.cpp:86-95).
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
@@ -161,16 +186,19 @@ __device__ __forceinline__ Pick combine(Pick a, Pick b) {
   return Pick{w.v1, w.i1, fmaxf(l.v1, w.v2)};
 }
 
-__global__ __launch_bounds__(256) void argmax_advance_kernel(int* tokens, float* margins,
-                                                             int* tok, int* pos, int* cache_len,
-                                                             const float* logits, int n, int V,
-                                                             int step, int advance) {
+constexpr int kPickParts = 32;  // blocks per row in the first stage of the greedy pick
+
+// Stage 1: block (b, part) reduces a contiguous slice of row b to one candidate.
+__global__ __launch_bounds__(256) void pick_partial_kernel(float* pv1, int* pi1, float* pv2,
+                                                           const float* logits, int V) {
   __shared__ float s_v1[256], s_v2[256];
   __shared__ int s_i1[256];
-  const int b = blockIdx.x, t = threadIdx.x;
+  const int b = blockIdx.x, part = blockIdx.y, t = threadIdx.x;
+  const int span = (V + kPickParts - 1) / kPickParts;
+  const int lo = part * span, hi = min(V, lo + span);
   const float* row = logits + (size_t)b * V;
   Pick p{-__builtin_inff(), 0x7fffffff, -__builtin_inff()};
-  for (int v = t; v < V; v += 256) p = combine(p, Pick{row[v], v, -__builtin_inff()});
+  for (int v = lo + t; v < hi; v += 256) p = combine(p, Pick{row[v], v, -__builtin_inff()});
   s_v1[t] = p.v1;
   s_i1[t] = p.i1;
   s_v2[t] = p.v2;
@@ -186,11 +214,40 @@ __global__ __launch_bounds__(256) void argmax_advance_kernel(int* tokens, float*
     __syncthreads();
   }
   if (t == 0) {
-    const int pick = s_i1[0];
-    tokens[(size_t)step * n + b] = pick;
-    margins[(size_t)step * n + b] = s_v1[0] - s_v2[0];
-    tok[b] = pick;
-    pos[b] += advance;
+    const int k = b * kPickParts + part;
+    pv1[k] = s_v1[0];
+    pi1[k] = s_i1[0];
+    pv2[k] = s_v2[0];
+  }
+}
+
+// Stage 2: one wave per row merges the row's candidates, stores the pick and advances.
+__global__ __launch_bounds__(64) void pick_final_kernel(int* tokens, float* margins, int* tok,
+                                                        int* pos, int* cache_len,
+                                                        const int* prompt_len, const float* pv1,
+                                                        const int* pi1, const float* pv2,
+                                                        int n) {
+  const int b = blockIdx.x, t = threadIdx.x;
+  Pick p{-__builtin_inff(), 0x7fffffff, -__builtin_inff()};
+  if (t < kPickParts) {
+    const int k = b * kPickParts + t;
+    p = Pick{pv1[k], pi1[k], pv2[k]};
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const Pick q{__shfl_xor(p.v1, off, 64), __shfl_xor(p.i1, off, 64),
+                 __shfl_xor(p.v2, off, 64)};
+    p = combine(p, q);
+  }
+  if (t == 0) {
+    // pos[b] is the position of the last token fed: prompt_len-1 for the pick after the
+    // prompt (step 0), prompt_len-1+t for step t. The state lives on the device, so one
+    // captured decode step replays for every t.
+    const int step = pos[b] - (prompt_len[b] - 1);
+    tokens[(size_t)step * n + b] = p.i1;
+    margins[(size_t)step * n + b] = p.v1 - p.v2;
+    tok[b] = p.i1;
+    pos[b] += 1;
     cache_len[b] = pos[b] + 1;
   }
 }
@@ -227,9 +284,10 @@ hipError_t embed(float* x, const int* tok, const int* pos0, const bf16* wte, con
   return hipGetLastError();
 }
 
-hipError_t layernorm(bf16* out, const float* x, const bf16* w, const bf16* b, int rows, int d,
-                     hipStream_t s) {
-  layernorm_kernel<<<(rows + 3) / 4, 256, 0, s>>>(out, x, w, b, rows, d);
+hipError_t residual_layernorm(float* x, const float* y, const bf16* bias, bf16* out,
+                              const bf16* w, const bf16* b, int rows, int d, hipStream_t s) {
+  if (d > 256 * kLnMaxPerThread) return hipErrorInvalidValue;
+  residual_layernorm_kernel<<<rows, 256, 0, s>>>(x, y, bias, out, w, b, d);
   return hipGetLastError();
 }
 
@@ -261,12 +319,6 @@ hipError_t to_bf16(bf16* out, const float* in, size_t count, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t bias_residual(float* x, const float* y, const bf16* bias, int rows, int cols,
-                         hipStream_t s) {
-  bias_residual_kernel<<<grid_for((size_t)rows * cols), 256, 0, s>>>(x, y, bias, rows, cols);
-  return hipGetLastError();
-}
-
 hipError_t bias_gelu(bf16* out, const float* y, const bf16* bias, int rows, int cols,
                      hipStream_t s) {
   bias_gelu_kernel<<<grid_for((size_t)rows * cols), 256, 0, s>>>(out, y, bias, rows, cols);
@@ -279,11 +331,18 @@ hipError_t gather_last(float* out, const float* x, const int* len, int n, int S,
   return hipGetLastError();
 }
 
+size_t pick_scratch_floats(int n) { return (size_t)3 * n * kPickParts; }
+
 hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
-                          const float* logits, int n, int V, int step, int advance,
-                          hipStream_t s) {
-  argmax_advance_kernel<<<n, 256, 0, s>>>(tokens, margins, tok, pos, cache_len, logits, n, V,
-                                          step, advance);
+                          const int* prompt_len, const float* logits, float* scratch, int n,
+                          int V, hipStream_t s) {
+  float* pv1 = scratch;
+  int* pi1 = reinterpret_cast<int*>(scratch + (size_t)n * kPickParts);
+  float* pv2 = scratch + (size_t)2 * n * kPickParts;
+  pick_partial_kernel<<<dim3(n, kPickParts), 256, 0, s>>>(pv1, pi1, pv2, logits, V);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  pick_final_kernel<<<n, 64, 0, s>>>(tokens, margins, tok, pos, cache_len, prompt_len, pv1, pi1,
+                                     pv2, n);
   return hipGetLastError();
 }
 

@@ -36,6 +36,7 @@ GEN_SYMBOLS = (
     "dadgpt_gpt2_init_params",
     "dadgpt_gpt2_create",
     "dadgpt_gpt2_destroy",
+    "dadgpt_gpt2_set_graphs",
     "dadgpt_gpt2_generate",
 )
 
@@ -91,6 +92,7 @@ def gen_lib():
     L.dadgpt_gpt2_create.argtypes = [cfgp, vp, i, i, ctypes.POINTER(vp)]
     L.dadgpt_gpt2_destroy.argtypes = [vp]
     L.dadgpt_gpt2_destroy.restype = None
+    L.dadgpt_gpt2_set_graphs.argtypes = [vp, i]
     L.dadgpt_gpt2_generate.argtypes = [vp, vp, vp, i, i, i, vp, vp, vp, ctypes.POINTER(Timing)]
     for name in GEN_SYMBOLS:
         if name not in ("dadgpt_gen_last_error", "dadgpt_blas_destroy", "dadgpt_gpt2_destroy",
@@ -194,6 +196,10 @@ class GPT2:
             self._m = ctypes.c_void_p()
 
     __del__ = close
+
+    def set_graphs(self, enable: bool) -> None:
+        """Replay a captured decode step (default) or launch every step eagerly."""
+        _check(gen_lib().dadgpt_gpt2_set_graphs(self._m, int(enable)))
 
     def generate(self, prompts, new_tokens: int, logits: bool = False, timing: bool = False):
         """prompts: list of 1-D int sequences. Returns a dict with tokens [n, new_tokens]

@@ -38,7 +38,8 @@ typedef struct dadgpt_gpt2 dadgpt_gpt2;
 typedef struct dadgpt_gpt2_timing {
   float prefill_ms;      /* the batched prefill, through the first greedy pick */
   float decode_ms;       /* all decode steps */
-  float decode_attn_ms;  /* the decode-attention launches inside those steps */
+  float decode_attn_ms;  /* the decode-attention launches inside those steps (measured with
+                            graphs off only: -1 with graphs on) */
   int decode_steps;
 } dadgpt_gpt2_timing;
 
@@ -62,6 +63,12 @@ int dadgpt_gpt2_init_params(uint16_t* params, const dadgpt_gpt2_config* config, 
 int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params, int max_batch,
                        int attn_fp32, dadgpt_gpt2** out);
 void dadgpt_gpt2_destroy(dadgpt_gpt2* model);
+
+/* Decode steps after the first replay one captured HIP graph per batch size (default on);
+ * off, every step is launched kernel by kernel (and timing brackets each attention launch).
+ * The replayed step reads all per-step state (tokens, positions, cache lengths) from device
+ * memory, so it is the same work as the eager step. */
+int dadgpt_gpt2_set_graphs(dadgpt_gpt2* model, int enable);
 
 /* Greedy generation for n <= max_batch prompts (host arrays):
  *   prompts [n, prompt_stride] int32 token ids, row b holding prompt_lens[b] >= 1 tokens;

@@ -247,6 +247,24 @@ def test_generate_is_deterministic_and_batch_independent(gpu):
 
 
 @pytest.mark.gpu
+def test_graph_replayed_steps_equal_eager_steps(gpu):
+    """The captured decode step, replayed for every step after the first, gives the same
+    tokens and logits as launching each step eagerly; checked over two calls in a row (the
+    second with a smaller batch, so a second graph is captured) with eager work between."""
+    cfg = TINY64
+    case("graph replay vs eager decode steps")
+    model, _ = _gpu_model(cfg, seed=25, max_batch=4)
+    for prompts in (_prompts(cfg, [7, 30, 2, 15], 700), _prompts(cfg, [11, 4], 800)):
+        g = model.generate(prompts, 9, logits=True)
+        model.set_graphs(False)
+        e = model.generate(prompts, 9, logits=True)
+        model.set_graphs(True)
+        np.testing.assert_array_equal(g["tokens"], e["tokens"])
+        np.testing.assert_array_equal(g["logits"], e["logits"])
+    model.close()
+
+
+@pytest.mark.gpu
 def test_generate_rejects_overflowing_context(gpu):
     from dadgpt_amd import attention as A
 
