@@ -18,6 +18,7 @@ the decode-attention time share, and the comparison with fp32 attention.
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-generate]
     python bench.py --profile-sample     # each kernel --reps times + a copy of known size,
                                          # for rocprofv3 --pmc runs; prints no bench line
+    python bench.py --generate-only      # the config 5 leg alone (for rocprofv3)
 """
 from __future__ import annotations
 
@@ -63,6 +64,8 @@ def parse():
     p.add_argument("--cpu-slices", type=int, default=24)
     p.add_argument("--profile-sample", action="store_true")
     p.add_argument("--no-generate", action="store_true", help="skip the config 5 leg")
+    p.add_argument("--generate-only", action="store_true",
+                   help="run only the config 5 leg (for profiling); prints no bench line")
     p.add_argument("--prewarm-seconds", type=float, default=2.0,
                    help="untimed fwd+bwd steps before the warmup, so clocks have ramped")
     return p.parse_args()
@@ -286,6 +289,9 @@ def main():
 
     import torch
 
+    if args.generate_only:
+        generate_cfg5()
+        return
     wl = Workload(args.decode_copies)
     wl.A.lib()
     if args.profile_sample:
