@@ -31,11 +31,12 @@ hipError_t fill(bf16* p, size_t n, float value, hipStream_t s);
 hipError_t embed(float* x, const int* tok, const int* pos0, const bf16* wte, const bf16* wpe,
                  int n, int S, int d, hipStream_t s);
 
-// Per row (d <= 2048): if y, x[r] += y[r] + bias (the residual add of a projection); then,
-// if w, out[r] = bf16(LayerNorm(x[r]) * w + b) with eps 1e-5 (two-pass mean and variance,
-// fp32).
+// Per row (d <= 2048): if y, x[r] += sum_{s < splits} y[s][r] + bias (the residual add of a
+// projection, y holding `splits` partial sums [splits][rows][d]); then, if w,
+// out[r] = bf16(LayerNorm(x[r]) * w + b) with eps 1e-5 (two-pass mean and variance, fp32).
 hipError_t residual_layernorm(float* x, const float* y, const bf16* bias, bf16* out,
-                              const bf16* w, const bf16* b, int rows, int d, hipStream_t s);
+                              const bf16* w, const bf16* b, int rows, int d, hipStream_t s,
+                              int splits = 1);
 
 // qkv [n*S, 3d] fp32 (+ bias bqkv [3d] fp32): q -> qh [n*H, S, dh]; k, v -> kh, vh
 // [n*H, S, dh] when kh is not null; k, v of the rows s < nvalid[b] -> caches
@@ -70,6 +71,30 @@ size_t pick_scratch_floats(int n);
 hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
                           const int* prompt_len, const float* logits, float* scratch, int n,
                           int V, hipStream_t s);
+
+// ---- skinny projections of the decode step (skinny.hip) ----
+
+enum SkinnyPrologue { kProRows = 0, kProLayerNorm = 1, kProGelu = 2 };
+
+struct SkinnyArgs {
+  float* parts;             // out [K/kc][M][N] fp32: one partial sum per K-chunk
+  const bf16* wt;           // W^T [N][K]
+  int M, N, K, kc;          // rows (<= 16), columns, reduction length, K-chunk (K % kc == 0)
+  const bf16* act;          // kProRows: A [M][K]
+  const float* x_in;        // kProLayerNorm: residual stream [M][K]
+  const float* in_parts;    // kProLayerNorm / kProGelu: [in_splits][M][K] partial sums
+  int in_splits;
+  const bf16* in_bias;      // [K] (optional for kProLayerNorm)
+  const bf16* ln_w;         // kProLayerNorm: LayerNorm weight and bias [K]
+  const bf16* ln_b;
+  float* x_out;             // kProLayerNorm: x + parts + bias stored here (optional)
+};
+
+bool skinny_supported(int M, int K);
+int skinny_chunk(int K);  // the K-chunk a K-long reduction uses (<= 768, divides K)
+hipError_t skinny_gemm(int prologue, const SkinnyArgs& args, hipStream_t s);
+// out [cols][rows] = in [rows][cols]^T (bf16)
+hipError_t transpose(bf16* out, const bf16* in, int rows, int cols, hipStream_t s);
 
 // bqkv [3d] fp32 <- (bq, bk, bv) bf16.
 hipError_t pack_bias(float* bqkv, const bf16* bq, const bf16* bk, const bf16* bv, int d,

@@ -127,6 +127,12 @@ struct dadgpt_gpt2 {
 
   std::vector<bf16*> wqkv;   // per layer [d, 3d]
   std::vector<float*> bqkv;  // per layer [3d]
+  // decode steps of at most 16 sequences (d_model <= 768): transposed weights for the skinny
+  // projections, the second residual buffer, and the fc2 partial sums
+  bool skinny = false;
+  std::vector<bf16*> wqkv_t, wo_t, w1_t, w2_t;  // [3d, d], [d, d], [d_ff, d], [d, d_ff]
+  float *xb = nullptr, *parts2 = nullptr;
+  int fc2_splits = 1;
   std::vector<void*> kc, vc;  // per layer [max_batch, H, ctx, dh]
 
   float *x = nullptr, *qkv = nullptr, *y = nullptr, *f = nullptr, *xl = nullptr;
@@ -289,7 +295,10 @@ int head(dadgpt_gpt2* m, int n) {
 // One decode step for n sequences: embed each sequence's last token at its position, the
 // blocks, the head. Everything it reads and advances is device state, so a captured copy
 // replays for every step.
+int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev);
+
 int decode_step(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
+  if (m->skinny && n <= 16) return decode_step_skinny(m, n, attn_ev);
   const auto& c = m->c;
   TRY_HIP(embed(m->x, m->cur_tok, m->cur_pos, m->P(m->off.tok_emb), m->P(m->off.pos_emb), n, 1,
                 c.d_model, m->stream),
@@ -298,6 +307,97 @@ int decode_step(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   for (int l = 0; l < c.n_layers; ++l)
     TRY(block(m, l, n, 1, false, attn_ev ? attn_ev + 2 * l : nullptr));
   return head(m, n);
+}
+
+// The decode step on the skinny projections (n <= 16 sequences). Per layer 6 dependent
+// launches: QKV (LayerNorm 1 of x + previous fc2 partials + bias in its prologue) -> QKV split
+// + cache append -> decode attention -> Wo -> fc1 (residual add + LayerNorm 2 in its
+// prologue) -> fc2 (bias + GELU of fc1 in its prologue, partial sums out). The residual
+// stream alternates between m->x and m->xb.
+int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
+  const auto& c = m->c;
+  const int d = c.d_model, H = c.n_heads, dh = m->dh;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(dh));  // src/model.cpp:389
+  hipStream_t s = m->stream;
+  TRY_HIP(embed(m->x, m->cur_tok, m->cur_pos, m->P(m->off.tok_emb), m->P(m->off.pos_emb), n, 1,
+                d, s),
+          "embed");
+  for (int l = 0; l < c.n_layers; ++l) {
+    const auto& L = m->off.layers[l];
+    SkinnyArgs q{};
+    q.parts = m->qkv;
+    q.wt = m->wqkv_t[l];
+    q.M = n, q.N = 3 * d, q.K = d, q.kc = skinny_chunk(d);
+    q.x_in = m->x;
+    if (l > 0) {
+      q.in_parts = m->parts2;
+      q.in_splits = m->fc2_splits;
+      q.in_bias = m->P(m->off.layers[l - 1].fc2_b);
+    }
+    q.ln_w = m->P(L.ln1_w), q.ln_b = m->P(L.ln1_b);
+    q.x_out = m->xb;
+    TRY_HIP(skinny_gemm(kProLayerNorm, q, s), "skinny QKV");
+    const bf16* attn_in = m->a;
+    if (m->fp32)
+      TRY_HIP(qkv_split<float>((float*)m->qh, nullptr, nullptr, (float*)m->kc[l],
+                               (float*)m->vc[l], m->qkv, m->bqkv[l], m->cur_pos, m->ones, n, 1,
+                               H, dh, c.ctx_len, s),
+              "qkv_split");
+    else
+      TRY_HIP(qkv_split<bf16>((bf16*)m->qh, nullptr, nullptr, (bf16*)m->kc[l], (bf16*)m->vc[l],
+                              m->qkv, m->bqkv[l], m->cur_pos, m->ones, n, 1, H, dh, c.ctx_len,
+                              s),
+              "qkv_split");
+    if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[2 * l], s), "hipEventRecord");
+    if (int st = attention_decode(m, l, n, scale)) return attn_fail(st, "decode attention");
+    if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[2 * l + 1], s), "hipEventRecord");
+    if (m->fp32)
+      TRY_HIP(to_bf16(m->a, (const float*)m->ao, (size_t)n * d, s), "to_bf16");
+    else
+      attn_in = (const bf16*)m->ao;
+
+    SkinnyArgs o{};
+    o.parts = m->y;
+    o.wt = m->wo_t[l];
+    o.M = n, o.N = d, o.K = d, o.kc = skinny_chunk(d);
+    o.act = attn_in;
+    TRY_HIP(skinny_gemm(kProRows, o, s), "skinny Wo");
+
+    SkinnyArgs f1{};
+    f1.parts = m->f;
+    f1.wt = m->w1_t[l];
+    f1.M = n, f1.N = c.d_ff, f1.K = d, f1.kc = skinny_chunk(d);
+    f1.x_in = m->xb;
+    f1.in_parts = m->y;
+    f1.in_splits = d / o.kc;
+    f1.in_bias = m->P(L.bo);
+    f1.ln_w = m->P(L.ln2_w), f1.ln_b = m->P(L.ln2_b);
+    f1.x_out = m->x;
+    TRY_HIP(skinny_gemm(kProLayerNorm, f1, s), "skinny fc1");
+
+    SkinnyArgs f2{};
+    f2.parts = m->parts2;
+    f2.wt = m->w2_t[l];
+    f2.M = n, f2.N = d, f2.K = c.d_ff, f2.kc = skinny_chunk(c.d_ff);
+    f2.in_parts = m->f;
+    f2.in_splits = d / f1.kc;
+    f2.in_bias = m->P(L.fc1_b);
+    TRY_HIP(skinny_gemm(kProGelu, f2, s), "skinny fc2");
+  }
+  // residual add of the last fc2 and the final LayerNorm, then the tied logits
+  TRY_HIP(residual_layernorm(m->x, m->parts2, m->P(m->off.layers[c.n_layers - 1].fc2_b), m->h,
+                             m->P(m->off.lnf_w), m->P(m->off.lnf_b), n, d, s, m->fc2_splits),
+          "residual_layernorm");
+  SkinnyArgs lg{};
+  lg.parts = m->logits;
+  lg.wt = m->P(m->off.tok_emb);  // [V, d]: already W^T of the tied projection
+  lg.M = n, lg.N = c.vocab_size, lg.K = d, lg.kc = skinny_chunk(d);
+  lg.act = m->h;
+  TRY_HIP(skinny_gemm(kProRows, lg, s), "skinny logits");
+  TRY_HIP(argmax_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
+                         m->lens, m->logits, m->pick, n, c.vocab_size, s),
+          "argmax_advance");
+  return DADGPT_OK;
 }
 
 // The captured decode step for batch size n (captured on first use; hipBLASLt plans must
@@ -476,6 +576,38 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       (st = m->alloc_n(&m->out_tok, rows, "tokens out")) ||
       (st = m->alloc_n(&m->out_margin, rows, "margins out")))
     return bail(st);
+  // the skinny decode path: one K-chunk for every reduction over d_model (so the QKV, Wo,
+  // fc1 and logits projections write a single partial), d_ff a multiple of 32
+  m->skinny = c.d_model <= 768 && skinny_chunk(c.d_model) == c.d_model &&
+              skinny_supported(1, c.d_model) && skinny_supported(1, c.d_ff);
+  if (m->skinny) {
+    m->fc2_splits = c.d_ff / skinny_chunk(c.d_ff);
+    const int nb = max_batch < 16 ? max_batch : 16;
+    m->wqkv_t.resize(c.n_layers);
+    m->wo_t.resize(c.n_layers);
+    m->w1_t.resize(c.n_layers);
+    m->w2_t.resize(c.n_layers);
+    if ((st = m->alloc_n(&m->xb, (size_t)nb * d, "residual b")) ||
+        (st = m->alloc_n(&m->parts2, (size_t)m->fc2_splits * nb * d, "fc2 partials")))
+      return bail(st);
+    for (int l = 0; l < c.n_layers; ++l) {
+      const auto& L = m->off.layers[l];
+      if ((st = m->alloc_n(&m->wqkv_t[l], 3 * d * d, "wqkv^T")) ||
+          (st = m->alloc_n(&m->wo_t[l], d * d, "wo^T")) ||
+          (st = m->alloc_n(&m->w1_t[l], (size_t)c.d_ff * d, "fc1^T")) ||
+          (st = m->alloc_n(&m->w2_t[l], (size_t)d * c.d_ff, "fc2^T")))
+        return bail(st);
+      if ((st = check_hip(transpose(m->wqkv_t[l], m->wqkv[l], (int)d, 3 * (int)d, m->stream),
+                          "transpose")) ||
+          (st = check_hip(transpose(m->wo_t[l], m->P(L.Wo), (int)d, (int)d, m->stream),
+                          "transpose")) ||
+          (st = check_hip(transpose(m->w1_t[l], m->P(L.fc1_w), (int)d, c.d_ff, m->stream),
+                          "transpose")) ||
+          (st = check_hip(transpose(m->w2_t[l], m->P(L.fc2_w), c.d_ff, (int)d, m->stream),
+                          "transpose")))
+        return bail(st);
+    }
+  }
   m->ws_bytes = dadgpt_decode_workspace_bytes(max_batch, c.n_heads, c.ctx_len, m->dh);
   if (m->ws_bytes) {
     if ((st = m->alloc(&m->ws, m->ws_bytes, "decode workspace"))) return bail(st);

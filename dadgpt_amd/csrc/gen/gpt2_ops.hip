@@ -74,7 +74,7 @@ constexpr int kLnMaxPerThread = 8;  // d <= 2048
 __global__ __launch_bounds__(256) void residual_layernorm_kernel(float* x, const float* y,
                                                                  const bf16* bias, bf16* out,
                                                                  const bf16* w, const bf16* b,
-                                                                 int d) {
+                                                                 int d, int splits) {
   __shared__ float sm[4];
   float* xr = x + (size_t)blockIdx.x * d;
   float v[kLnMaxPerThread];
@@ -86,7 +86,9 @@ __global__ __launch_bounds__(256) void residual_layernorm_kernel(float* x, const
     if (c < d) {
       v[i] = xr[c];
       if (y) {
-        v[i] += y[(size_t)blockIdx.x * d + c] + (float)bias[c];
+        for (int sp = 0; sp < splits; ++sp)
+          v[i] += y[((size_t)sp * gridDim.x + blockIdx.x) * d + c];
+        v[i] += (float)bias[c];
         xr[c] = v[i];
       }
       sum += v[i];
@@ -285,9 +287,10 @@ hipError_t embed(float* x, const int* tok, const int* pos0, const bf16* wte, con
 }
 
 hipError_t residual_layernorm(float* x, const float* y, const bf16* bias, bf16* out,
-                              const bf16* w, const bf16* b, int rows, int d, hipStream_t s) {
+                              const bf16* w, const bf16* b, int rows, int d, hipStream_t s,
+                              int splits) {
   if (d > 256 * kLnMaxPerThread) return hipErrorInvalidValue;
-  residual_layernorm_kernel<<<rows, 256, 0, s>>>(x, y, bias, out, w, b, d);
+  residual_layernorm_kernel<<<rows, 256, 0, s>>>(x, y, bias, out, w, b, d, splits);
   return hipGetLastError();
 }
 
