@@ -250,8 +250,8 @@ def generate_cfg5():
     total_ms = t["prefill_ms"] + t["decode_ms"]
     out = {
         "config": "GPT-2 124M arch (d768 L12 H12 ff3072 ctx1024 V50257), random init, 16 "
-                  "prompts len U[16,256], 128 greedy tokens, bf16 attention + bf16 hipBLASLt "
-                  "projections, fp32 residual",
+                  "prompts len U[16,256], 128 greedy tokens, bf16 attention, bf16 projections "
+                  "(hipBLASLt prefill, skinny MFMA decode), fp32 residual",
         "tokens": int(GEN_N * GEN_NEW),
         "tokens_per_s": round(GEN_N * GEN_NEW / (total_ms * 1e-3), 1),
         "decode_tokens_per_s": round(GEN_N * t["decode_steps"] / (t["decode_ms"] * 1e-3), 1),

@@ -9,8 +9,10 @@
  * The reference decodes one sequence at a time with 2*H cache memcpys and 2*H cuBLAS GEMVs per
  * layer and token. Here the prompts of a batch prefill together (one flash-attention launch per
  * layer over the padded batch, the KV append fused into the QKV split), and every decode step
- * runs one ragged decode-attention launch per layer for the whole batch. Projections are bf16
- * hipBLASLt GEMMs (<dadgpt/gpu_matmul.h>); the residual stream, LayerNorm statistics and
+ * runs one ragged decode-attention launch per layer for the whole batch. Prefill projections
+ * are bf16 hipBLASLt GEMMs (<dadgpt/gpu_matmul.h>); decode projections for batches of up to 16
+ * run on skinny MFMA kernels over pre-transposed weights with the residual add + LayerNorm
+ * and bias + GELU fused into their prologues. The residual stream, LayerNorm statistics and
  * logits are fp32. Attention runs in bf16 (default) or in fp32 (attn_fp32 = 1: fp32 Q/K/V,
  * fp32 caches, the fp32 kernels) with everything else identical.
  *
@@ -57,8 +59,9 @@ int dadgpt_gpt2_init_params(uint16_t* params, const dadgpt_gpt2_config* config, 
                             void* stream);
 
 /* A model over a caller-owned device parameter arena (kept by pointer: it must outlive the
- * model). Allocates the fused QKV weights, the KV caches [max_batch, H, ctx_len, d_head] per
- * layer, activations for max_batch x ctx_len rows, and a hipBLASLt handle. d_head must be 32
+ * model). Allocates the fused QKV weights, transposed copies of the projection weights, the
+ * KV caches [max_batch, H, ctx_len, d_head] per layer, activations for max_batch x ctx_len
+ * rows, and a hipBLASLt handle. d_head must be 32
  * or 64. */
 int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params, int max_batch,
                        int attn_fp32, dadgpt_gpt2** out);
