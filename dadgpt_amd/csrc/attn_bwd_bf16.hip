@@ -84,33 +84,53 @@ __device__ __forceinline__ void store_rows_bf16(bf16* dst, const f32x16 (&acc)[D
 constexpr int kKW = 32;  // keys per wave
 
 // One 32-query block (tile rows 32*qb ..) against the wave's 32 keys. Register 8j+e of lane
-// half hi holds tile query 32qb + 16j + 8hi + e. slse holds the natural-log logsumexp of the
-// tile's queries (converted to log2 units here). MASK zeroes P for keys after the query and
-// for tile rows past S (rows_left = S - r0; those rows hold copies of row S-1).
+// half hi holds tile query 32qb + 16j + 8hi + e. The two score products start from
+// accumulators that already hold the per-query statistics, read from LDS straight into them:
+//   s  = -lse/scale + Q K^T         so P = exp2(c s) with c = scale log2(e)
+//   dp = -delta + dO V^T            so P dp = P (dP - delta) = dS
+// which leaves two multiplies and an exp2 per score on the VALU. slc holds the tile's
+// -lse/scale, sdl its -delta. MASK zeroes P for keys after the query and for tile rows past S
+// (rows_left = S - r0; those rows hold copies of row S-1).
 template <int D, bool MASK>
 __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dvacc)[D / 32],
                                            const bf16x8 (&kop)[D / 16],
                                            const bf16x8 (&vop)[D / 16], const bf16* sq,
-                                           const bf16* sdo, const float* slse,
-                                           const float* sdel, int qb, int key_minus_r0,
-                                           int rows_left, int lane, float scale_log2) {
+                                           const bf16* sdo, const float* slc, const float* sdl,
+                                           int qb, int key_minus_r0, int rows_left, int lane,
+                                           float c) {
   constexpr int DS = D / 16, DB = D / 32;
   const int l32 = lane & 31, hi = lane >> 5;
-  f32x16 s = f32x16{}, dp = f32x16{};
   const int qr = 32 * qb + sigma32(l32);
+  bf16x8 qa[DS], da[DS];
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) {
-    s = mfma32(lds_op(sq, rm_off<D>(qr, 2 * ds + hi)), kop[ds], s);
-    dp = mfma32(lds_op(sdo, rm_off<D>(qr, 2 * ds + hi)), vop[ds], dp);
+    qa[ds] = lds_op(sq, rm_off<D>(qr, 2 * ds + hi));
+    da[ds] = lds_op(sdo, rm_off<D>(qr, 2 * ds + hi));
+  }
+  f32x16 s, dp;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int qt0 = 32 * qb + 16 * j + 8 * hi;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(slc + qt0 + 4 * h);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(sdl + qt0 + 4 * h);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s[8 * j + 4 * h + e] = a[e];
+        dp[8 * j + 4 * h + e] = b[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    s = mfma32(qa[ds], kop[ds], s);
+    dp = mfma32(da[ds], vop[ds], dp);
   }
   bf16x8 pb[2], dsb[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int qt0 = 32 * qb + 16 * j + 8 * hi;
-    const f32x4 la = *reinterpret_cast<const f32x4*>(slse + qt0);
-    const f32x4 lb = *reinterpret_cast<const f32x4*>(slse + qt0 + 4);
-    const f32x4 da = *reinterpret_cast<const f32x4*>(sdel + qt0);
-    const f32x4 dbv = *reinterpret_cast<const f32x4*>(sdel + qt0 + 4);
     u32x4 wp, wd;
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2) {
@@ -118,13 +138,11 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int e = 2 * e2 + h;
-        const float l2 = (e < 4 ? la[e] : lb[e - 4]) * kLog2e;
-        const float de = e < 4 ? da[e] : dbv[e - 4];
-        float pe = fast_exp2(fmaf(s[8 * j + e], scale_log2, -l2));
+        float pe = fast_exp2(s[8 * j + e] * c);
         // key > query (key - r0 > tile query index), or a row past S
         if (MASK) pe = (key_minus_r0 > qt0 + e || qt0 + e >= rows_left) ? 0.f : pe;
         p[h] = pe;
-        d[h] = pe * (dp[8 * j + e] - de);
+        d[h] = pe * dp[8 * j + e];
       }
       wp[e2] = pack_bf16x2(p[0], p[1]);
       wd[e2] = pack_bf16x2(d[0], d[1]);
@@ -133,9 +151,9 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
     dsb[j] = as_bf16x8(wd);
   }
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
+  for (int j = 0; j < 2; ++j) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int db = 0; db < DB; ++db) {
       // A = dO^T / Q^T: lane d = 32db + l32 gets tile queries 32qb + 16j + 8hi + 0..7
       dvacc[db] = mfma32(lds_tr_op<D>(sdo, 32 * qb + 16 * j, 32 * db, lane), pb[j], dvacc[db]);
       dkacc[db] = mfma32(lds_tr_op<D>(sq, 32 * qb + 16 * j, 32 * db, lane), dsb[j], dkacc[db]);
@@ -143,31 +161,26 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
   }
 }
 
-// Direct global->LDS load of the 64 fp32 row statistics (lse or delta) of one tile: lane i
-// writes row0 + i (rows past S read row S-1; the EDGE path masks them).
-__device__ __forceinline__ void dma_row_stats(float* lds, const float* g, int row0, int S,
-                                              int lane) {
-  dma_lds(g + min(row0 + lane, S - 1), lds, 4);
-}
-
 template <int D>
 __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
     bf16* __restrict__ dk, bf16* __restrict__ dv, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, int S, float scale_log2,
-    float scale) {
+    const float* __restrict__ lse, const float* __restrict__ delta, int S, float c,
+    float lse_mul, float dk_mul) {
   constexpr int KB = kKW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
-  // Q and dO tiles with their lse and delta rows, triple-buffered (constant buffer indices in
-  // the unrolled loop; see the forward kernel).
+  // Q and dO tiles, triple-buffered (constant buffer indices in the unrolled loop; see the
+  // forward kernel), and per wave and buffer the tile's lse and delta rows, converted in place
+  // to -lse/scale and -delta: each wave loads and converts its own copy, so the conversion
+  // needs no barrier.
   __shared__ __attribute__((aligned(16))) bf16 sq[3][kTileRows * D];
   __shared__ __attribute__((aligned(16))) bf16 sdo[3][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) float sl[3][kTileRows];
-  __shared__ __attribute__((aligned(16))) float sd[3][kTileRows];
+  __shared__ __attribute__((aligned(16))) float sst[kWaves][3][2][kTileRows];
 
   const int bh = blockIdx.x;
   const int kblk = blockIdx.y;  // key block 0 sees the most query tiles: dispatched first
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
   const size_t base = (size_t)bh * S * D;
   const bf16* qg = q + base;
@@ -197,41 +210,37 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
     dkacc[db] = f32x16{};
     dvacc[db] = f32x16{};
   }
-  // Land the operand loads before the first direct load: the compiler does not see those, so
-  // a wait it places later for these registers would also wait for every tile in flight.
-  wait_vm_lds<0>();
 
-  // Direct loads per wave per tile: Q and dO, plus the lse row (wave 0) or delta row (wave 1).
+  // Direct loads per wave per tile: its share of Q and dO, and its own lse and delta rows.
   using Dma = DmaTile<D, kWaves>;
-  constexpr int NI = 2 * Dma::PER_WAVE;
-  const bool stats_wave = wave < 2;
-  auto issue = [&](int t, bf16* nq, bf16* ndo, float* nl, float* nd) {
-    Dma::load(nq, qg, t * kTileRows, S, wave, lane);
-    Dma::load(ndo, dog, t * kTileRows, S, wave, lane);
-    if (wave == 0) dma_row_stats(nl, lseg, t * kTileRows, S, lane);
-    if (wave == 1) dma_row_stats(nd, delg, t * kTileRows, S, lane);
+  constexpr int NI = 2 * Dma::PER_WAVE + 2;
+  uint32_t doff[Dma::PER_WAVE];
+  Dma::offsets(doff, wave, lane);
+  float(*st)[2][kTileRows] = sst[wave];
+  auto issue = [&](int t, bf16* nq, bf16* ndo, int buf) {
+    Dma::load_any(nq, qg, t * kTileRows, S, doff, wave, lane);
+    Dma::load_any(ndo, dog, t * kTileRows, S, doff, wave, lane);
+    dma_row64(st[buf][0], lseg, t * kTileRows, S, lane);
+    dma_row64(st[buf][1], delg, t * kTileRows, S, lane);
   };
-  // wait until only one tile's loads (the most recent) may be outstanding, or none
-  auto wait_tiles = [&](bool one_pending) {
-    if (one_pending) {
-      if (stats_wave) wait_vm_lds<NI + 1>(); else wait_vm_lds<NI>();
-    } else {
-      wait_vm_lds<0>();
-    }
-  };
-  issue(t_first, sq[0], sdo[0], sl[0], sd[0]);
-  if (t_first + 1 < t_end) issue(t_first + 1, sq[1], sdo[1], sl[1], sd[1]);
-  wait_tiles(t_first + 1 < t_end);
+  // The first two tiles load alongside the operands above: one wait covers all of them (the
+  // compiler, which does not see the direct loads, then has nothing left to wait for).
+  issue(t_first, sq[0], sdo[0], 0);
+  if (t_first + 1 < t_end) issue(t_first + 1, sq[1], sdo[1], 1);
+  wait_vm_lds<0>();
   __builtin_amdgcn_s_barrier();
 
   // One query tile: prefetch tile t+2 (into the buffers of tile t-1, released by the last
-  // barrier), compute tile t, wait for tile t+1 and barrier.
-  auto tile = [&](int t, const bf16* cq, const bf16* cdo, const float* cl, const float* cd,
-                  bf16* nq, bf16* ndo, float* nl, float* nd) {
+  // barrier), convert this wave's lse row, compute tile t, wait for tile t+1 and barrier.
+  auto tile = [&](int t, const bf16* cq, const bf16* cdo, int cb, bf16* nq, bf16* ndo,
+                  int nb) {
     const int r0 = t * kTileRows;
     const bool prefetch = t + 2 < t_end;
-    if (prefetch) issue(t + 2, nq, ndo, nl, nd);
+    if (prefetch) issue(t + 2, nq, ndo, nb);
     if (kw0 < S && r0 + kTileRows - 1 >= kw0) {
+      // -lse/scale and -delta (this wave's copy; its LDS accesses complete in order)
+      st[cb][0][lane] *= lse_mul;
+      st[cb][1][lane] = -st[cb][1][lane];
       const bool edge = r0 + kTileRows > S;
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
@@ -239,24 +248,27 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
         if (qlo + 31 < kw0) continue;   // every key of the wave is after every query
         // some key after some query, or rows past S: mask
         if (edge || qlo < kw0 + kKW - 1)
-          dkdv_block<D, true>(dkacc, dvacc, kop, vop, cq, cdo, cl, cd, qb, key - r0, S - r0,
-                              lane, scale_log2);
+          dkdv_block<D, true>(dkacc, dvacc, kop, vop, cq, cdo, st[cb][0], st[cb][1], qb,
+                              key - r0, S - r0, lane, c);
         else
-          dkdv_block<D, false>(dkacc, dvacc, kop, vop, cq, cdo, cl, cd, qb, key - r0, S - r0,
-                               lane, scale_log2);
+          dkdv_block<D, false>(dkacc, dvacc, kop, vop, cq, cdo, st[cb][0], st[cb][1], qb,
+                               key - r0, S - r0, lane, c);
       }
     }
-    wait_tiles(prefetch);
+    if (prefetch)
+      wait_vm_lds<NI>();
+    else
+      wait_vm_lds<0>();
     __builtin_amdgcn_s_barrier();
   };
   for (int t = t_first; t < t_end; t += 3) {
-    tile(t, sq[0], sdo[0], sl[0], sd[0], sq[2], sdo[2], sl[2], sd[2]);
-    if (t + 1 < t_end) tile(t + 1, sq[1], sdo[1], sl[1], sd[1], sq[0], sdo[0], sl[0], sd[0]);
-    if (t + 2 < t_end) tile(t + 2, sq[2], sdo[2], sl[2], sd[2], sq[1], sdo[1], sl[1], sd[1]);
+    tile(t, sq[0], sdo[0], 0, sq[2], sdo[2], 2);
+    if (t + 1 < t_end) tile(t + 1, sq[1], sdo[1], 1, sq[0], sdo[0], 0);
+    if (t + 2 < t_end) tile(t + 2, sq[2], sdo[2], 2, sq[1], sdo[1], 1);
   }
 
   if (key < S) {
-    store_rows_bf16<DB>(dk + base + (size_t)key * D, dkacc, scale, hi);
+    store_rows_bf16<DB>(dk + base + (size_t)key * D, dkacc, dk_mul, hi);
     store_rows_bf16<DB>(dv + base + (size_t)key * D, dvacc, 1.0f, hi);
   }
 }
@@ -319,7 +331,8 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
 
   const int bh = blockIdx.x;
   const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
   const size_t base = (size_t)bh * S * D;
   const bf16* kg = k + base;
@@ -339,36 +352,39 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
     doop[ds] = in ? ld_g128(dout + base + (size_t)qrow * D + 16 * ds + 8 * hi)
                   : as_bf16x8(u32x4{0, 0, 0, 0});
   }
-  const float lse2 = qrow < S ? lse[(size_t)bh * S + qrow] * kLog2e : 0.f;
-  const float dlt = qrow < S ? delta[(size_t)bh * S + qrow] : 0.f;
+  // (rows past S read row S-1: finite values for rows that are never stored)
+  float lse_q = lse[(size_t)bh * S + min(qrow, S - 1)];
+  float dlt = delta[(size_t)bh * S + min(qrow, S - 1)];
 
   f32x16 dqacc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
-  // Land the operand loads before the first direct load (see the dK/dV kernel).
-  wait_vm_lds<0>();
 
   // Keys past S read row S-1; every chunk holding such keys is a DIAG chunk (the key is after
-  // every valid query), so they are masked.
+  // every valid query), so they are masked. The first two tiles load alongside the operands
+  // above, under one wait (see the dK/dV kernel).
   using Dma = DmaTile<D, kWaves>;
   constexpr int NI = 2 * Dma::PER_WAVE;
-  Dma::load(sk[0], kg, 0, S, wave, lane);
-  Dma::load(sv[0], vg, 0, S, wave, lane);
+  uint32_t doff[Dma::PER_WAVE];
+  Dma::offsets(doff, wave, lane);
+  Dma::load_any(sk[0], kg, 0, S, doff, wave, lane);
+  Dma::load_any(sv[0], vg, 0, S, doff, wave, lane);
   if (n_tiles > 1) {
-    Dma::load(sk[1], kg, kTileRows, S, wave, lane);
-    Dma::load(sv[1], vg, kTileRows, S, wave, lane);
-    wait_vm_lds<NI>();
-  } else {
-    wait_vm_lds<0>();
+    Dma::load_any(sk[1], kg, kTileRows, S, doff, wave, lane);
+    Dma::load_any(sv[1], vg, kTileRows, S, doff, wave, lane);
   }
+  wait_vm_lds<0>();
   __builtin_amdgcn_s_barrier();
+  // Use the two statistics only from here on, so their load shares the wait above.
+  asm volatile("" : "+v"(lse_q), "+v"(dlt));
+  const float lse2 = lse_q * kLog2e;
 
   auto tile = [&](int t, const bf16* ck, const bf16* cv, bf16* nk, bf16* nv) {
     const int k0 = t * kTileRows;
     const bool prefetch = t + 2 < n_tiles;
     if (prefetch) {
-      Dma::load(nk, kg, k0 + 2 * kTileRows, S, wave, lane);
-      Dma::load(nv, vg, k0 + 2 * kTileRows, S, wave, lane);
+      Dma::load_any(nk, kg, k0 + 2 * kTileRows, S, doff, wave, lane);
+      Dma::load_any(nv, vg, k0 + 2 * kTileRows, S, doff, wave, lane);
     }
     if (q0 < S) {
 #pragma unroll
@@ -421,8 +437,11 @@ hipError_t launch_bwd_bf16_t(bf16* dq, bf16* dk, bf16* dv, float* delta, const b
   }
   if (phases & kBwdDkdv) {
     constexpr int KB = kKW * kWaves;
+    // s = S - lse/scale needs a nonzero scale: a zero one (P = exp(-lse)) runs with 1e-30,
+    // whose S*scale terms are then below fp32 resolution next to lse/scale.
+    const float se = scale != 0.f ? scale : 1e-30f;
     dkdv_bf16_kernel<D><<<dim3(BH, (S + KB - 1) / KB), 64 * kWaves, 0, stream>>>(
-        dk, dv, q, k, v, dout, lse, delta, S, sl2, scale);
+        dk, dv, q, k, v, dout, lse, delta, S, se * kLog2e, -1.0f / se, scale);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return e;

@@ -18,7 +18,9 @@
 // VALU per score, the forward's other bound at d_head 64: the scale is folded into the
 // exponent (one FMA: exp2(s*c - m)), the max takes half a v_max3 per score, the bf16 pack
 // half a v_cvt_pk, and the row sum one fp32 add (in fp32, before the bf16 rounding, so the
-// saved logsumexp keeps fp32 accuracy). Rescaling is lazy: the running max m only moves when
+// saved logsumexp keeps fp32 accuracy). The causal mask costs no VALU: a diagonal chunk's
+// score MFMAs start from an accumulator of 0 / -inf read from a per-lane table in LDS, so
+// masked scores arrive as -inf and exponentiate to exactly 0. Rescaling is lazy: the running max m only moves when
 // a row's new maximum exceeds it by more than kRescale (log2 units), so the O accumulators are rescaled
 // on a few chunks per row instead of every chunk; P stays below 2^kRescale, and O and l carry
 // the same factor, which the epilogue's division removes.
@@ -53,6 +55,36 @@ constexpr int kQW = 32 * kNQB;            // queries per wave
 constexpr int kWaves = DADGPT_FWD_WAVES;  // waves per workgroup
 constexpr int kMinBlocks = DADGPT_FWD_MINB;
 constexpr float kRescale = 8.0f;          // lazy-rescale threshold, log2 units
+// The diagonal-chunk mask table assumes one query block per wave: a wave's chunks are then
+// either fully visible or its diagonal chunk (first key = first query).
+static_assert(kNQB == 1, "one 32-query block per wave");
+
+// Causal mask of a diagonal chunk (first key = first query of the wave) in score-accumulator
+// layout: element r of lane (l32, hi) holds key 16*(r>>3) + 8*hi + (r&7) of query l32, -inf
+// where the key comes after the query. Stored as table[j][lane] = elements 4j..4j+3.
+__device__ __forceinline__ void write_mask_table(f32x4 (*table)[64], int lane) {
+  const int l32 = lane & 31, hi = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f32x4 m;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = 4 * j + e;
+      m[e] = 16 * (r >> 3) + 8 * hi + (r & 7) > l32 ? neg_inf() : 0.0f;
+    }
+    table[j][lane] = m;
+  }
+}
+__device__ __forceinline__ f32x16 read_mask_table(const f32x4 (*table)[64], int lane) {
+  f32x16 m;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const f32x4 v = table[j][lane];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m[4 * j + e] = v[e];
+  }
+  return m;
+}
 
 // K operands of one 32-key chunk (tile keys 32*kb ..): A operands of S^T = K Q^T, K rows read
 // through sigma32 so that register r of lane half hi holds key 32kb + 16*(r>>3) + 8*hi + (r&7).
@@ -65,12 +97,13 @@ __device__ __forceinline__ void fwd_k_ops(bf16x8 (&ka)[D / 16], const bf16* lk, 
   for (int ds = 0; ds < D / 16; ++ds) ka[ds] = lds_op(lk, rm_off<D>(krow, 2 * ds + hi));
 }
 
-// s[i] = K[chunk] Q_i^T for the wave's NQB query blocks; each K operand feeds every block.
+// s[i] = init + K[chunk] Q_i^T for the wave's NQB query blocks; each K operand feeds every
+// block. init is 0, or the causal mask's 0 / -inf for a diagonal chunk.
 template <int D, int NQB>
 __device__ __forceinline__ void fwd_scores(f32x16 (&s)[NQB], const bf16x8 (&qop)[NQB][D / 16],
-                                           const bf16x8 (&ka)[D / 16]) {
+                                           const bf16x8 (&ka)[D / 16], const f32x16& init) {
 #pragma unroll
-  for (int i = 0; i < NQB; ++i) s[i] = f32x16{};
+  for (int i = 0; i < NQB; ++i) s[i] = init;
 #pragma unroll
   for (int ds = 0; ds < D / 16; ++ds)
 #pragma unroll
@@ -87,34 +120,24 @@ __device__ __forceinline__ void fwd_v_ops(bf16x8 (&va)[D / 32][2], const bf16* l
     for (int j = 0; j < 2; ++j) va[db][j] = lds_tr_op<D>(lv, 32 * kb + 16 * j, 32 * db, lane);
 }
 
-// Online softmax of one chunk's scores and O^T += V^T[:, chunk] P^T. DIAG chunks mask keys
-// after the query.
-template <int D, int NQB, bool DIAG>
+// Online softmax of one chunk's scores (masked ones already -inf) and
+// O^T += V^T[:, chunk] P^T.
+template <int D, int NQB>
 __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[NQB][D / 32],
                                                float (&mrun)[NQB], float (&lrun)[NQB],
-                                               const bf16x8 (&va)[D / 32][2], int qrow_minus_c0,
-                                               int lane, float scale_log2) {
-  const int hi = lane >> 5;
+                                               const bf16x8 (&va)[D / 32][2], float scale_log2) {
   constexpr int DB = D / 32;
   // ---- online softmax, per query = per lane ----
   bf16x8 pb[NQB][2];
 #pragma unroll
   for (int i = 0; i < NQB; ++i) {
-    // key offset within the chunk minus (query - c0): > 0 means masked
-    const int rel = qrow_minus_c0 + 32 * i - 8 * hi;
-    if (DIAG) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        s[i][r] = 16 * (r >> 3) + (r & 7) > rel ? neg_inf() : s[i][r];
-    }
     float mx = s[i][0];
 #pragma unroll
     for (int r = 1; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s[i][r]), s[i][r + 1]);
-    mx = max_halves(fmaxf(mx, s[i][15]));
-    if (DIAG) mx = mx == neg_inf() ? mx : mx * scale_log2;  // a fully masked row stays -inf
-    else mx *= scale_log2;
+    // every row of a chunk the wave computes has an unmasked key, so mx is finite
+    mx = max_halves(fmaxf(mx, s[i][15])) * scale_log2;
     // Lazy rescale (wave-uniform branch): move m only when some row's max exceeds it by more
-    // than kRescale. A row whose chunk is fully masked has mx = -inf: no change.
+    // than kRescale.
     if (__builtin_amdgcn_ballot_w64(mx > mrun[i] + kRescale) != 0) {
       const float mnew = fmaxf(mrun[i], mx);
       // 0 on a row's first chunk (mrun = -inf); 1 while a row has seen no key
@@ -132,12 +155,8 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = 8 * j + 2 * e;
-        float p0 = fast_exp2(fmaf(s[i][r], scale_log2, mneg));
-        float p1 = fast_exp2(fmaf(s[i][r + 1], scale_log2, mneg));
-        if (DIAG) {  // exact zeros for masked keys, whatever the scale
-          p0 = 16 * j + 2 * e > rel ? 0.f : p0;
-          p1 = 16 * j + 2 * e + 1 > rel ? 0.f : p1;
-        }
+        const float p0 = fast_exp2(fmaf(s[i][r], scale_log2, mneg));
+        const float p1 = fast_exp2(fmaf(s[i][r + 1], scale_log2, mneg));
         w[e] = pack_bf16x2(p0, p1);
         ls += p0 + p1;
       }
@@ -171,6 +190,7 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
   // one buffer does not alias reads of another (it inserts no wait for it).
   __shared__ __attribute__((aligned(16))) bf16 sk[3][kTileRows * D];
   __shared__ __attribute__((aligned(16))) bf16 sv[3][kTileRows * D];
+  __shared__ f32x4 smask[4][64];
 
   const int bh = blockIdx.x;
   const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
@@ -186,16 +206,13 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
   const int n_tiles = wg_last / kTileRows + 1;
 
   // B operands of S^T: lane holds query q0 + 32i + l32, columns 16*ds + 8*hi + 0..7.
+  // (rows past S read row S-1: finite scores for rows that are never stored)
   bf16x8 qop[kNQB][DS];
 #pragma unroll
   for (int i = 0; i < kNQB; ++i) {
-    const int row = q0 + 32 * i + l32;
+    const int row = min(q0 + 32 * i + l32, S - 1);
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      qop[i][ds] = row < S ? ld_g128(qg + (size_t)row * D + 16 * ds + 8 * hi)
-                           : as_bf16x8(u32x4{0, 0, 0, 0});
-      if (negate_q) qop[i][ds] = neg_bf16x8(qop[i][ds]);
-    }
+    for (int ds = 0; ds < DS; ++ds) qop[i][ds] = ld_g128(qg + (size_t)row * D + 16 * ds + 8 * hi);
   }
 
   f32x16 oacc[kNQB][DB];
@@ -208,21 +225,29 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
     lrun[i] = 0.f;
   }
 
-  // Land the Q loads before the first direct load: the compiler does not see those, so a
-  // wait it placed later for qop would also wait for every tile in flight.
-  wait_vm_lds<0>();
+  if (wave == 0) write_mask_table(smask, lane);  // published by the first barrier
+
+  // The first two tiles load alongside Q, under one wait; Q is touched only after it (the
+  // compiler, which does not see the direct loads, then has nothing left to wait for).
   using Dma = DmaTile<D, kWaves>;
   constexpr int NI = 2 * Dma::PER_WAVE;  // DMA instructions per wave per tile (K and V)
-  Dma::load(sk[0], kg, 0, S, wave, lane);
-  Dma::load(sv[0], vg, 0, S, wave, lane);
+  uint32_t doff[Dma::PER_WAVE];
+  Dma::offsets(doff, wave, lane);
+  Dma::load_any(sk[0], kg, 0, S, doff, wave, lane);
+  Dma::load_any(sv[0], vg, 0, S, doff, wave, lane);
   if (n_tiles > 1) {
-    Dma::load(sk[1], kg, kTileRows, S, wave, lane);
-    Dma::load(sv[1], vg, kTileRows, S, wave, lane);
-    wait_vm_lds<NI>();
-  } else {
-    wait_vm_lds<0>();
+    Dma::load_any(sk[1], kg, kTileRows, S, doff, wave, lane);
+    Dma::load_any(sv[1], vg, kTileRows, S, doff, wave, lane);
   }
+  wait_vm_lds<0>();
   __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int i = 0; i < kNQB; ++i)
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      asm volatile("" : "+v"(qop[i][ds]));
+      if (negate_q) qop[i][ds] = neg_bf16x8(qop[i][ds]);
+    }
 
   // One key tile: prefetch tile t+2 into (nk, nv) (it held tile t-1, released by the last
   // barrier), compute tile t from (ck, cv), then wait for tile t+1 (only tile t+2's loads may
@@ -231,8 +256,8 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
     const int k0 = t * kTileRows;
     const bool prefetch = t + 2 < n_tiles;
     if (prefetch) {
-      Dma::load(nk, kg, k0 + 2 * kTileRows, S, wave, lane);
-      Dma::load(nv, vg, k0 + 2 * kTileRows, S, wave, lane);
+      Dma::load_any(nk, kg, k0 + 2 * kTileRows, S, doff, wave, lane);
+      Dma::load_any(nv, vg, k0 + 2 * kTileRows, S, doff, wave, lane);
     }
     // Issue order is pinned with scheduling barriers: all K operand reads, then both chunks'
     // score MFMAs, then each chunk's V^T reads ahead of its softmax, so no MFMA waits on an
@@ -240,27 +265,32 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
     // chunk's softmax.
     if (q0 < S && k0 <= q0 + kQW - 1) {  // some key of the tile at or before a query
       const bool live1 = k0 + 32 <= q0 + kQW - 1;  // likewise for chunk 1
+      // the chunk whose first key is the wave's first query is the one to mask
+      const bool diag0 = k0 == q0, diag1 = k0 + 32 == q0;
       bf16x8 ka0[DS], ka1[DS], va[DB][2];
       f32x16 s0[kNQB], s1[kNQB];
       fwd_k_ops<D>(ka0, ck, 0, lane);
       if (live1) fwd_k_ops<D>(ka1, ck, 1, lane);
       __builtin_amdgcn_sched_barrier(0);
-      fwd_scores<D, kNQB>(s0, qop, ka0);
-      if (live1) fwd_scores<D, kNQB>(s1, qop, ka1);
+      // (the mask is read where it is used: one chunk per wave takes this path, and a table
+      // held across the operand reads would not fit the register budget)
+      if (diag0)
+        fwd_scores<D, kNQB>(s0, qop, ka0, read_mask_table(smask, lane));
+      else
+        fwd_scores<D, kNQB>(s0, qop, ka0, f32x16{});
+      if (live1) {
+        if (diag1)
+          fwd_scores<D, kNQB>(s1, qop, ka1, read_mask_table(smask, lane));
+        else
+          fwd_scores<D, kNQB>(s1, qop, ka1, f32x16{});
+      }
       fwd_v_ops<D>(va, cv, 0, lane);
       __builtin_amdgcn_sched_barrier(0);
-      const int rel0 = q0 + l32 - k0;
-      if (k0 + 31 > q0)  // some key after some query: mask
-        fwd_softmax_pv<D, kNQB, true>(s0, oacc, mrun, lrun, va, rel0, lane, scale_log2);
-      else
-        fwd_softmax_pv<D, kNQB, false>(s0, oacc, mrun, lrun, va, rel0, lane, scale_log2);
+      fwd_softmax_pv<D, kNQB>(s0, oacc, mrun, lrun, va, scale_log2);
       if (live1) {
         fwd_v_ops<D>(va, cv, 1, lane);
         __builtin_amdgcn_sched_barrier(0);
-        if (k0 + 63 > q0)
-          fwd_softmax_pv<D, kNQB, true>(s1, oacc, mrun, lrun, va, rel0 - 32, lane, scale_log2);
-        else
-          fwd_softmax_pv<D, kNQB, false>(s1, oacc, mrun, lrun, va, rel0 - 32, lane, scale_log2);
+        fwd_softmax_pv<D, kNQB>(s1, oacc, mrun, lrun, va, scale_log2);
       }
     }
     if (prefetch)
@@ -303,8 +333,11 @@ hipError_t launch_fwd_bf16_t(bf16* out, float* lse, const bf16* q, const bf16* k
                              int BH, int S, float scale, hipStream_t stream) {
   constexpr int QB = kQW * kWaves;
   dim3 grid(BH, (S + QB - 1) / QB);
-  fwd_bf16_kernel<D><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S,
-                                                       fabsf(scale) * kLog2e, scale < 0.f);
+  // Masked scores are -inf and exponentiate as exp2(-inf * c - m), so c must be positive: a
+  // zero scale (uniform attention) runs with c = 1e-30: every score below 1e22 in magnitude
+  // then has |s*c - m| < 2^-25, an fp32 weight of exactly 1.
+  const float c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);
+  fwd_bf16_kernel<D><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c, scale < 0.f);
   return hipGetLastError();
 }
 

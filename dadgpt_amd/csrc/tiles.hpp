@@ -131,6 +131,36 @@ __device__ __forceinline__ void dma_lds(const void* gsrc, const void* lds_dst, i
                  : "memory");
 }
 
+// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset
+// (the instruction's saddr form): a tile loop moves only the scalar base.
+__device__ __forceinline__ void dma_lds16_sbase(const void* gbase, uint32_t voff,
+                                                const void* lds_dst) {
+  const uint32_t lds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst;
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(base), "v"(voff), "s"(gbase)
+               : "memory");
+}
+__device__ __forceinline__ void dma_lds4_sbase(const void* gbase, uint32_t voff,
+                                               const void* lds_dst) {
+  const uint32_t lds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst;
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+               :
+               : "s"(base), "v"(voff), "s"(gbase)
+               : "memory");
+}
+
+// 64 consecutive fp32 values g[row0 .. row0+63] into LDS, one per lane; rows past S read
+// row S-1.
+__device__ __forceinline__ void dma_row64(float* lds, const float* g, int row0, int S,
+                                          int lane) {
+  const int rows_left = S - row0;  // wave-uniform
+  const uint32_t off = (uint32_t)(rows_left < 64 ? min(lane, rows_left - 1) : lane) * 4u;
+  dma_lds4_sbase(g + row0, off, lds);
+}
+
 template <int D, int WAVES>
 struct DmaTile {
   static constexpr int C = D / 8;                       // 16-byte chunks per row
@@ -148,6 +178,35 @@ struct DmaTile {
       const int chunk = (slot % C) ^ swz<D>(row);
       const int grow = min(row0 + row, S - 1);
       dma_lds(g + (size_t)grow * D + chunk * 8, lds_tile + slot0 * 8, 16);
+    }
+  }
+
+  // Byte offset, from the tile's first row, of the global piece that fills this lane's slot
+  // of wave-instruction n (fixed for the whole kernel).
+  __device__ __forceinline__ static void offsets(uint32_t (&off)[PER_WAVE], int wave, int lane) {
+#pragma unroll
+    for (int n = 0; n < PER_WAVE; ++n) {
+      const int slot = (wave * PER_WAVE + n) * 64 + lane;
+      const int row = slot / C;
+      off[n] = (uint32_t)(row * D + ((slot % C) ^ swz<D>(row)) * 8) * 2u;
+    }
+  }
+
+  // Either form: a tile that crosses S moves the offsets of rows past S back to row S-1
+  // (the slot's chunk swizzle is kept; it is the destination's).
+  __device__ __forceinline__ static void load_any(bf16* lds_tile, const bf16* g, int row0, int S,
+                                                  const uint32_t (&off)[PER_WAVE], int wave,
+                                                  int lane) {
+    const int rows_left = S - row0;  // wave-uniform
+    const bf16* base = g + (size_t)row0 * D;
+#pragma unroll
+    for (int n = 0; n < PER_WAVE; ++n) {
+      uint32_t o = off[n];
+      if (rows_left < kTileRows) {
+        const int r = (wave * PER_WAVE + n) * (64 / C) + lane / C;
+        if (r >= rows_left) o -= (uint32_t)((r - rows_left + 1) * D * 2);
+      }
+      dma_lds16_sbase(base, o, lds_tile + (wave * PER_WAVE + n) * 64 * 8);
     }
   }
 };

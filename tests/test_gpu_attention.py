@@ -144,6 +144,31 @@ def test_bf16_forward_backward_small(gpu, BH, S, D):
         assert max_abs(host(a), b) <= TOL_GRAD, nm
 
 
+@pytest.mark.parametrize("scale", [0.0, -0.125, 1.0])
+@pytest.mark.parametrize("D", [64, 32])
+def test_bf16_scale_zero_negative_large(gpu, scale, D):
+    """Zero scale (uniform weights over the causal prefix), a negative scale (applied by
+    negating Q) and a large one (sharp rows that move the running maximum often)."""
+    BH, S = 2, 200
+    case(f"bf16 scale={scale} BH={BH} S={S} D={D}")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=90 + D, with_dout=True, bf16=True)
+    q, k, v, g = (dev(x, torch.bfloat16) for x in (qn, kn, vn, gn))
+    out, lse = A.attention_forward(q, k, v, scale)
+    dq, dk, dv, _ = A.attention_backward(g, out, lse, q, k, v, scale)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oracle.attn_fwd(qn, kn, vn, scale, threads=8)
+    assert max_abs(host(out), o_ref) <= TOL_O
+    assert max_abs(host(lse), l_ref) <= TOL_LSE
+    if scale == 0.0:  # row i is the mean of V_0..V_i; lse = ln(i + 1)
+        assert max_abs(host(lse)[0], np.log(np.arange(1, S + 1))) <= TOL_LSE
+    # dQ and dK carry the scale factor, and a large scale sharpens P: the bf16 rounding of
+    # dS (relative 2^-9) grows with |scale|, so the gradient bound scales with it.
+    tol_grad = TOL_GRAD * max(1.0, abs(scale) / scale_of(D))
+    ref = oracle.attn_bwd(gn, qn, kn, vn, scale, threads=8)[:3]
+    for a, b, nm in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+        assert max_abs(host(a), b) <= tol_grad, nm
+
+
 def torch_reference(q, k, v, scale, dout=None, chunk=16):
     """Materialized fp32 causal attention on the GPU with torch (GEMMs on contiguous
     operands): O, lse and, with dout, dQ/dK/dV plus the two quantities the column-sum bounds
