@@ -16,14 +16,13 @@
 //                               (bf16), no lane exchange
 //
 // VALU per score, the forward's other bound at d_head 64: the scale is folded into the
-// exponent (one FMA: exp2(s*c - m)), the max takes half a v_max3 per score, the bf16 pack
-// half a v_cvt_pk, and the row sum one fp32 add (in fp32, before the bf16 rounding, so the
-// saved logsumexp keeps fp32 accuracy). The causal mask costs no VALU: a diagonal chunk's
-// score MFMAs start from an accumulator of 0 / -inf read from a per-lane table in LDS, so
-// masked scores arrive as -inf and exponentiate to exactly 0. Rescaling is lazy: the running max m only moves when
-// a row's new maximum exceeds it by more than kRescale (log2 units), so the O accumulators are rescaled
-// on a few chunks per row instead of every chunk; P stays below 2^kRescale, and O and l carry
-// the same factor, which the epilogue's division removes.
+// exponent (one FMA: exp2(s*c - m)), the bf16 pack takes half a v_cvt_pk and the row sum one
+// fp32 add (in fp32, before the bf16 rounding, so the saved logsumexp keeps fp32 accuracy).
+// The running maximum m is not recomputed per chunk: it moves only when a chunk's P would
+// reach 2^64 (see fwd_softmax_pv), so the row max leaves the per-chunk path. The causal mask
+// costs no VALU either: a diagonal chunk's score MFMAs start from an accumulator of 0 / -inf
+// read from a per-lane table in LDS, so masked scores arrive as -inf and exponentiate to
+// exactly 0.
 //
 // The launch bound caps registers so that several waves share each SIMD, which interleaves
 // one wave's softmax with another's MFMAs and covers LDS latency. K and V tiles are
@@ -54,7 +53,9 @@ constexpr int kNQB = DADGPT_FWD_NQB;
 constexpr int kQW = 32 * kNQB;            // queries per wave
 constexpr int kWaves = DADGPT_FWD_WAVES;  // waves per workgroup
 constexpr int kMinBlocks = DADGPT_FWD_MINB;
-constexpr float kRescale = 8.0f;          // lazy-rescale threshold, log2 units
+// A chunk whose P reaches this in some row moves the running maximum (see fwd_softmax_pv):
+// with P < 2^64, O and l stay far inside fp32 range over any sequence length.
+constexpr float kMaxP = 0x1p64f;
 // The diagonal-chunk mask table assumes one query block per wave: a wave's chunks are then
 // either fully visible or its diagonal chunk (first key = first query).
 static_assert(kNQB == 1, "one 32-query block per wave");
@@ -120,49 +121,62 @@ __device__ __forceinline__ void fwd_v_ops(bf16x8 (&va)[D / 32][2], const bf16* l
     for (int j = 0; j < 2; ++j) va[db][j] = lds_tr_op<D>(lv, 32 * kb + 16 * j, 32 * db, lane);
 }
 
+// P = exp2(s*c - m) of one chunk as bf16 B operands; returns this lane's fp32 sum of them.
+__device__ __forceinline__ float fwd_exp(bf16x8 (&pb)[2], const f32x16& s, float m,
+                                         float scale_log2) {
+  const float mneg = -m;
+  float ls = 0.f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = 8 * j + 2 * e;
+      const float p0 = fast_exp2(fmaf(s[r], scale_log2, mneg));
+      const float p1 = fast_exp2(fmaf(s[r + 1], scale_log2, mneg));
+      w[e] = pack_bf16x2(p0, p1);
+      ls += p0 + p1;
+    }
+    pb[j] = as_bf16x8(w);
+  }
+  return ls;
+}
+
 // Online softmax of one chunk's scores (masked ones already -inf) and
 // O^T += V^T[:, chunk] P^T.
+//
+// The exponentials are taken against the running maximum m as it stands, without the
+// chunk's own maximum: m only has to keep P finite and away from the fp32 limits, not equal
+// the true maximum (O and l carry the same factor 2^-m, which the epilogue's division and
+// lse = m + log2 l remove). A chunk whose P reaches 2^kMaxLog2P in some row (or is
+// inf/NaN: m is -inf before a row's first chunk) takes the slow path: m moves to the
+// chunk's maximum, O and l are rescaled, and the chunk's exponentials are redone. That is a
+// wave's first chunk and, for ordinary scores, almost nothing else, so the row maximum is
+// off the per-chunk path.
 template <int D, int NQB>
 __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[NQB][D / 32],
                                                float (&mrun)[NQB], float (&lrun)[NQB],
                                                const bf16x8 (&va)[D / 32][2], float scale_log2) {
   constexpr int DB = D / 32;
-  // ---- online softmax, per query = per lane ----
   bf16x8 pb[NQB][2];
 #pragma unroll
   for (int i = 0; i < NQB; ++i) {
-    float mx = s[i][0];
+    float ls = fwd_exp(pb[i], s[i], mrun[i], scale_log2);
+    if (__builtin_amdgcn_ballot_w64(!(ls < kMaxP)) != 0) {  // wave-uniform
+      float mx = s[i][0];
 #pragma unroll
-    for (int r = 1; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s[i][r]), s[i][r + 1]);
-    // every row of a chunk the wave computes has an unmasked key, so mx is finite
-    mx = max_halves(fmaxf(mx, s[i][15])) * scale_log2;
-    // Lazy rescale (wave-uniform branch): move m only when some row's max exceeds it by more
-    // than kRescale.
-    if (__builtin_amdgcn_ballot_w64(mx > mrun[i] + kRescale) != 0) {
+      for (int r = 1; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s[i][r]), s[i][r + 1]);
+      // every row of a chunk the wave computes has an unmasked key, so mx is finite
+      mx = max_halves(fmaxf(mx, s[i][15])) * scale_log2;
       const float mnew = fmaxf(mrun[i], mx);
-      // 0 on a row's first chunk (mrun = -inf); 1 while a row has seen no key
-      const float corr = mnew == neg_inf() ? 1.0f : fast_exp2(mrun[i] - mnew);
+      const float corr = fast_exp2(mrun[i] - mnew);  // 0 on a row's first chunk
       mrun[i] = mnew;
       lrun[i] *= corr;
 #pragma unroll
       for (int db = 0; db < DB; ++db) oacc[i][db] *= corr;
+      ls = fwd_exp(pb[i], s[i], mnew, scale_log2);
     }
-    const float mneg = -mrun[i];
-    float ls = lrun[i];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      u32x4 w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 8 * j + 2 * e;
-        const float p0 = fast_exp2(fmaf(s[i][r], scale_log2, mneg));
-        const float p1 = fast_exp2(fmaf(s[i][r + 1], scale_log2, mneg));
-        w[e] = pack_bf16x2(p0, p1);
-        ls += p0 + p1;
-      }
-      pb[i][j] = as_bf16x8(w);
-    }
-    lrun[i] = ls;
+    lrun[i] += ls;
   }
   // ---- O^T += V^T[:, chunk] P^T; each V^T operand read once for every query block ----
 #pragma unroll
@@ -259,38 +273,24 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
       Dma::load_any(nk, kg, k0 + 2 * kTileRows, S, doff, wave, lane);
       Dma::load_any(nv, vg, k0 + 2 * kTileRows, S, doff, wave, lane);
     }
-    // Issue order is pinned with scheduling barriers: all K operand reads, then both chunks'
-    // score MFMAs, then each chunk's V^T reads ahead of its softmax, so no MFMA waits on an
-    // LDS read issued just before it and the second chunk's MFMAs run under the first
-    // chunk's softmax.
     if (q0 < S && k0 <= q0 + kQW - 1) {  // some key of the tile at or before a query
-      const bool live1 = k0 + 32 <= q0 + kQW - 1;  // likewise for chunk 1
-      // the chunk whose first key is the wave's first query is the one to mask
-      const bool diag0 = k0 == q0, diag1 = k0 + 32 == q0;
-      bf16x8 ka0[DS], ka1[DS], va[DB][2];
-      f32x16 s0[kNQB], s1[kNQB];
-      fwd_k_ops<D>(ka0, ck, 0, lane);
-      if (live1) fwd_k_ops<D>(ka1, ck, 1, lane);
-      __builtin_amdgcn_sched_barrier(0);
-      // (the mask is read where it is used: one chunk per wave takes this path, and a table
-      // held across the operand reads would not fit the register budget)
-      if (diag0)
-        fwd_scores<D, kNQB>(s0, qop, ka0, read_mask_table(smask, lane));
-      else
-        fwd_scores<D, kNQB>(s0, qop, ka0, f32x16{});
-      if (live1) {
-        if (diag1)
-          fwd_scores<D, kNQB>(s1, qop, ka1, read_mask_table(smask, lane));
+      // One 32-key chunk at a time: the operand reads of a chunk are issued together, and
+      // the other waves on the SIMD (three per SIMD) cover their latency. Holding both
+      // chunks' scores at once measured no faster and costs registers.
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int c0 = k0 + 32 * kb;
+        if (c0 > q0 + kQW - 1) break;  // every key of the chunk after every query
+        bf16x8 ka[DS], va[DB][2];
+        f32x16 sc[kNQB];
+        fwd_k_ops<D>(ka, ck, kb, lane);
+        fwd_v_ops<D>(va, cv, kb, lane);
+        // the chunk whose first key is the wave's first query is the one to mask
+        if (c0 == q0)
+          fwd_scores<D, kNQB>(sc, qop, ka, read_mask_table(smask, lane));
         else
-          fwd_scores<D, kNQB>(s1, qop, ka1, f32x16{});
-      }
-      fwd_v_ops<D>(va, cv, 0, lane);
-      __builtin_amdgcn_sched_barrier(0);
-      fwd_softmax_pv<D, kNQB>(s0, oacc, mrun, lrun, va, scale_log2);
-      if (live1) {
-        fwd_v_ops<D>(va, cv, 1, lane);
-        __builtin_amdgcn_sched_barrier(0);
-        fwd_softmax_pv<D, kNQB>(s1, oacc, mrun, lrun, va, scale_log2);
+          fwd_scores<D, kNQB>(sc, qop, ka, f32x16{});
+        fwd_softmax_pv<D, kNQB>(sc, oacc, mrun, lrun, va, scale_log2);
       }
     }
     if (prefetch)

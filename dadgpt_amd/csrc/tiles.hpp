@@ -165,11 +165,16 @@ template <int D, int WAVES>
 struct DmaTile {
   static constexpr int C = D / 8;                       // 16-byte chunks per row
   static constexpr int SLOTS = kTileRows * C;           // 16-byte slots per tile
-  static constexpr int PER_WAVE = SLOTS / (64 * WAVES); // wave-instructions per tile
-  static_assert(SLOTS % (64 * WAVES) == 0, "whole wave-instructions per tile");
+  // wave-instructions per tile and wave; with more waves than instructions the surplus waves
+  // stage nothing (and their waits for these loads return at once)
+  static constexpr int PER_WAVE = SLOTS >= 64 * WAVES ? SLOTS / (64 * WAVES) : 1;
+  static constexpr int ACTIVE = SLOTS / (64 * PER_WAVE);  // waves that stage
+  static_assert(SLOTS % (64 * WAVES) == 0 || (64 * WAVES) % SLOTS == 0,
+                "whole wave-instructions per tile");
 
   __device__ __forceinline__ static void load(bf16* lds_tile, const bf16* g, int row0, int S,
                                               int wave, int lane) {
+    if (wave >= ACTIVE) return;
 #pragma unroll
     for (int n = 0; n < PER_WAVE; ++n) {
       const int slot0 = (wave * PER_WAVE + n) * 64;
@@ -197,6 +202,7 @@ struct DmaTile {
   __device__ __forceinline__ static void load_any(bf16* lds_tile, const bf16* g, int row0, int S,
                                                   const uint32_t (&off)[PER_WAVE], int wave,
                                                   int lane) {
+    if (wave >= ACTIVE) return;
     const int rows_left = S - row0;  // wave-uniform
     const bf16* base = g + (size_t)row0 * D;
 #pragma unroll
