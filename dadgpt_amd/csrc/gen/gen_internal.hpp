@@ -74,25 +74,30 @@ hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* 
 
 // ---- skinny projections of the decode step (skinny.hip) ----
 
-enum SkinnyPrologue { kProRows = 0, kProLayerNorm = 1, kProGelu = 2 };
+enum SkinnyPrologue { kProRows = 0, kProLn = 1 };
+enum SkinnyEpilogue { kEpiStore = 0, kEpiQkv = 1, kEpiGelu = 2, kEpiResidual = 3 };
 
 struct SkinnyArgs {
-  float* parts;             // out [K/kc][M][N] fp32: one partial sum per K-chunk
-  const bf16* wt;           // W^T [N][K]
-  int M, N, K, kc;          // rows (<= 16), columns, reduction length, K-chunk (K % kc == 0)
-  const bf16* act;          // kProRows: A [M][K]
-  const float* x_in;        // kProLayerNorm: residual stream [M][K]
-  const float* in_parts;    // kProLayerNorm / kProGelu: [in_splits][M][K] partial sums
-  int in_splits;
-  const bf16* in_bias;      // [K] (optional for kProLayerNorm)
-  const bf16* ln_w;         // kProLayerNorm: LayerNorm weight and bias [K]
+  const bf16* wt;        // W^T [N][K]
+  int M, N, K;           // rows (<= 16), columns, reduction length
+  const bf16* act;       // kProRows: A [M][K]
+  const float* x;        // kProLn: A = LayerNorm(x [M][K]) * ln_w + ln_b
+  const bf16* ln_w;
   const bf16* ln_b;
-  float* x_out;             // kProLayerNorm: x + parts + bias stored here (optional)
+  float* out;            // kEpiStore: [M][N]
+  const float* bias_f;   // kEpiQkv: fp32 bias [N]
+  const bf16* bias;      // kEpiGelu, kEpiResidual: bias [N]
+  bf16* g;               // kEpiGelu: gelu(A W + bias) [M][N]
+  float* x_out;          // kEpiResidual: residual stream [M][N], += A W + bias in place
+  void* q;               // kEpiQkv: q [M, H, dh] and k, v into the caches
+  void* kcache;          //   [.., H, max_len, dh] at row pos[m]; bf16, or fp32 if qkv_fp32
+  void* vcache;
+  const int* pos;
+  int H, dh, max_len, qkv_fp32;
 };
 
-bool skinny_supported(int M, int K);
-int skinny_chunk(int K);  // the K-chunk a K-long reduction uses (<= 768, divides K)
-hipError_t skinny_gemm(int prologue, const SkinnyArgs& args, hipStream_t s);
+bool skinny_supported(int M, int K);  // M <= 16 and a K the kernels are built for
+hipError_t skinny_gemm(int prologue, int epilogue, const SkinnyArgs& args, hipStream_t s);
 // out [cols][rows] = in [rows][cols]^T (bf16)
 hipError_t transpose(bf16* out, const bf16* in, int rows, int cols, hipStream_t s);
 

@@ -8,6 +8,7 @@
 // step when the caller asks for every step's logits).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -127,12 +128,9 @@ struct dadgpt_gpt2 {
 
   std::vector<bf16*> wqkv;   // per layer [d, 3d]
   std::vector<float*> bqkv;  // per layer [3d]
-  // decode steps of at most 16 sequences (d_model <= 768): transposed weights for the skinny
-  // projections, the second residual buffer, and the fc2 partial sums
+  // decode steps of at most 16 sequences: transposed weights for the skinny projections
   bool skinny = false;
   std::vector<bf16*> wqkv_t, wo_t, w1_t, w2_t;  // [3d, d], [d, d], [d_ff, d], [d, d_ff]
-  float *xb = nullptr, *parts2 = nullptr;
-  int fc2_splits = 1;
   std::vector<void*> kc, vc;  // per layer [max_batch, H, ctx, dh]
 
   float *x = nullptr, *qkv = nullptr, *y = nullptr, *f = nullptr, *xl = nullptr;
@@ -309,11 +307,11 @@ int decode_step(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   return head(m, n);
 }
 
-// The decode step on the skinny projections (n <= 16 sequences). Per layer 6 dependent
-// launches: QKV (LayerNorm 1 of x + previous fc2 partials + bias in its prologue) -> QKV split
-// + cache append -> decode attention -> Wo -> fc1 (residual add + LayerNorm 2 in its
-// prologue) -> fc2 (bias + GELU of fc1 in its prologue, partial sums out). The residual
-// stream alternates between m->x and m->xb.
+// The decode step on the skinny projections (n <= 16 sequences). Per layer 5 dependent
+// launches, each projection doing the elementwise work around it (see skinny.hip):
+// QKV (LayerNorm 1 of x in its prologue; bias, q out, K/V appended to the caches) -> decode
+// attention -> Wo (bias + residual add into x) -> fc1 (LayerNorm 2 of x; bias + GELU into g)
+// -> fc2 (bias + residual add into x). x is the fp32 residual stream.
 int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   const auto& c = m->c;
   const int d = c.d_model, H = c.n_heads, dh = m->dh;
@@ -325,75 +323,53 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   for (int l = 0; l < c.n_layers; ++l) {
     const auto& L = m->off.layers[l];
     SkinnyArgs q{};
-    q.parts = m->qkv;
     q.wt = m->wqkv_t[l];
-    q.M = n, q.N = 3 * d, q.K = d, q.kc = skinny_chunk(d);
-    q.x_in = m->x;
-    if (l > 0) {
-      q.in_parts = m->parts2;
-      q.in_splits = m->fc2_splits;
-      q.in_bias = m->P(m->off.layers[l - 1].fc2_b);
-    }
-    q.ln_w = m->P(L.ln1_w), q.ln_b = m->P(L.ln1_b);
-    q.x_out = m->xb;
-    TRY_HIP(skinny_gemm(kProLayerNorm, q, s), "skinny QKV");
-    const bf16* attn_in = m->a;
-    if (m->fp32)
-      TRY_HIP(qkv_split<float>((float*)m->qh, nullptr, nullptr, (float*)m->kc[l],
-                               (float*)m->vc[l], m->qkv, m->bqkv[l], m->cur_pos, m->ones, n, 1,
-                               H, dh, c.ctx_len, s),
-              "qkv_split");
-    else
-      TRY_HIP(qkv_split<bf16>((bf16*)m->qh, nullptr, nullptr, (bf16*)m->kc[l], (bf16*)m->vc[l],
-                              m->qkv, m->bqkv[l], m->cur_pos, m->ones, n, 1, H, dh, c.ctx_len,
-                              s),
-              "qkv_split");
+    q.M = n, q.N = 3 * d, q.K = d;
+    q.x = m->x, q.ln_w = m->P(L.ln1_w), q.ln_b = m->P(L.ln1_b);
+    q.bias_f = m->bqkv[l];
+    q.q = m->qh, q.kcache = m->kc[l], q.vcache = m->vc[l], q.pos = m->cur_pos;
+    q.H = H, q.dh = dh, q.max_len = c.ctx_len, q.qkv_fp32 = m->fp32;
+    TRY_HIP(skinny_gemm(kProLn, kEpiQkv, q, s), "skinny QKV");
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[2 * l], s), "hipEventRecord");
     if (int st = attention_decode(m, l, n, scale)) return attn_fail(st, "decode attention");
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[2 * l + 1], s), "hipEventRecord");
+    const bf16* attn_in = m->a;
     if (m->fp32)
       TRY_HIP(to_bf16(m->a, (const float*)m->ao, (size_t)n * d, s), "to_bf16");
     else
       attn_in = (const bf16*)m->ao;
 
     SkinnyArgs o{};
-    o.parts = m->y;
     o.wt = m->wo_t[l];
-    o.M = n, o.N = d, o.K = d, o.kc = skinny_chunk(d);
+    o.M = n, o.N = d, o.K = d;
     o.act = attn_in;
-    TRY_HIP(skinny_gemm(kProRows, o, s), "skinny Wo");
+    o.bias = m->P(L.bo), o.x_out = m->x;
+    TRY_HIP(skinny_gemm(kProRows, kEpiResidual, o, s), "skinny Wo");
 
     SkinnyArgs f1{};
-    f1.parts = m->f;
     f1.wt = m->w1_t[l];
-    f1.M = n, f1.N = c.d_ff, f1.K = d, f1.kc = skinny_chunk(d);
-    f1.x_in = m->xb;
-    f1.in_parts = m->y;
-    f1.in_splits = d / o.kc;
-    f1.in_bias = m->P(L.bo);
-    f1.ln_w = m->P(L.ln2_w), f1.ln_b = m->P(L.ln2_b);
-    f1.x_out = m->x;
-    TRY_HIP(skinny_gemm(kProLayerNorm, f1, s), "skinny fc1");
+    f1.M = n, f1.N = c.d_ff, f1.K = d;
+    f1.x = m->x, f1.ln_w = m->P(L.ln2_w), f1.ln_b = m->P(L.ln2_b);
+    f1.bias = m->P(L.fc1_b), f1.g = m->g;
+    TRY_HIP(skinny_gemm(kProLn, kEpiGelu, f1, s), "skinny fc1");
 
     SkinnyArgs f2{};
-    f2.parts = m->parts2;
     f2.wt = m->w2_t[l];
-    f2.M = n, f2.N = d, f2.K = c.d_ff, f2.kc = skinny_chunk(c.d_ff);
-    f2.in_parts = m->f;
-    f2.in_splits = d / f1.kc;
-    f2.in_bias = m->P(L.fc1_b);
-    TRY_HIP(skinny_gemm(kProGelu, f2, s), "skinny fc2");
+    f2.M = n, f2.N = d, f2.K = c.d_ff;
+    f2.act = m->g;
+    f2.bias = m->P(L.fc2_b), f2.x_out = m->x;
+    TRY_HIP(skinny_gemm(kProRows, kEpiResidual, f2, s), "skinny fc2");
   }
-  // residual add of the last fc2 and the final LayerNorm, then the tied logits
-  TRY_HIP(residual_layernorm(m->x, m->parts2, m->P(m->off.layers[c.n_layers - 1].fc2_b), m->h,
-                             m->P(m->off.lnf_w), m->P(m->off.lnf_b), n, d, s, m->fc2_splits),
+  // final LayerNorm, then the tied logits
+  TRY_HIP(residual_layernorm(m->x, nullptr, nullptr, m->h, m->P(m->off.lnf_w),
+                             m->P(m->off.lnf_b), n, d, s),
           "residual_layernorm");
   SkinnyArgs lg{};
-  lg.parts = m->logits;
   lg.wt = m->P(m->off.tok_emb);  // [V, d]: already W^T of the tied projection
-  lg.M = n, lg.N = c.vocab_size, lg.K = d, lg.kc = skinny_chunk(d);
+  lg.M = n, lg.N = c.vocab_size, lg.K = d;
   lg.act = m->h;
-  TRY_HIP(skinny_gemm(kProRows, lg, s), "skinny logits");
+  lg.out = m->logits;
+  TRY_HIP(skinny_gemm(kProRows, kEpiStore, lg, s), "skinny logits");
   TRY_HIP(argmax_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
                          m->lens, m->logits, m->pick, n, c.vocab_size, s),
           "argmax_advance");
@@ -576,20 +552,14 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       (st = m->alloc_n(&m->out_tok, rows, "tokens out")) ||
       (st = m->alloc_n(&m->out_margin, rows, "margins out")))
     return bail(st);
-  // the skinny decode path: one K-chunk for every reduction over d_model (so the QKV, Wo,
-  // fc1 and logits projections write a single partial), d_ff a multiple of 32
-  m->skinny = c.d_model <= 768 && skinny_chunk(c.d_model) == c.d_model &&
-              skinny_supported(1, c.d_model) && skinny_supported(1, c.d_ff);
+  // the skinny decode path: reduction lengths the kernels are built for, LayerNorm rows that
+  // fit the prologue's registers
+  m->skinny = skinny_supported(1, c.d_model) && skinny_supported(1, c.d_ff) && c.d_model <= 1024;
   if (m->skinny) {
-    m->fc2_splits = c.d_ff / skinny_chunk(c.d_ff);
-    const int nb = max_batch < 16 ? max_batch : 16;
     m->wqkv_t.resize(c.n_layers);
     m->wo_t.resize(c.n_layers);
     m->w1_t.resize(c.n_layers);
     m->w2_t.resize(c.n_layers);
-    if ((st = m->alloc_n(&m->xb, (size_t)nb * d, "residual b")) ||
-        (st = m->alloc_n(&m->parts2, (size_t)m->fc2_splits * nb * d, "fc2 partials")))
-      return bail(st);
     for (int l = 0; l < c.n_layers; ++l) {
       const auto& L = m->off.layers[l];
       if ((st = m->alloc_n(&m->wqkv_t[l], 3 * d * d, "wqkv^T")) ||

@@ -1,22 +1,31 @@
 // Decode-step projections for at most 16 rows (one token per sequence): out[M,N] = A[M,K] W
 // with W stored transposed, W^T [N, K] bf16, so that every MFMA operand is a contiguous
 // 16-byte load straight from HBM (no LDS staging of the weights). These GEMMs are weight
-// streams (M <= 16): the point is to have the whole weight matrix in flight at once and to
-// fold the elementwise work around each projection into it, because at this size every
+// streams (M <= 16) far smaller than the bytes HBM needs in flight to reach its bandwidth,
+// so each one takes about one memory latency if all its weight loads are issued at once, on
+// many CUs; the work around each projection is folded into it, because at this size every
 // dependent kernel costs its launch plus a memory round trip.
 //
-// Workgroup = 4 waves x 16 output columns; wave w owns columns n0 + 16w .. +15 and one
-// K-chunk of KC (blockIdx.y selects the chunk; partial sums go to parts[chunk], summed by the
-// consumer in chunk order). v_mfma_f32_16x16x32_bf16: lane l supplies A[l%16][8(l/16)+e] and
-// B[8(l/16)+e][l%16] and holds D[4(l/16)+r][l%16]. Here A = W^T (rows = output columns n) and
-// B = the activations transposed (columns = rows m of the batch), so D = out^T.
+// Workgroup = 16 output columns x W waves: wave w takes the K range [w K/W, (w+1) K/W)
+// (W = 4, or 16 for K >= 2048) and issues all its weight loads up front; the partial products
+// are summed through LDS and the epilogue runs in the same workgroup, so no result crosses
+// workgroups. The grid is N/16 workgroups (144 for the QKV projection of GPT-2 124M, 192 for
+// fc1, 48 for Wo and fc2). The epilogue's own inputs (bias, residual, cache row) are loaded
+// first, so their latency hides under the weight stream.
+// v_mfma_f32_16x16x32_bf16: lane l supplies A[l%16][8(l/16)+e] and B[8(l/16)+e][l%16] and
+// holds D[4(l/16)+r][l%16]. Here A = W^T (rows = output columns n) and B = the activations
+// transposed (columns = rows m of the batch), so D = out^T.
 //
-// The activations reach the MFMA through LDS, produced by a prologue (one of):
-//   kProRows    A = bf16 rows act[m][k]                                   (Wo, logits)
-//   kProLayerNorm  x' = x + sum_s parts_s + bias (the residual add of the previous
-//               projection), A = LayerNorm(x') * w + b over the full row (K = the chunk,
-//               <= 768); workgroup (0,0) also stores x' (the next residual stream) (QKV, fc1)
-//   kProGelu    A = gelu(sum_s parts_s + bias) for this chunk's columns    (fc2)
+// Prologues (where the B operands come from):
+//   kProRows  bf16 activations act [M][K], read straight from global memory (L2-resident)
+//   kProLn    A = bf16(LayerNorm(x) w + b) of the fp32 residual stream x [M][K], computed by
+//             every workgroup into LDS (two-pass mean and variance, eps 1e-5); the weight
+//             loads are issued before it, so the stream runs under it
+// Epilogues (per output element, after the bias):
+//   kEpiStore     out [M][N] fp32                                       (logits)
+//   kEpiQkv       q -> q [M, H, dh]; k, v -> the caches [.., H, max_len, dh] at row pos[m]
+//   kEpiGelu      g [M][N] = bf16(gelu(.))                              (fc1)
+//   kEpiResidual  x [M][N] += .  (the residual stream, in place)        (Wo, fc2)
 #include <hip/hip_runtime.h>
 
 #include "gen_internal.hpp"
@@ -26,11 +35,12 @@ namespace dadgpt::gen {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kRows = 16;         // batch rows of the skinny path
-constexpr int kMaxLnVals = 48;    // LayerNorm prologue: K <= 16 * 48 = 768
-constexpr int kPad = 8;           // LDS row padding (16 bytes): conflict-free operand reads
+constexpr int kRows = 16;      // batch rows of the skinny path
+constexpr int kPad = 8;        // LDS row padding (16 bytes): conflict-free operand reads
+constexpr int kMaxLnK = 1024;  // kProLn: the prologue holds a row's values in registers
 
 // GELU, tanh form (src/tensor_ops.cpp:86-95): 0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)), one
 // exponential and one reciprocal instead of tanhf (the result is rounded to bf16).
@@ -39,7 +49,6 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x / (1.0f + __expf(-2.0f * u));
 }
 
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f32x4 ld_bf16x4(const bf16* p) {
   const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
   return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
@@ -51,130 +60,163 @@ __device__ __forceinline__ float sum16(float v) {  // over the 16 lanes of a row
   return v;
 }
 
-template <int PRO, int KC>
-__global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyArgs a) {
-  constexpr int NT = KC / 32;  // MFMA k-steps of a chunk
-  __shared__ __attribute__((aligned(16))) bf16 act[kRows][KC + kPad];
+template <int EPI>
+struct Epi {  // the epilogue's per-lane inputs, loaded (not yet converted) before the weights
+  f32x4 bias_f = {0.f, 0.f, 0.f, 0.f};
+  bf16x4 bias = {};
+  f32x4 x = {0.f, 0.f, 0.f, 0.f};
+  int pos = 0;
+};
+
+// WAVES waves, each over a K range of KW (K = WAVES * KW).
+template <int PRO, int EPI, int KW, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
+  constexpr int K = WAVES * KW, NT = KW / 32;  // MFMA k-steps per wave
+  constexpr int LDS_K = PRO == kProLn ? K : 1;
+  static_assert(PRO != kProLn || WAVES == 4, "the LayerNorm prologue uses 16 threads per row");
+  __shared__ __attribute__((aligned(16))) bf16 act[kRows][LDS_K + kPad];
+  __shared__ f32x4 red[WAVES - 1][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int n0 = blockIdx.x * 64 + wave * 16;
-  const int chunk = blockIdx.y, k0 = chunk * KC;
+  const int n0 = blockIdx.x * 16, kw0 = wave * KW;
+  const int M = a.M, N = a.N;
+  const int m = lane & 15, nl = n0 + 4 * (lane >> 4);  // this lane's row and first column
+  const bool full4 = nl + 3 < N;                       // its 4 columns all exist
 
-  // Issue order: the prologue's (small) loads first, then this wave's weight operands, so
-  // the prologue math waits only for its own data (loads complete in order) while the
-  // weights keep streaming.
-  bf16x8 w[NT];
-  auto load_weights = [&] {
-    // row n of W^T (clamped to N-1 past the edge; those columns are not stored), 8 k per lane
-    const int n = min(n0 + (lane & 15), a.N - 1);
-    const bf16* wp = a.wt + (size_t)n * a.K + k0 + 8 * (lane >> 4);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) w[t] = *reinterpret_cast<const bf16x8*>(wp + 32 * t);
-  };
-
-  // prologue: the activations of this chunk into LDS (rows m >= M are zero); loads use
-  // clamped, always-valid addresses
-  if constexpr (PRO == kProRows) {
-    constexpr int PER = kRows * KC / 8 / 256;  // 16-byte pieces per thread
-    static_assert(PER * 256 * 8 == kRows * KC, "whole pieces per thread");
-    bf16x8 v[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int p = tid + 256 * i, m = p / (KC / 8), j = 8 * (p % (KC / 8));
-      v[i] = *reinterpret_cast<const bf16x8*>(a.act + (size_t)min(m, a.M - 1) * a.K + k0 + j);
-    }
-    load_weights();
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int p = tid + 256 * i, m = p / (KC / 8), j = 8 * (p % (KC / 8));
-      if (m >= a.M) v[i] = bf16x8{};
-      *reinterpret_cast<bf16x8*>(&act[m][j]) = v[i];
-    }
-  } else if constexpr (PRO == kProGelu) {
-    constexpr int PER = kRows * KC / 4 / 256;  // 4-float pieces per thread
-    static_assert(PER * 256 * 4 == kRows * KC, "whole pieces per thread");
-    f32x4 v[PER], bias[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int p = tid + 256 * i, m = p / (KC / 4), j = 4 * (p % (KC / 4));
-      v[i] = *reinterpret_cast<const f32x4*>(a.in_parts + (size_t)min(m, a.M - 1) * a.K + k0 + j);
-      bias[i] = ld_bf16x4(a.in_bias + k0 + j);
-    }
-    for (int sp = 1; sp < a.in_splits; ++sp) {
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int p = tid + 256 * i, m = p / (KC / 4), j = 4 * (p % (KC / 4));
-        v[i] += *reinterpret_cast<const f32x4*>(
-            a.in_parts + ((size_t)sp * a.M + min(m, a.M - 1)) * a.K + k0 + j);
+  // 0. the epilogue's inputs (wave 0 finishes the outputs), first in the load queue
+  Epi<EPI> ep;
+  if (wave == 0 && m < M && nl < N) {
+    if constexpr (EPI == kEpiQkv) {
+      ep.pos = a.pos[m];
+      ep.bias_f = *reinterpret_cast<const f32x4*>(a.bias_f + nl);  // 3d is a multiple of 16
+    } else if constexpr (EPI != kEpiStore) {
+      if (full4) {
+        ep.bias = *reinterpret_cast<const bf16x4*>(a.bias + nl);
+        if constexpr (EPI == kEpiResidual)
+          ep.x = *reinterpret_cast<const f32x4*>(a.x_out + (size_t)m * N + nl);
+      } else {
+        for (int r = 0; nl + r < N; ++r) {
+          ep.bias[r] = a.bias[nl + r];
+          if constexpr (EPI == kEpiResidual) ep.x[r] = a.x_out[(size_t)m * N + nl + r];
+        }
       }
     }
-    load_weights();
+  }
+
+  // 0b. the LayerNorm prologue's rows and parameters (16 threads per row, K/16 values each),
+  //     also ahead of the weights
+  constexpr int NV = PRO == kProLn ? K / 64 : 1;  // float4 pieces per thread
+  const int lr = tid >> 4, lj = tid & 15;
+  f32x4 xv[NV];
+  bf16x4 lw[NV], lb[NV];
+  if constexpr (PRO == kProLn) {
+    static_assert(K % 64 == 0 && K <= kMaxLnK, "row fits the registers");
+    const int rr = min(lr, M - 1);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int p = tid + 256 * i, m = p / (KC / 4), j = 4 * (p % (KC / 4));
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        act[m][j + e] = static_cast<bf16>(m < a.M ? gelu_tanh(v[i][e] + bias[i][e]) : 0.0f);
+    for (int i = 0; i < NV; ++i) {
+      const int c = 4 * (lj + 16 * i);
+      xv[i] = *reinterpret_cast<const f32x4*>(a.x + (size_t)rr * K + c);
+      lw[i] = *reinterpret_cast<const bf16x4*>(a.ln_w + c);
+      lb[i] = *reinterpret_cast<const bf16x4*>(a.ln_b + c);
     }
-  } else {  // kProLayerNorm: 16 threads per row, the whole row (K = KC) in registers
-    static_assert(KC % 64 == 0 && KC / 64 <= kMaxLnVals / 4, "row fits the registers");
-    constexpr int NV = KC / 64;  // float4 pieces per thread
-    const int m = tid >> 4, j = tid & 15, mm = min(m, a.M - 1);
-    f32x4 v[NV];
+  }
+
+  // 1. this wave's weight operands: row n of W^T (clamped to N-1 past the edge; those columns
+  //    are not stored), 8 k per lane and step; all issued before anything waits
+  bf16x8 w[NT];
+  {
+    const bf16* wp = a.wt + (size_t)min(n0 + (lane & 15), N - 1) * K + kw0 + 8 * (lane >> 4);
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
-      v[i] = *reinterpret_cast<const f32x4*>(a.x_in + (size_t)mm * a.K + 4 * (j + 16 * i));
-    for (int sp = 0; sp < a.in_splits; ++sp) {
+    for (int t = 0; t < NT; ++t) w[t] = *reinterpret_cast<const bf16x8*>(wp + 32 * t);
+  }
+  // (nothing that consumes a load moves above here: every load is in flight before the first
+  // wait)
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. B operands: lane holds batch row m = lane%16 (rows m >= M are zero), k = 8(lane/16) ..
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (PRO == kProRows) {
+    const bf16* ap = a.act + (size_t)min(m, M - 1) * K + kw0 + 8 * (lane >> 4);
+    bf16x8 b[NT];
 #pragma unroll
-      for (int i = 0; i < NV; ++i)
-        v[i] += *reinterpret_cast<const f32x4*>(a.in_parts + ((size_t)sp * a.M + mm) * a.K +
-                                                4 * (j + 16 * i));
-    }
-    if (a.in_bias) {
+    for (int t = 0; t < NT; ++t) b[t] = *reinterpret_cast<const bf16x8*>(ap + 32 * t);
 #pragma unroll
-      for (int i = 0; i < NV; ++i) v[i] += ld_bf16x4(a.in_bias + 4 * (j + 16 * i));
-    }
-    load_weights();
+    for (int t = 0; t < NT; ++t)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[t], m < M ? b[t] : bf16x8{}, acc, 0, 0,
+                                                    0);
+  } else {
+    // LayerNorm of the 16 rows into LDS (two-pass mean and variance in fp32, eps 1e-5)
     float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) sum += v[i][0] + v[i][1] + v[i][2] + v[i][3];
-    const float mean = sum16(sum) / (float)a.K;
+    for (int i = 0; i < NV; ++i) sum += xv[i][0] + xv[i][1] + xv[i][2] + xv[i][3];
+    const float mean = sum16(sum) / (float)K;
     float sq = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sq += (v[i][e] - mean) * (v[i][e] - mean);
-    const float inv_std = 1.0f / sqrtf(sum16(sq) / (float)a.K + 1e-5f);
-    const bool store_x = a.x_out && blockIdx.x == 0 && blockIdx.y == 0 && m < a.M;
+      for (int e = 0; e < 4; ++e) sq += (xv[i][e] - mean) * (xv[i][e] - mean);
+    const float inv_std = 1.0f / sqrtf(sum16(sq) / (float)K + 1e-5f);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int c = 4 * (j + 16 * i);
-      if (store_x) *reinterpret_cast<f32x4*>(a.x_out + (size_t)m * a.K + c) = v[i];
-      const f32x4 g = ld_bf16x4(a.ln_w + c), b = ld_bf16x4(a.ln_b + c);
       bf16x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        o[e] = static_cast<bf16>(m < a.M ? (v[i][e] - mean) * inv_std * g[e] + b[e] : 0.0f);
-      *reinterpret_cast<bf16x4*>(&act[m][c]) = o;
+        o[e] = static_cast<bf16>(lr < M ? (xv[i][e] - mean) * inv_std * (float)lw[i][e] +
+                                              (float)lb[i][e]
+                                        : 0.0f);
+      *reinterpret_cast<bf16x4*>(&act[lr][4 * (lj + 16 * i)]) = o;
     }
+    __syncthreads();
+    const bf16* ap = &act[m][kw0 + 8 * (lane >> 4)];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          w[t], *reinterpret_cast<const bf16x8*>(ap + 32 * t), acc, 0, 0, 0);
   }
+
+  // 3. sum the waves' products (wave 0 keeps the result): lane holds out[m][nl + r]
+  if (wave > 0) red[wave - 1][lane] = acc;
   __syncthreads();
-
-  // 3. D = W^T A^T over the chunk
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const bf16* arow = &act[lane & 15][8 * (lane >> 4)];
+  if (wave > 0) return;
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-        w[t], *reinterpret_cast<const bf16x8*>(arow + 32 * t), acc, 0, 0, 0);
-
-  // 4. lane holds out[m = lane%16][n0 + 4(lane/16) + r]
-  const int m = lane & 15;
-  if (m < a.M) {
-    float* out = a.parts + ((size_t)chunk * a.M + m) * a.N;
+  for (int i = 0; i < WAVES - 1; ++i) acc += red[i][lane];
+  if (m >= M || nl >= N) return;
+  if constexpr (EPI == kEpiStore) {
+    float* o = a.out + (size_t)m * N + nl;
+    if (full4 && (((size_t)m * N + nl) & 3) == 0)
+      *reinterpret_cast<f32x4*>(o) = acc;
+    else
+      for (int r = 0; nl + r < N && r < 4; ++r) o[r] = acc[r];
+  } else if constexpr (EPI == kEpiGelu) {
+    bf16x4 o;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int n = n0 + 4 * (lane >> 4) + r;
-      if (n < a.N) out[n] = acc[r];
+    for (int r = 0; r < 4; ++r)
+      o[r] = static_cast<bf16>(gelu_tanh(acc[r] + (float)ep.bias[r]));
+    bf16* g = a.g + (size_t)m * N + nl;
+    if (full4)
+      *reinterpret_cast<bf16x4*>(g) = o;
+    else
+      for (int r = 0; nl + r < N; ++r) g[r] = o[r];
+  } else if constexpr (EPI == kEpiResidual) {
+    const f32x4 xn = ep.x + acc +
+                     f32x4{(float)ep.bias[0], (float)ep.bias[1], (float)ep.bias[2], (float)ep.bias[3]};
+    float* x = a.x_out + (size_t)m * N + nl;
+    if (full4)
+      *reinterpret_cast<f32x4*>(x) = xn;
+    else
+      for (int r = 0; nl + r < N; ++r) x[r] = xn[r];
+  } else {  // kEpiQkv: the 4 columns lie in one head (d_head is a multiple of 4)
+    const f32x4 val = acc + ep.bias_f;
+    const int d = N / 3, which = nl / d, c = nl % d, hh = c / a.dh, ee = c % a.dh;
+    const size_t head = (size_t)m * a.H + hh;
+    const size_t idx = which == 0 ? head * a.dh + ee : (head * a.max_len + ep.pos) * a.dh + ee;
+    void* dst = which == 0 ? a.q : which == 1 ? a.kcache : a.vcache;
+    if (a.qkv_fp32) {
+      *reinterpret_cast<f32x4*>(static_cast<float*>(dst) + idx) = val;
+    } else {
+      bf16x4 o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = static_cast<bf16>(val[r]);
+      *reinterpret_cast<bf16x4*>(static_cast<bf16*>(dst) + idx) = o;
     }
   }
 }
@@ -193,42 +235,54 @@ __global__ void transpose_kernel(bf16* out, const bf16* in, int rows, int cols) 
   }
 }
 
+template <int PRO, int EPI, int KW, int WAVES>
+hipError_t launch_kw(const SkinnyArgs& a, hipStream_t s) {
+  if constexpr (PRO == kProLn && (WAVES != 4 || 4 * KW > kMaxLnK)) {
+    return hipErrorInvalidValue;
+  } else {
+    skinny_kernel<PRO, EPI, KW, WAVES><<<dim3((a.N + 15) / 16), 64 * WAVES, 0, s>>>(a);
+    return hipGetLastError();
+  }
+}
+
+// The LayerNorm prologue splits K over 4 waves; the row prologue keeps each wave's range at
+// 128-256 (so all of a wave's loads fit in registers at once) with up to 16 waves.
+template <int PRO, int EPI>
+hipError_t launch_k(const SkinnyArgs& a, hipStream_t s) {
+  switch (a.K) {  // the reduction lengths of the supported configurations
+    case 128: return launch_kw<PRO, EPI, 32, 4>(a, s);
+    case 512: return launch_kw<PRO, EPI, 128, 4>(a, s);
+    case 768: return launch_kw<PRO, EPI, 192, 4>(a, s);
+    case 1024: return launch_kw<PRO, EPI, 256, 4>(a, s);
+    case 2048: return launch_kw<PRO, EPI, 128, 16>(a, s);
+    case 3072: return launch_kw<PRO, EPI, 192, 16>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace
 
 bool skinny_supported(int M, int K) {
-  return M >= 1 && M <= kRows && K % 128 == 0 && K >= 128;
+  return M >= 1 && M <= kRows &&
+         (K == 128 || K == 512 || K == 768 || K == 1024 || K == 2048 || K == 3072);
 }
 
-// The K-chunk of a reduction: the largest of 768, 512, 384, 256, 128 that divides K.
-int skinny_chunk(int K) {
-  for (int kc : {768, 512, 384, 256, 128})
-    if (K % kc == 0) return kc;
-  return 128;
-}
-
-namespace {
-template <int PRO>
-hipError_t launch_pro(const SkinnyArgs& a, dim3 grid, hipStream_t s) {
-  switch (a.kc) {
-    case 128: skinny_gemm_kernel<PRO, 128><<<grid, 256, 0, s>>>(a); break;
-    case 256: skinny_gemm_kernel<PRO, 256><<<grid, 256, 0, s>>>(a); break;
-    case 384: skinny_gemm_kernel<PRO, 384><<<grid, 256, 0, s>>>(a); break;
-    case 512: skinny_gemm_kernel<PRO, 512><<<grid, 256, 0, s>>>(a); break;
-    case 768: skinny_gemm_kernel<PRO, 768><<<grid, 256, 0, s>>>(a); break;
+hipError_t skinny_gemm(int pro, int epi, const SkinnyArgs& a, hipStream_t s) {
+  if (!skinny_supported(a.M, a.K) || a.N < 1) return hipErrorInvalidValue;
+  if (pro == kProLn && a.K > kMaxLnK) return hipErrorInvalidValue;
+  if (epi == kEpiQkv && (a.N % 3 || (a.N / 3) % a.dh)) return hipErrorInvalidValue;
+  if (pro == kProRows) {
+    switch (epi) {
+      case kEpiStore: return launch_k<kProRows, kEpiStore>(a, s);
+      case kEpiResidual: return launch_k<kProRows, kEpiResidual>(a, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  switch (epi) {
+    case kEpiQkv: return launch_k<kProLn, kEpiQkv>(a, s);
+    case kEpiGelu: return launch_k<kProLn, kEpiGelu>(a, s);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
-}
-}  // namespace
-
-hipError_t skinny_gemm(int pro, const SkinnyArgs& args, hipStream_t s) {
-  if (!skinny_supported(args.M, args.K) || args.K % args.kc ||
-      (pro == kProLayerNorm && args.kc != args.K))
-    return hipErrorInvalidValue;
-  const dim3 grid((args.N + 63) / 64, args.K / args.kc);
-  if (pro == kProRows) return launch_pro<kProRows>(args, grid, s);
-  if (pro == kProLayerNorm) return launch_pro<kProLayerNorm>(args, grid, s);
-  return launch_pro<kProGelu>(args, grid, s);
 }
 
 hipError_t transpose(bf16* out, const bf16* in, int rows, int cols, hipStream_t s) {
