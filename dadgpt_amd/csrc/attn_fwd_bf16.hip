@@ -26,9 +26,10 @@
 //
 // The launch bound caps registers so that several waves share each SIMD, which interleaves
 // one wave's softmax with another's MFMAs and covers LDS latency. K and V tiles are
-// triple-buffered in LDS and staged by direct global->LDS loads (no registers, no LDS-store
-// instructions): tiles t+1 and t+2 are in flight while tile t is on the MFMA pipes; one
-// barrier per tile.
+// double-buffered in LDS and staged by direct global->LDS loads (no registers, no LDS-store
+// instructions): tile t+1 is in flight while tile t is on the MFMA pipes; one barrier per
+// tile. (Triple buffering measured slower: the third buffer's LDS cost more than the extra
+// tile of lead gained.)
 #include "common.hpp"
 #include "kernels.hpp"
 #include "tiles.hpp"
@@ -198,17 +199,17 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
   constexpr int QB = kQW * kWaves;
   constexpr int DS = D / 16;  // 16-wide K-steps along D
   constexpr int DB = D / 32;  // 32-row blocks of O^T
-  // K and V tiles, triple-buffered: tile t is read while t+1 and t+2 are in flight. With the
-  // tile loop unrolled by three every access names its buffer by a constant index, so the
-  // compiler addresses all three from one register and knows that a pending direct load into
-  // one buffer does not alias reads of another (it inserts no wait for it).
-  __shared__ __attribute__((aligned(16))) bf16 sk[3][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sv[3][kTileRows * D];
+  // K and V tiles, double-buffered: tile t is read while t+1 is in flight. With the tile loop
+  // unrolled by two every access names its buffer by a constant index, so the compiler
+  // addresses both from one register.
+  __shared__ __attribute__((aligned(16))) bf16 sk[2][kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 sv[2][kTileRows * D];
   __shared__ f32x4 smask[4][64];
 
   const int bh = blockIdx.x;
   const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
   const int l32 = lane & 31, hi = lane >> 5;
   const size_t base = (size_t)bh * S * D;
   const bf16* qg = q + base;
@@ -241,18 +242,13 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
 
   if (wave == 0) write_mask_table(smask, lane);  // published by the first barrier
 
-  // The first two tiles load alongside Q, under one wait; Q is touched only after it (the
+  // The first tile loads alongside Q, under one wait; Q is touched only after it (the
   // compiler, which does not see the direct loads, then has nothing left to wait for).
   using Dma = DmaTile<D, kWaves>;
-  constexpr int NI = 2 * Dma::PER_WAVE;  // DMA instructions per wave per tile (K and V)
   uint32_t doff[Dma::PER_WAVE];
   Dma::offsets(doff, wave, lane);
   Dma::load_any(sk[0], kg, 0, S, doff, wave, lane);
   Dma::load_any(sv[0], vg, 0, S, doff, wave, lane);
-  if (n_tiles > 1) {
-    Dma::load_any(sk[1], kg, kTileRows, S, doff, wave, lane);
-    Dma::load_any(sv[1], vg, kTileRows, S, doff, wave, lane);
-  }
   wait_vm_lds<0>();
   __builtin_amdgcn_s_barrier();
 #pragma unroll
@@ -263,20 +259,19 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
       if (negate_q) qop[i][ds] = neg_bf16x8(qop[i][ds]);
     }
 
-  // One key tile: prefetch tile t+2 into (nk, nv) (it held tile t-1, released by the last
-  // barrier), compute tile t from (ck, cv), then wait for tile t+1 (only tile t+2's loads may
-  // still be in flight) and barrier, which also ends every wave's reads of tile t.
+  // One key tile: prefetch tile t+1 into (nk, nv) (it held tile t-1, released by the last
+  // barrier), compute tile t from (ck, cv), then wait for tile t+1 and barrier, which also
+  // ends every wave's reads of tile t.
   auto tile = [&](int t, const bf16* ck, const bf16* cv, bf16* nk, bf16* nv) {
     const int k0 = t * kTileRows;
-    const bool prefetch = t + 2 < n_tiles;
+    const bool prefetch = t + 1 < n_tiles;
     if (prefetch) {
-      Dma::load_any(nk, kg, k0 + 2 * kTileRows, S, doff, wave, lane);
-      Dma::load_any(nv, vg, k0 + 2 * kTileRows, S, doff, wave, lane);
+      Dma::load_any(nk, kg, k0 + kTileRows, S, doff, wave, lane);
+      Dma::load_any(nv, vg, k0 + kTileRows, S, doff, wave, lane);
     }
     if (q0 < S && k0 <= q0 + kQW - 1) {  // some key of the tile at or before a query
-      // One 32-key chunk at a time: the operand reads of a chunk are issued together, and
-      // the other waves on the SIMD (three per SIMD) cover their latency. Holding both
-      // chunks' scores at once measured no faster and costs registers.
+      // One 32-key chunk at a time (holding both chunks' scores at once measured no faster
+      // and costs registers); the other waves on the SIMD cover the operand reads' latency.
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const int c0 = k0 + 32 * kb;
@@ -284,25 +279,23 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
         bf16x8 ka[DS], va[DB][2];
         f32x16 sc[kNQB];
         fwd_k_ops<D>(ka, ck, kb, lane);
-        fwd_v_ops<D>(va, cv, kb, lane);
         // the chunk whose first key is the wave's first query is the one to mask
         if (c0 == q0)
           fwd_scores<D, kNQB>(sc, qop, ka, read_mask_table(smask, lane));
         else
           fwd_scores<D, kNQB>(sc, qop, ka, f32x16{});
+        // V^T operands only now (K's are dead): their latency hides under the softmax
+        __builtin_amdgcn_sched_barrier(0);
+        fwd_v_ops<D>(va, cv, kb, lane);
         fwd_softmax_pv<D, kNQB>(sc, oacc, mrun, lrun, va, scale_log2);
       }
     }
-    if (prefetch)
-      wait_vm_lds<NI>();
-    else
-      wait_vm_lds<0>();
+    wait_vm_lds<0>();
     __builtin_amdgcn_s_barrier();
   };
-  for (int t = 0; t < n_tiles; t += 3) {
-    tile(t, sk[0], sv[0], sk[2], sv[2]);
+  for (int t = 0; t < n_tiles; t += 2) {
+    tile(t, sk[0], sv[0], sk[1], sv[1]);
     if (t + 1 < n_tiles) tile(t + 1, sk[1], sv[1], sk[0], sv[0]);
-    if (t + 2 < n_tiles) tile(t + 2, sk[2], sv[2], sk[1], sv[1]);
   }
 
   // ---- epilogue: O = O^T / l, lse = ln2 * (m + log2 l) ----

@@ -116,8 +116,14 @@ struct RowTile {
 // that publishes a tile. The compiler's own vector-memory waits stay correct because loads
 // complete in order, so unseen younger loads can only lengthen them. M0 is written here and
 // used by nothing else in these kernels.
+// LDS byte offset of a generic pointer into LDS: the low 32 bits of a flat address in the
+// shared aperture are the LDS address (an address-space cast would add a null check).
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(uintptr_t)p;
+}
+
 __device__ __forceinline__ void dma_lds(const void* gsrc, const void* lds_dst, int bytes) {
-  const uint32_t lds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst;
+  const uint32_t lds = lds_offset(lds_dst);
   const uint32_t base = __builtin_amdgcn_readfirstlane(lds);  // wave-uniform destination
   if (bytes == 16)
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
@@ -135,7 +141,7 @@ __device__ __forceinline__ void dma_lds(const void* gsrc, const void* lds_dst, i
 // (the instruction's saddr form): a tile loop moves only the scalar base.
 __device__ __forceinline__ void dma_lds16_sbase(const void* gbase, uint32_t voff,
                                                 const void* lds_dst) {
-  const uint32_t lds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst;
+  const uint32_t lds = lds_offset(lds_dst);
   const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
@@ -144,7 +150,7 @@ __device__ __forceinline__ void dma_lds16_sbase(const void* gbase, uint32_t voff
 }
 __device__ __forceinline__ void dma_lds4_sbase(const void* gbase, uint32_t voff,
                                                const void* lds_dst) {
-  const uint32_t lds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst;
+  const uint32_t lds = lds_offset(lds_dst);
   const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
                :
