@@ -16,7 +16,7 @@
 // row-major LDS tiles with ds_read_b64_tr_b16, so every tile is staged once, row-major.
 // Masking is compiled only into the blocks that straddle the diagonal (template DIAG), so the
 // other blocks run branch-free. The streamed tiles (Q and dO for dK/dV, K and V for dQ) are
-// triple-buffered in LDS through direct global->LDS loads, two tiles ahead of the compute.
+// double-buffered in LDS through direct global->LDS loads, one tile ahead of the compute.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "tiles.hpp"
@@ -101,32 +101,40 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
   constexpr int DS = D / 16, DB = D / 32;
   const int l32 = lane & 31, hi = lane >> 5;
   const int qr = 32 * qb + sigma32(l32);
-  bf16x8 qa[DS], da[DS];
+  // Phases, fenced so the compiler keeps them apart (each phase's operands are dead before
+  // the next one's are read): S = stats + Q K^T, dP = stats + dO V^T, softmax,
+  // dV += dO^T P, dK += Q^T dS.
+  auto stats = [&](const float* row, f32x16& acc) {
 #pragma unroll
-  for (int ds = 0; ds < DS; ++ds) {
-    qa[ds] = lds_op(sq, rm_off<D>(qr, 2 * ds + hi));
-    da[ds] = lds_op(sdo, rm_off<D>(qr, 2 * ds + hi));
-  }
-  f32x16 s, dp;
+    for (int j = 0; j < 2; ++j) {
+      const int qt0 = 32 * qb + 16 * j + 8 * hi;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int qt0 = 32 * qb + 16 * j + 8 * hi;
+      for (int h = 0; h < 2; ++h) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(row + qt0 + 4 * h);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(slc + qt0 + 4 * h);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(sdl + qt0 + 4 * h);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s[8 * j + 4 * h + e] = a[e];
-        dp[8 * j + 4 * h + e] = b[e];
+        for (int e = 0; e < 4; ++e) acc[8 * j + 4 * h + e] = a[e];
       }
     }
-  }
+  };
+  f32x16 s, dp;
+  {
+    bf16x8 qa[DS];
 #pragma unroll
-  for (int ds = 0; ds < DS; ++ds) {
-    s = mfma32(qa[ds], kop[ds], s);
-    dp = mfma32(da[ds], vop[ds], dp);
+    for (int ds = 0; ds < DS; ++ds) qa[ds] = lds_op(sq, rm_off<D>(qr, 2 * ds + hi));
+    stats(slc, s);
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) s = mfma32(qa[ds], kop[ds], s);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    bf16x8 da[DS];
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) da[ds] = lds_op(sdo, rm_off<D>(qr, 2 * ds + hi));
+    stats(sdl, dp);
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) dp = mfma32(da[ds], vop[ds], dp);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   bf16x8 pb[2], dsb[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -150,14 +158,29 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
     pb[j] = as_bf16x8(wp);
     dsb[j] = as_bf16x8(wd);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    bf16x8 t[DB][2];  // A = dO^T: lane d = 32db + l32 gets tile queries 32qb + 16j + 8hi + 0..7
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      // A = dO^T / Q^T: lane d = 32db + l32 gets tile queries 32qb + 16j + 8hi + 0..7
-      dvacc[db] = mfma32(lds_tr_op<D>(sdo, 32 * qb + 16 * j, 32 * db, lane), pb[j], dvacc[db]);
-      dkacc[db] = mfma32(lds_tr_op<D>(sq, 32 * qb + 16 * j, 32 * db, lane), dsb[j], dkacc[db]);
-    }
+      for (int j = 0; j < 2; ++j) t[db][j] = lds_tr_op<D>(sdo, 32 * qb + 16 * j, 32 * db, lane);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) dvacc[db] = mfma32(t[db][j], pb[j], dvacc[db]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    bf16x8 t[DB][2];  // A = Q^T
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) t[db][j] = lds_tr_op<D>(sq, 32 * qb + 16 * j, 32 * db, lane);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) dkacc[db] = mfma32(t[db][j], dsb[j], dkacc[db]);
   }
 }
 
@@ -169,13 +192,13 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
     float lse_mul, float dk_mul) {
   constexpr int KB = kKW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
-  // Q and dO tiles, triple-buffered (constant buffer indices in the unrolled loop; see the
+  // Q and dO tiles, double-buffered (constant buffer indices in the unrolled loop; see the
   // forward kernel), and per wave and buffer the tile's lse and delta rows, converted in place
   // to -lse/scale and -delta: each wave loads and converts its own copy, so the conversion
   // needs no barrier.
-  __shared__ __attribute__((aligned(16))) bf16 sq[3][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sdo[3][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) float sst[kWaves][3][2][kTileRows];
+  __shared__ __attribute__((aligned(16))) bf16 sq[2][kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 sdo[2][kTileRows * D];
+  __shared__ __attribute__((aligned(16))) float sst[kWaves][2][2][kTileRows];
 
   const int bh = blockIdx.x;
   const int kblk = blockIdx.y;  // key block 0 sees the most query tiles: dispatched first
@@ -213,7 +236,6 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
 
   // Direct loads per wave per tile: its share of Q and dO, and its own lse and delta rows.
   using Dma = DmaTile<D, kWaves>;
-  constexpr int NI = 2 * Dma::PER_WAVE + 2;
   uint32_t doff[Dma::PER_WAVE];
   Dma::offsets(doff, wave, lane);
   float(*st)[2][kTileRows] = sst[wave];
@@ -223,20 +245,19 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
     dma_row64(st[buf][0], lseg, t * kTileRows, S, lane);
     dma_row64(st[buf][1], delg, t * kTileRows, S, lane);
   };
-  // The first two tiles load alongside the operands above: one wait covers all of them (the
+  // The first tile loads alongside the operands above: one wait covers all of them (the
   // compiler, which does not see the direct loads, then has nothing left to wait for).
   issue(t_first, sq[0], sdo[0], 0);
-  if (t_first + 1 < t_end) issue(t_first + 1, sq[1], sdo[1], 1);
   wait_vm_lds<0>();
   __builtin_amdgcn_s_barrier();
 
-  // One query tile: prefetch tile t+2 (into the buffers of tile t-1, released by the last
-  // barrier), convert this wave's lse row, compute tile t, wait for tile t+1 and barrier.
+  // One query tile: prefetch tile t+1 (into the buffers of tile t-1, released by the last
+  // barrier), convert this wave's statistics rows, compute tile t, wait for tile t+1 and
+  // barrier.
   auto tile = [&](int t, const bf16* cq, const bf16* cdo, int cb, bf16* nq, bf16* ndo,
                   int nb) {
     const int r0 = t * kTileRows;
-    const bool prefetch = t + 2 < t_end;
-    if (prefetch) issue(t + 2, nq, ndo, nb);
+    if (t + 1 < t_end) issue(t + 1, nq, ndo, nb);
     if (kw0 < S && r0 + kTileRows - 1 >= kw0) {
       // -lse/scale and -delta (this wave's copy; its LDS accesses complete in order)
       st[cb][0][lane] *= lse_mul;
@@ -255,16 +276,12 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
                                key - r0, S - r0, lane, c);
       }
     }
-    if (prefetch)
-      wait_vm_lds<NI>();
-    else
-      wait_vm_lds<0>();
+    wait_vm_lds<0>();
     __builtin_amdgcn_s_barrier();
   };
-  for (int t = t_first; t < t_end; t += 3) {
-    tile(t, sq[0], sdo[0], 0, sq[2], sdo[2], 2);
+  for (int t = t_first; t < t_end; t += 2) {
+    tile(t, sq[0], sdo[0], 0, sq[1], sdo[1], 1);
     if (t + 1 < t_end) tile(t + 1, sq[1], sdo[1], 1, sq[0], sdo[0], 0);
-    if (t + 2 < t_end) tile(t + 2, sq[2], sdo[2], 2, sq[1], sdo[1], 1);
   }
 
   if (key < S) {
@@ -325,9 +342,9 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
     const float* __restrict__ delta, int S, float scale_log2, float scale) {
   constexpr int QB = kQW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
-  // K and V tiles, triple-buffered (constant buffer indices; see the forward kernel).
-  __shared__ __attribute__((aligned(16))) bf16 sk[3][kTileRows * D];
-  __shared__ __attribute__((aligned(16))) bf16 sv[3][kTileRows * D];
+  // K and V tiles, double-buffered (constant buffer indices; see the forward kernel).
+  __shared__ __attribute__((aligned(16))) bf16 sk[2][kTileRows * D];
+  __shared__ __attribute__((aligned(16))) bf16 sv[2][kTileRows * D];
 
   const int bh = blockIdx.x;
   const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
@@ -361,18 +378,13 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
   for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
 
   // Keys past S read row S-1; every chunk holding such keys is a DIAG chunk (the key is after
-  // every valid query), so they are masked. The first two tiles load alongside the operands
+  // every valid query), so they are masked. The first tile loads alongside the operands
   // above, under one wait (see the dK/dV kernel).
   using Dma = DmaTile<D, kWaves>;
-  constexpr int NI = 2 * Dma::PER_WAVE;
   uint32_t doff[Dma::PER_WAVE];
   Dma::offsets(doff, wave, lane);
   Dma::load_any(sk[0], kg, 0, S, doff, wave, lane);
   Dma::load_any(sv[0], vg, 0, S, doff, wave, lane);
-  if (n_tiles > 1) {
-    Dma::load_any(sk[1], kg, kTileRows, S, doff, wave, lane);
-    Dma::load_any(sv[1], vg, kTileRows, S, doff, wave, lane);
-  }
   wait_vm_lds<0>();
   __builtin_amdgcn_s_barrier();
   // Use the two statistics only from here on, so their load shares the wait above.
@@ -381,10 +393,9 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
 
   auto tile = [&](int t, const bf16* ck, const bf16* cv, bf16* nk, bf16* nv) {
     const int k0 = t * kTileRows;
-    const bool prefetch = t + 2 < n_tiles;
-    if (prefetch) {
-      Dma::load_any(nk, kg, k0 + 2 * kTileRows, S, doff, wave, lane);
-      Dma::load_any(nv, vg, k0 + 2 * kTileRows, S, doff, wave, lane);
+    if (t + 1 < n_tiles) {
+      Dma::load_any(nk, kg, k0 + kTileRows, S, doff, wave, lane);
+      Dma::load_any(nv, vg, k0 + kTileRows, S, doff, wave, lane);
     }
     if (q0 < S) {
 #pragma unroll
@@ -399,16 +410,12 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
                              scale_log2);
       }
     }
-    if (prefetch)
-      wait_vm_lds<NI>();
-    else
-      wait_vm_lds<0>();
+    wait_vm_lds<0>();
     __builtin_amdgcn_s_barrier();
   };
-  for (int t = 0; t < n_tiles; t += 3) {
-    tile(t, sk[0], sv[0], sk[2], sv[2]);
+  for (int t = 0; t < n_tiles; t += 2) {
+    tile(t, sk[0], sv[0], sk[1], sv[1]);
     if (t + 1 < n_tiles) tile(t + 1, sk[1], sv[1], sk[0], sv[0]);
-    if (t + 2 < n_tiles) tile(t + 2, sk[2], sv[2], sk[1], sv[1]);
   }
 
   if (qrow < S) store_rows_bf16<DB>(dq + base + (size_t)qrow * D, dqacc, scale, hi);
