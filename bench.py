@@ -184,6 +184,31 @@ class Workload:
         self.fwd()
         self.bwd()
 
+    def tokens(self):
+        """Forward and backward over the token-major layout of a fused QKV projection
+        ([B*T, 3*H*D] in, [B*T, H*D] out, gradient [B*T, 3*H*D]): the same kernels reading and
+        writing rows where the projections keep them, with no split/merge passes."""
+        import torch
+        A, HD = self.A, H * D
+        if not hasattr(self, "qkv"):
+            self.qkv = torch.cat([t.view(B, H, T, D).permute(0, 2, 1, 3).reshape(B * T, HD)
+                                  for t in (self.q, self.k, self.v)], dim=1).contiguous()
+            self.g_tok = self.g.view(B, H, T, D).permute(0, 2, 1, 3).reshape(B * T, HD).clone()
+            self.o_tok = torch.empty_like(self.g_tok)
+            self.dqkv = torch.empty_like(self.qkv)
+        qkv, dqkv = self.qkv, self.dqkv
+
+        def fwd():
+            A.flash_attention_forward_bf16_tokens(self.o_tok, HD, self.lse, qkv, qkv[:, HD:],
+                                                  qkv[:, 2 * HD:], 3 * HD, B, H, T, D, SCALE)
+
+        def bwd():
+            A.flash_attention_backward_bf16_tokens(dqkv, dqkv[:, HD:], dqkv[:, 2 * HD:], 3 * HD,
+                                                   self.delta, self.g_tok, self.o_tok, HD,
+                                                   self.lse, qkv, qkv[:, HD:], qkv[:, 2 * HD:],
+                                                   3 * HD, B, H, T, D, SCALE)
+        return fwd, bwd
+
     def decode(self, i):
         self.A.decode_attention(self.od, self.qd, self.kcs[i % self.ncopy],
                                 self.vcs[i % self.ncopy], self.lens, DEC_N, DEC_H, DEC_L, DEC_D,
@@ -328,6 +353,11 @@ def main():
         "bwd_dkdv": event_time_ms(wl.phase(2), args.reps, stream),
     }
     bwd_ms = event_time_ms(wl.bwd, args.reps, stream)
+    tok_fwd, tok_bwd = wl.tokens()
+    for _ in range(5):
+        tok_fwd()
+        tok_bwd()
+    tok_ms = (event_time_ms(tok_fwd, args.reps, stream), event_time_ms(tok_bwd, args.reps, stream))
     print(f"[bench] kernels {json.dumps({k: round(x, 4) for k, x in kern_ms.items()})}",
           file=sys.stderr, flush=True)
 
@@ -366,6 +396,12 @@ def main():
         tf = fl / (ms * 1e-3) / 1e12
         comps[name] = {"ms": round(ms, 5), "tflops": round(tf, 2),
                        "frac_mfma_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+    comps["tokens_layout"] = {
+        "fwd_ms": round(tok_ms[0], 5), "bwd_ms": round(tok_ms[1], 5),
+        "fwd_tflops": round(FWD_FLOPS / (tok_ms[0] * 1e-3) / 1e12, 2),
+        "bwd_tflops": round(BWD_FLOPS / (tok_ms[1] * 1e-3) / 1e12, 2),
+        "layout": "q,k,v in one token-major [B*T, 3*H*D] buffer, out/dout [B*T, H*D], "
+                  "dq,dk,dv into one [B*T, 3*H*D] buffer"}
     comps["decode"] = {"us_per_launch": round(dec_ms * 1e3, 3), "bytes": wl.dec_bytes,
                        "gbps": round(dec_gbps, 1),
                        "frac_hbm_peak": round(dec_gbps / PEAK_HBM_GBPS, 4),

@@ -34,6 +34,10 @@ C_SYMBOLS = (
     "dadgpt_flash_attention_forward_bf16",
     "dadgpt_flash_attention_backward_bf16",
     "dadgpt_flash_attention_backward_bf16_phase",
+    "dadgpt_flash_attention_forward_bf16_strided",
+    "dadgpt_flash_attention_backward_bf16_strided",
+    "dadgpt_flash_attention_forward_bf16_tokens",
+    "dadgpt_flash_attention_backward_bf16_tokens",
     "dadgpt_decode_workspace_bytes",
     "dadgpt_decode_attention_bf16",
     "dadgpt_decode_attention_f32",
@@ -45,6 +49,11 @@ CXX_SYMBOLS = (
 )
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported", 3: "hip error", 4: "workspace"}
+
+
+class HeadStrides(ctypes.Structure):
+    """dadgpt_head_strides: element strides of a [B, H, S, d_head] view (batch, head, row)."""
+    _fields_ = [("batch", ctypes.c_int64), ("head", ctypes.c_int64), ("row", ctypes.c_int64)]
 
 
 class LibraryNotBuilt(RuntimeError):
@@ -88,6 +97,15 @@ def lib():
     L.dadgpt_flash_attention_forward_bf16.argtypes = [vp] * 5 + [i, i, i, f, vp]
     L.dadgpt_flash_attention_backward_bf16.argtypes = [vp] * 10 + [i, i, i, f, vp]
     L.dadgpt_flash_attention_backward_bf16_phase.argtypes = [i] + [vp] * 10 + [i, i, i, f, vp]
+    i64, hs = ctypes.c_int64, ctypes.POINTER(HeadStrides)
+    L.dadgpt_flash_attention_forward_bf16_strided.argtypes = [vp] * 5 + [i, i, i, i, f, hs, vp]
+    L.dadgpt_flash_attention_backward_bf16_strided.argtypes = [vp] * 10 + [i, i, i, i, f, hs,
+                                                                          vp]
+    L.dadgpt_flash_attention_forward_bf16_tokens.argtypes = [vp, i64, vp, vp, vp, vp, i64, i, i,
+                                                             i, i, f, vp]
+    L.dadgpt_flash_attention_backward_bf16_tokens.argtypes = [vp, vp, vp, i64, vp, vp, vp, i64,
+                                                              vp, vp, vp, vp, i64, i, i, i, i, f,
+                                                              vp]
     L.dadgpt_decode_workspace_bytes.restype = sz
     L.dadgpt_decode_workspace_bytes.argtypes = [i, i, i, i]
     L.dadgpt_decode_attention_bf16.argtypes = [vp] * 5 + [i, i, i, i, f, vp, sz, vp]
@@ -198,6 +216,70 @@ def flash_attention_backward_bf16_phase(phase: int, dq, dk, dv, delta, dout, out
     _check(lib().dadgpt_flash_attention_backward_bf16_phase(
         int(phase), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta), _ptr(dout), _ptr(out), _ptr(lse),
         _ptr(q), _ptr(k), _ptr(v), BH, S, d_head, scale, _stream_ptr(stream)))
+
+
+# ------------------------------------------------ strided layouts (no split/merge passes)
+
+def _head_view(t, name, shape=None):
+    """A bf16 device view [B, H, S, d_head] whose rows are contiguous -> its strides."""
+    if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be a bfloat16 device tensor")
+    if t.dim() != 4 or t.stride(3) != 1:
+        raise ValueError(f"{name} must be a [B, H, S, d_head] view with contiguous rows")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    return HeadStrides(t.stride(0), t.stride(1), t.stride(2))
+
+
+def flash_attention_forward_bf16_strided(out, lse, q, k, v, scale: float, stream=None) -> None:
+    """Forward over [B, H, S, d_head] views of any row placement (e.g. heads sliced out of
+    the token-major projection output, or a KV cache's first S rows); lse [B*H, S] fp32.
+    Replaces split_heads + flash forward + merge_heads (src/model.cpp:384-392,423-424)."""
+    B, H, S, D = q.shape
+    st = (HeadStrides * 4)(*[_head_view(t, nm, (B, H, S, D))
+                             for t, nm in ((q, "q"), (k, "k"), (v, "v"), (out, "out"))])
+    _require(lse, "lse", torch.float32, B * H * S)
+    _check(lib().dadgpt_flash_attention_forward_bf16_strided(
+        _ptr(out), _ptr(lse), _ptr(q), _ptr(k), _ptr(v), B, H, S, D, scale, st,
+        _stream_ptr(stream)))
+
+
+def flash_attention_backward_bf16_strided(dq, dk, dv, delta, dout, out, lse, q, k, v,
+                                          scale: float, stream=None) -> None:
+    """Backward over [B, H, S, d_head] views (see flash_attention_forward_bf16_strided);
+    replaces split_heads + flash backward + 3 merge_heads (src/model.cpp:564-576,619-624)."""
+    B, H, S, D = q.shape
+    views = ((q, "q"), (k, "k"), (v, "v"), (out, "out"), (dout, "dout"), (dq, "dq"),
+             (dk, "dk"), (dv, "dv"))
+    st = (HeadStrides * 8)(*[_head_view(t, nm, (B, H, S, D)) for t, nm in views])
+    _require(delta, "delta", torch.float32, B * H * S)
+    _require(lse, "lse", torch.float32, B * H * S)
+    _check(lib().dadgpt_flash_attention_backward_bf16_strided(
+        _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta), _ptr(dout), _ptr(out), _ptr(lse), _ptr(q),
+        _ptr(k), _ptr(v), B, H, S, D, scale, st, _stream_ptr(stream)))
+
+
+def flash_attention_forward_bf16_tokens(out, ld_out: int, lse, q, k, v, ld_qkv: int, B: int,
+                                        H: int, S: int, d_head: int, scale: float,
+                                        stream=None) -> None:
+    """Token-major forward: rows b*S + s of q, k, v (pitch ld_qkv) and out (pitch ld_out)
+    hold the H heads side by side. q, k, v may be slices of one fused [B*S, 3*H*d_head]
+    projection output (ld_qkv = 3*H*d_head). Raw device buffers, as the C ABI."""
+    _check(lib().dadgpt_flash_attention_forward_bf16_tokens(
+        _ptr(out), ld_out, _ptr(lse), _ptr(q), _ptr(k), _ptr(v), ld_qkv, B, H, S, d_head, scale,
+        _stream_ptr(stream)))
+
+
+def flash_attention_backward_bf16_tokens(dq, dk, dv, ld_dqkv: int, delta, dout, out,
+                                         ld_out: int, lse, q, k, v, ld_qkv: int, B: int, H: int,
+                                         S: int, d_head: int, scale: float,
+                                         stream=None) -> None:
+    """Token-major backward (see flash_attention_forward_bf16_tokens); dq, dk, dv rows
+    ld_dqkv apart (3*H*d_head: the gradient of a fused QKV projection output)."""
+    _check(lib().dadgpt_flash_attention_backward_bf16_tokens(
+        _ptr(dq), _ptr(dk), _ptr(dv), ld_dqkv, _ptr(delta), _ptr(dout), _ptr(out), ld_out,
+        _ptr(lse), _ptr(q), _ptr(k), _ptr(v), ld_qkv, B, H, S, d_head, scale,
+        _stream_ptr(stream)))
 
 
 def decode_workspace_bytes(n_seq: int, n_heads: int, max_len: int, d_head: int) -> int:

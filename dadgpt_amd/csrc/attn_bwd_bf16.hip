@@ -36,22 +36,39 @@ constexpr int kDkdvMinBlocks = DADGPT_DKDV_MINB;
 constexpr int kDqMinBlocks = DADGPT_DQ_MINB;
 
 // ---------------------------------------------------------------- delta
-template <int D>
+template <int D, bool STRIDED>
 __global__ __launch_bounds__(256) void delta_bf16_kernel(float* __restrict__ delta,
                                                          const bf16* __restrict__ dout,
-                                                         const bf16* __restrict__ out,
-                                                         long rows) {
-  // 8 lanes per row, 16 bytes each per step.
+                                                         const bf16* __restrict__ out, int S,
+                                                         long long rows, int row_blocks,
+                                                         const AttnLayout L) {
+  // 32 rows per workgroup, 8 lanes per row, 16 bytes each per step. Contiguous: rows of the
+  // flat [BH*S, D] matrices (`rows` of them); strided: row_blocks workgroups per (b,h) slice.
   constexpr int LPR = 8;
-  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
-  const long row = gid / LPR;
-  const int part = (int)(gid % LPR);
+  const int part = threadIdx.x % LPR;
+  const bf16 *dor, *orow;
+  long long drow;  // row of delta
+  bool valid;
+  if constexpr (STRIDED) {
+    const int bh = blockIdx.x / row_blocks;
+    const int row = (blockIdx.x - bh * row_blocks) * (256 / LPR) + threadIdx.x / LPR;
+    const Slice<D, true> sl(L, bh, S);
+    dor = sl.row(dout, kTDO, row);
+    orow = sl.row(out, kTO, row);
+    drow = (long long)bh * S + row;
+    valid = row < S;
+  } else {
+    drow = (long long)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
+    dor = dout + drow * D;
+    orow = out + drow * D;
+    valid = drow < rows;
+  }
   float acc = 0.f;
-  if (row < rows) {
+  if (valid) {
 #pragma unroll
     for (int c = part; c < D / 8; c += LPR) {
-      const u32x4 a = ld_g128u(dout + row * D + c * 8);
-      const u32x4 b = ld_g128u(out + row * D + c * 8);
+      const u32x4 a = ld_g128u(dor + c * 8);
+      const u32x4 b = ld_g128u(orow + c * 8);
 #pragma unroll
       for (int w = 0; w < 4; ++w)
         acc += bf16_lo(a[w]) * bf16_lo(b[w]) + bf16_hi(a[w]) * bf16_hi(b[w]);
@@ -60,7 +77,7 @@ __global__ __launch_bounds__(256) void delta_bf16_kernel(float* __restrict__ del
   acc += __shfl_xor(acc, 1, 64);
   acc += __shfl_xor(acc, 2, 64);
   acc += __shfl_xor(acc, 4, 64);
-  if (row < rows && part == 0) delta[row] = acc;
+  if (valid && part == 0) delta[drow] = acc;
 }
 
 // Stores lanes' f32x16 accumulators C[d][row] (lane = row l32, element r = d row
@@ -184,12 +201,12 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
   }
 }
 
-template <int D>
+template <int D, bool STRIDED>
 __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
     bf16* __restrict__ dk, bf16* __restrict__ dv, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, float c,
-    float lse_mul, float dk_mul) {
+    float lse_mul, float dk_mul, const AttnLayout L) {
   constexpr int KB = kKW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
   // Q and dO tiles, double-buffered (constant buffer indices in the unrolled loop; see the
@@ -205,9 +222,10 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
-  const size_t base = (size_t)bh * S * D;
-  const bf16* qg = q + base;
-  const bf16* dog = dout + base;
+  const Slice<D, STRIDED> sl(L, bh, S);
+  const bf16* qg = sl.base(q, kTQ);
+  const bf16* dog = sl.base(dout, kTDO);
+  const int qp = sl.pitch(kTQ), dop = sl.pitch(kTDO);  // row pitches of the streamed tiles
   const float* lseg = lse + (size_t)bh * S;
   const float* delg = delta + (size_t)bh * S;
 
@@ -221,9 +239,9 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) {
     const bool in = key < S;
-    kop[ds] = in ? ld_g128(k + base + (size_t)key * D + 16 * ds + 8 * hi)
+    kop[ds] = in ? ld_g128(sl.row(k, kTK, key) + 16 * ds + 8 * hi)
                  : as_bf16x8(u32x4{0, 0, 0, 0});
-    vop[ds] = in ? ld_g128(v + base + (size_t)key * D + 16 * ds + 8 * hi)
+    vop[ds] = in ? ld_g128(sl.row(v, kTV, key) + 16 * ds + 8 * hi)
                  : as_bf16x8(u32x4{0, 0, 0, 0});
   }
 
@@ -236,12 +254,13 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
 
   // Direct loads per wave per tile: its share of Q and dO, and its own lse and delta rows.
   using Dma = DmaTile<D, kWaves>;
-  uint32_t doff[Dma::PER_WAVE];
-  Dma::offsets(doff, wave, lane);
+  uint32_t qoff[Dma::PER_WAVE], dooff[Dma::PER_WAVE];
+  Dma::offsets(qoff, wave, lane, qp);
+  Dma::offsets(dooff, wave, lane, dop);
   float(*st)[2][kTileRows] = sst[wave];
   auto issue = [&](int t, bf16* nq, bf16* ndo, int buf) {
-    Dma::load_any(nq, qg, t * kTileRows, S, doff, wave, lane);
-    Dma::load_any(ndo, dog, t * kTileRows, S, doff, wave, lane);
+    Dma::load_any(nq, qg, t * kTileRows, S, qoff, wave, lane, qp);
+    Dma::load_any(ndo, dog, t * kTileRows, S, dooff, wave, lane, dop);
     dma_row64(st[buf][0], lseg, t * kTileRows, S, lane);
     dma_row64(st[buf][1], delg, t * kTileRows, S, lane);
   };
@@ -285,8 +304,8 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
   }
 
   if (key < S) {
-    store_rows_bf16<DB>(dk + base + (size_t)key * D, dkacc, dk_mul, hi);
-    store_rows_bf16<DB>(dv + base + (size_t)key * D, dvacc, 1.0f, hi);
+    store_rows_bf16<DB>(sl.row(dk, kTDK, key), dkacc, dk_mul, hi);
+    store_rows_bf16<DB>(sl.row(dv, kTDV, key), dvacc, 1.0f, hi);
   }
 }
 
@@ -335,11 +354,11 @@ __device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (
   }
 }
 
-template <int D>
+template <int D, bool STRIDED>
 __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
     bf16* __restrict__ dq, const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, const bf16* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ delta, int S, float scale_log2, float scale) {
+    const float* __restrict__ delta, int S, float scale_log2, float scale, const AttnLayout L) {
   constexpr int QB = kQW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
   // K and V tiles, double-buffered (constant buffer indices; see the forward kernel).
@@ -351,9 +370,10 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
-  const size_t base = (size_t)bh * S * D;
-  const bf16* kg = k + base;
-  const bf16* vg = v + base;
+  const Slice<D, STRIDED> sl(L, bh, S);
+  const bf16* kg = sl.base(k, kTK);
+  const bf16* vg = sl.base(v, kTV);
+  const int kp = sl.pitch(kTK), vp = sl.pitch(kTV);  // row pitches of the streamed tiles
 
   const int q0 = qblk * QB + wave * kQW;
   const int qrow = q0 + l32;
@@ -364,9 +384,9 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) {
     const bool in = qrow < S;
-    qop[ds] = in ? ld_g128(q + base + (size_t)qrow * D + 16 * ds + 8 * hi)
+    qop[ds] = in ? ld_g128(sl.row(q, kTQ, qrow) + 16 * ds + 8 * hi)
                  : as_bf16x8(u32x4{0, 0, 0, 0});
-    doop[ds] = in ? ld_g128(dout + base + (size_t)qrow * D + 16 * ds + 8 * hi)
+    doop[ds] = in ? ld_g128(sl.row(dout, kTDO, qrow) + 16 * ds + 8 * hi)
                   : as_bf16x8(u32x4{0, 0, 0, 0});
   }
   // (rows past S read row S-1: finite values for rows that are never stored)
@@ -381,10 +401,11 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
   // every valid query), so they are masked. The first tile loads alongside the operands
   // above, under one wait (see the dK/dV kernel).
   using Dma = DmaTile<D, kWaves>;
-  uint32_t doff[Dma::PER_WAVE];
-  Dma::offsets(doff, wave, lane);
-  Dma::load_any(sk[0], kg, 0, S, doff, wave, lane);
-  Dma::load_any(sv[0], vg, 0, S, doff, wave, lane);
+  uint32_t koff[Dma::PER_WAVE], voff[Dma::PER_WAVE];
+  Dma::offsets(koff, wave, lane, kp);
+  Dma::offsets(voff, wave, lane, vp);
+  Dma::load_any(sk[0], kg, 0, S, koff, wave, lane, kp);
+  Dma::load_any(sv[0], vg, 0, S, voff, wave, lane, vp);
   wait_vm_lds<0>();
   __builtin_amdgcn_s_barrier();
   // Use the two statistics only from here on, so their load shares the wait above.
@@ -394,8 +415,8 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
   auto tile = [&](int t, const bf16* ck, const bf16* cv, bf16* nk, bf16* nv) {
     const int k0 = t * kTileRows;
     if (t + 1 < n_tiles) {
-      Dma::load_any(nk, kg, k0 + kTileRows, S, doff, wave, lane);
-      Dma::load_any(nv, vg, k0 + kTileRows, S, doff, wave, lane);
+      Dma::load_any(nk, kg, k0 + kTileRows, S, koff, wave, lane, kp);
+      Dma::load_any(nv, vg, k0 + kTileRows, S, voff, wave, lane, vp);
     }
     if (q0 < S) {
 #pragma unroll
@@ -418,28 +439,38 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
     if (t + 1 < n_tiles) tile(t + 1, sk[1], sv[1], sk[0], sv[0]);
   }
 
-  if (qrow < S) store_rows_bf16<DB>(dq + base + (size_t)qrow * D, dqacc, scale, hi);
+  if (qrow < S) store_rows_bf16<DB>(sl.row(dq, kTDQ, qrow), dqacc, scale, hi);
 }
 
 template <int D>
 hipError_t launch_bwd_bf16_t(bf16* dq, bf16* dk, bf16* dv, float* delta, const bf16* dout,
                              const bf16* out, const float* lse, const bf16* q, const bf16* k,
-                             const bf16* v, int BH, int S, float scale, hipStream_t stream,
-                             int phases) {
+                             const bf16* v, int BH, int S, float scale, const AttnLayout& L,
+                             hipStream_t stream, int phases) {
   hipError_t e = hipSuccess;
+  const bool contiguous = is_contiguous(L, S, D);
   if (phases & kBwdDelta) {
-    const long rows = (long)BH * S;
-    const long threads = rows * 8;
-    delta_bf16_kernel<D><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(delta, dout,
-                                                                               out, rows);
+    const long long rows = (long long)BH * S;
+    const int row_blocks = (S + 31) / 32;
+    if (contiguous)
+      delta_bf16_kernel<D, false><<<(unsigned)((rows + 31) / 32), 256, 0, stream>>>(
+          delta, dout, out, S, rows, row_blocks, L);
+    else
+      delta_bf16_kernel<D, true><<<(unsigned)BH * row_blocks, 256, 0, stream>>>(
+          delta, dout, out, S, rows, row_blocks, L);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   // P = exp2(S * scale * log2(e) - lse * log2(e)) holds for either sign of the scale.
   const float sl2 = scale * kLog2e;
   if (phases & kBwdDq) {
     constexpr int QB = kQW * kWaves;
-    dq_bf16_kernel<D><<<dim3(BH, (S + QB - 1) / QB), 64 * kWaves, 0, stream>>>(
-        dq, q, k, v, dout, lse, delta, S, sl2, scale);
+    const dim3 grid(BH, (S + QB - 1) / QB);
+    if (contiguous)
+      dq_bf16_kernel<D, false><<<grid, 64 * kWaves, 0, stream>>>(dq, q, k, v, dout, lse, delta,
+                                                                  S, sl2, scale, L);
+    else
+      dq_bf16_kernel<D, true><<<grid, 64 * kWaves, 0, stream>>>(dq, q, k, v, dout, lse, delta,
+                                                                 S, sl2, scale, L);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (phases & kBwdDkdv) {
@@ -447,8 +478,13 @@ hipError_t launch_bwd_bf16_t(bf16* dq, bf16* dk, bf16* dv, float* delta, const b
     // s = S - lse/scale needs a nonzero scale: a zero one (P = exp(-lse)) runs with 1e-30,
     // whose S*scale terms are then below fp32 resolution next to lse/scale.
     const float se = scale != 0.f ? scale : 1e-30f;
-    dkdv_bf16_kernel<D><<<dim3(BH, (S + KB - 1) / KB), 64 * kWaves, 0, stream>>>(
-        dk, dv, q, k, v, dout, lse, delta, S, se * kLog2e, -1.0f / se, scale);
+    const dim3 grid(BH, (S + KB - 1) / KB);
+    if (contiguous)
+      dkdv_bf16_kernel<D, false><<<grid, 64 * kWaves, 0, stream>>>(
+          dk, dv, q, k, v, dout, lse, delta, S, se * kLog2e, -1.0f / se, scale, L);
+    else
+      dkdv_bf16_kernel<D, true><<<grid, 64 * kWaves, 0, stream>>>(
+          dk, dv, q, k, v, dout, lse, delta, S, se * kLog2e, -1.0f / se, scale, L);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return e;
@@ -459,13 +495,13 @@ hipError_t launch_bwd_bf16_t(bf16* dq, bf16* dk, bf16* dv, float* delta, const b
 hipError_t launch_bwd_bf16(bf16* dq, bf16* dk, bf16* dv, float* delta, const bf16* dout,
                            const bf16* out, const float* lse, const bf16* q, const bf16* k,
                            const bf16* v, int BH, int S, int D, float scale,
-                           hipStream_t stream, int phases) {
+                           const AttnLayout& layout, hipStream_t stream, int phases) {
   if (D == 64)
     return launch_bwd_bf16_t<64>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale,
-                                 stream, phases);
+                                 layout, stream, phases);
   if (D == 32)
     return launch_bwd_bf16_t<32>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale,
-                                 stream, phases);
+                                 layout, stream, phases);
   return hipErrorInvalidValue;
 }
 

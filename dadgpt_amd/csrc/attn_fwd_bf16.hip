@@ -188,12 +188,12 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[
       for (int i = 0; i < NQB; ++i) oacc[i][db] = mfma32(va[db][j], pb[i][j], oacc[i][db]);
 }
 
-template <int D>
+template <int D, bool STRIDED>
 __global__ __launch_bounds__(64 * kWaves, kMinBlocks)
 __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_kernel(
     bf16* __restrict__ out, float* __restrict__ lse, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, int S, float scale_log2,
-    int negate_q) {
+    int negate_q, const AttnLayout L) {
   // scale_log2 = |scale| * log2(e); a negative scale is applied by negating Q (exact in bf16),
   // so the row max of the raw scores is the row max of the scaled ones.
   constexpr int QB = kQW * kWaves;
@@ -211,10 +211,11 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
   const int l32 = lane & 31, hi = lane >> 5;
-  const size_t base = (size_t)bh * S * D;
-  const bf16* qg = q + base;
-  const bf16* kg = k + base;
-  const bf16* vg = v + base;
+  const Slice<D, STRIDED> sl(L, bh, S);
+  const bf16* qg = sl.base(q, kTQ);
+  const bf16* kg = sl.base(k, kTK);
+  const bf16* vg = sl.base(v, kTV);
+  const int qp = sl.pitch(kTQ), kp = sl.pitch(kTK), vp = sl.pitch(kTV);  // row pitches
 
   const int q0 = qblk * QB + wave * kQW;
   const int wg_last = min(S, (qblk + 1) * QB) - 1;
@@ -227,7 +228,7 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
   for (int i = 0; i < kNQB; ++i) {
     const int row = min(q0 + 32 * i + l32, S - 1);
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) qop[i][ds] = ld_g128(qg + (size_t)row * D + 16 * ds + 8 * hi);
+    for (int ds = 0; ds < DS; ++ds) qop[i][ds] = ld_g128(qg + (size_t)row * qp + 16 * ds + 8 * hi);
   }
 
   f32x16 oacc[kNQB][DB];
@@ -245,10 +246,11 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
   // The first tile loads alongside Q, under one wait; Q is touched only after it (the
   // compiler, which does not see the direct loads, then has nothing left to wait for).
   using Dma = DmaTile<D, kWaves>;
-  uint32_t doff[Dma::PER_WAVE];
-  Dma::offsets(doff, wave, lane);
-  Dma::load_any(sk[0], kg, 0, S, doff, wave, lane);
-  Dma::load_any(sv[0], vg, 0, S, doff, wave, lane);
+  uint32_t koff[Dma::PER_WAVE], voff[Dma::PER_WAVE];
+  Dma::offsets(koff, wave, lane, kp);
+  Dma::offsets(voff, wave, lane, vp);
+  Dma::load_any(sk[0], kg, 0, S, koff, wave, lane, kp);
+  Dma::load_any(sv[0], vg, 0, S, voff, wave, lane, vp);
   wait_vm_lds<0>();
   __builtin_amdgcn_s_barrier();
 #pragma unroll
@@ -266,8 +268,8 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
     const int k0 = t * kTileRows;
     const bool prefetch = t + 1 < n_tiles;
     if (prefetch) {
-      Dma::load_any(nk, kg, k0 + kTileRows, S, doff, wave, lane);
-      Dma::load_any(nv, vg, k0 + kTileRows, S, doff, wave, lane);
+      Dma::load_any(nk, kg, k0 + kTileRows, S, koff, wave, lane, kp);
+      Dma::load_any(nv, vg, k0 + kTileRows, S, voff, wave, lane, vp);
     }
     if (q0 < S && k0 <= q0 + kQW - 1) {  // some key of the tile at or before a query
       // One 32-key chunk at a time (holding both chunks' scores at once measured no faster
@@ -305,7 +307,7 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
     const float l = sum_halves(lrun[i]);
     const float inv = 1.0f / l;
     if (qrow < S) {
-      bf16* orow = out + base + (size_t)qrow * D;
+      bf16* orow = sl.row(out, kTO, qrow);
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -323,23 +325,30 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
 
 template <int D>
 hipError_t launch_fwd_bf16_t(bf16* out, float* lse, const bf16* q, const bf16* k, const bf16* v,
-                             int BH, int S, float scale, hipStream_t stream) {
+                             int BH, int S, float scale, const AttnLayout& L,
+                             hipStream_t stream) {
   constexpr int QB = kQW * kWaves;
   dim3 grid(BH, (S + QB - 1) / QB);
   // Masked scores are -inf and exponentiate as exp2(-inf * c - m), so c must be positive: a
   // zero scale (uniform attention) runs with c = 1e-30: every score below 1e22 in magnitude
   // then has |s*c - m| < 2^-25, an fp32 weight of exactly 1.
   const float c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);
-  fwd_bf16_kernel<D><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c, scale < 0.f);
+  if (is_contiguous(L, S, D))
+    fwd_bf16_kernel<D, false><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c,
+                                                                scale < 0.f, L);
+  else
+    fwd_bf16_kernel<D, true><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c,
+                                                               scale < 0.f, L);
   return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_fwd_bf16(bf16* out, float* lse, const bf16* q, const bf16* k, const bf16* v,
-                           int BH, int S, int D, float scale, hipStream_t stream) {
-  if (D == 64) return launch_fwd_bf16_t<64>(out, lse, q, k, v, BH, S, scale, stream);
-  if (D == 32) return launch_fwd_bf16_t<32>(out, lse, q, k, v, BH, S, scale, stream);
+                           int BH, int S, int D, float scale, const AttnLayout& layout,
+                           hipStream_t stream) {
+  if (D == 64) return launch_fwd_bf16_t<64>(out, lse, q, k, v, BH, S, scale, layout, stream);
+  if (D == 32) return launch_fwd_bf16_t<32>(out, lse, q, k, v, BH, S, scale, layout, stream);
   return hipErrorInvalidValue;
 }
 

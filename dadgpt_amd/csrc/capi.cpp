@@ -60,6 +60,10 @@ int check_attn(const char* fn, int BH, int S, int d_head, float scale,
   if (BH < 1 || S < 1)
     return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: BH=%d and S=%d must be positive", fn, BH, S);
   if (S > kMaxRows) return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: S=%d too large", fn, S);
+  // grids: BH workgroups of 256 lanes along x, 8 lanes per row in the delta kernel (the
+  // dispatch packet counts work-items in 32 bits)
+  if (BH > kMaxRows || (long long)BH * S > (1LL << 29))
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: BH=%d x S=%d too large", fn, BH, S);
   if (!supported(d_head))
     return fail(DADGPT_ERR_UNSUPPORTED, "flash attention: unsupported d_head %d", d_head);
   if (!std::isfinite(scale))
@@ -87,6 +91,49 @@ int check_decode(const char* fn, int n_seq, int H, int max_len, int d_head, floa
 }
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Strides of the strided/token-major calls: non-negative multiples of 8 elements (the kernels
+// move 16-byte pieces), rows at least d_head apart and at most 2^24 (64 rows of a tile stay
+// within a 32-bit byte offset). Converts them to the kernels' layout.
+int check_strides(const char* fn, int B, int H, int S, int d_head,
+                  const dadgpt_head_strides* strides, int count, dadgpt::AttnLayout* L) {
+  static const char* names[] = {"q", "k", "v", "out", "dout", "dq", "dk", "dv"};
+  if (strides == nullptr)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: strides is null", fn);
+  if (B < 1 || H < 1)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: B=%d and H=%d must be positive", fn, B, H);
+  if ((long long)B * H > kMaxRows)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: B=%d x H=%d too large", fn, B, H);
+  *L = dadgpt::contiguous_layout(S, d_head);
+  L->n_heads = H;
+  for (int i = 0; i < count; ++i) {
+    const dadgpt_head_strides& t = strides[i];
+    if (t.batch < 0 || t.head < 0 || t.row < d_head || t.row > kMaxRows || t.batch % 8 != 0 ||
+        t.head % 8 != 0 || t.row % 8 != 0)
+      return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                  "%s: strides of %s {batch %lld, head %lld, row %lld}: each must be a "
+                  "non-negative multiple of 8, with d_head (%d) <= row <= 2^24",
+                  fn, names[i], (long long)t.batch, (long long)t.head, (long long)t.row,
+                  d_head);
+    L->t[i] = dadgpt::HeadStrides{t.batch, t.head, (int)t.row};
+  }
+  return DADGPT_OK;
+}
+
+// Token-major rows hold all H heads side by side: every leading dimension is at least H*d_head.
+int check_ld(const char* fn, int H, int d_head, std::initializer_list<int64_t> lds) {
+  for (int64_t ld : lds)
+    if (ld < (int64_t)H * d_head || ld > kMaxRows)
+      return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                  "%s: leading dimension %lld outside [n_heads x d_head = %lld, 2^24]", fn,
+                  (long long)ld, (long long)H * d_head);
+  return DADGPT_OK;
+}
+
+// Token-major strides: row b*S + s holds the H heads side by side, rows ld elements apart.
+dadgpt_head_strides tokens(int64_t ld, int S, int d_head) {
+  return dadgpt_head_strides{ld * S, d_head, ld};
+}
 
 using dadgpt::bf16;
 const bf16* B(const uint16_t* p) { return reinterpret_cast<const bf16*>(p); }
@@ -155,6 +202,7 @@ int dadgpt_flash_attention_forward_bf16(uint16_t* out, float* lse, const uint16_
   const char* fn = "dadgpt_flash_attention_forward_bf16";
   if (int st = check_attn(fn, BH, S, d_head, scale, {out, lse, q, k, v})) return st;
   return from_hip(dadgpt::launch_fwd_bf16(B(out), lse, B(q), B(k), B(v), BH, S, d_head, scale,
+                                          dadgpt::contiguous_layout(S, d_head),
                                           as_stream(stream)),
                   fn);
 }
@@ -170,6 +218,7 @@ int dadgpt_flash_attention_backward_bf16(uint16_t* dq, uint16_t* dk, uint16_t* d
     return st;
   return from_hip(dadgpt::launch_bwd_bf16(B(dq), B(dk), B(dv), delta, B(dout), B(out), lse,
                                           B(q), B(k), B(v), BH, S, d_head, scale,
+                                          dadgpt::contiguous_layout(S, d_head),
                                           as_stream(stream)),
                   fn);
 }
@@ -187,8 +236,73 @@ int dadgpt_flash_attention_backward_bf16_phase(int phase, uint16_t* dq, uint16_t
     return st;
   return from_hip(dadgpt::launch_bwd_bf16(B(dq), B(dk), B(dv), delta, B(dout), B(out), lse,
                                           B(q), B(k), B(v), BH, S, d_head, scale,
+                                          dadgpt::contiguous_layout(S, d_head),
                                           as_stream(stream), 1 << phase),
                   fn);
+}
+
+int dadgpt_flash_attention_forward_bf16_strided(uint16_t* out, float* lse, const uint16_t* q,
+                                                const uint16_t* k, const uint16_t* v, int batch,
+                                                int H, int S, int d_head, float scale,
+                                                const dadgpt_head_strides* strides,
+                                                void* stream) {
+  const char* fn = "dadgpt_flash_attention_forward_bf16_strided";
+  dadgpt::AttnLayout L;
+  if (int st = check_strides(fn, batch, H, S, d_head, strides, 4, &L)) return st;
+  if (int st = check_attn(fn, batch * H, S, d_head, scale, {out, lse, q, k, v})) return st;
+  return from_hip(dadgpt::launch_fwd_bf16(B(out), lse, B(q), B(k), B(v), batch * H, S, d_head,
+                                          scale, L, as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_flash_attention_backward_bf16_strided(uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                                                 float* delta, const uint16_t* dout,
+                                                 const uint16_t* out, const float* lse,
+                                                 const uint16_t* q, const uint16_t* k,
+                                                 const uint16_t* v, int batch, int H, int S,
+                                                 int d_head, float scale,
+                                                 const dadgpt_head_strides* strides,
+                                                 void* stream) {
+  const char* fn = "dadgpt_flash_attention_backward_bf16_strided";
+  dadgpt::AttnLayout L;
+  if (int st = check_strides(fn, batch, H, S, d_head, strides, 8, &L)) return st;
+  if (int st = check_attn(fn, batch * H, S, d_head, scale,
+                          {dq, dk, dv, delta, dout, out, lse, q, k, v}))
+    return st;
+  return from_hip(dadgpt::launch_bwd_bf16(B(dq), B(dk), B(dv), delta, B(dout), B(out), lse,
+                                          B(q), B(k), B(v), batch * H, S, d_head, scale, L,
+                                          as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_flash_attention_forward_bf16_tokens(uint16_t* out, int64_t ld_out, float* lse,
+                                               const uint16_t* q, const uint16_t* k,
+                                               const uint16_t* v, int64_t ld_qkv, int batch,
+                                               int H, int S, int d_head, float scale,
+                                               void* stream) {
+  const char* fn = "dadgpt_flash_attention_forward_bf16_tokens";
+  if (int st = check_ld(fn, H, d_head, {ld_qkv, ld_out})) return st;
+  const dadgpt_head_strides in = tokens(ld_qkv, S, d_head), o = tokens(ld_out, S, d_head);
+  const dadgpt_head_strides st[4] = {in, in, in, o};
+  return dadgpt_flash_attention_forward_bf16_strided(out, lse, q, k, v, batch, H, S, d_head,
+                                                     scale, st, stream);
+}
+
+int dadgpt_flash_attention_backward_bf16_tokens(uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                                                int64_t ld_dqkv, float* delta,
+                                                const uint16_t* dout, const uint16_t* out,
+                                                int64_t ld_out, const float* lse,
+                                                const uint16_t* q, const uint16_t* k,
+                                                const uint16_t* v, int64_t ld_qkv, int batch,
+                                                int H, int S, int d_head, float scale,
+                                                void* stream) {
+  const char* fn = "dadgpt_flash_attention_backward_bf16_tokens";
+  if (int st = check_ld(fn, H, d_head, {ld_qkv, ld_out, ld_dqkv})) return st;
+  const dadgpt_head_strides in = tokens(ld_qkv, S, d_head), o = tokens(ld_out, S, d_head),
+                            g = tokens(ld_dqkv, S, d_head);
+  const dadgpt_head_strides st[8] = {in, in, in, o, o, g, g, g};
+  return dadgpt_flash_attention_backward_bf16_strided(dq, dk, dv, delta, dout, out, lse, q, k, v,
+                                                      batch, H, S, d_head, scale, st, stream);
 }
 
 size_t dadgpt_decode_workspace_bytes(int n_seq, int n_heads, int max_len, int d_head) {

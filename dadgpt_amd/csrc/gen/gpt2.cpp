@@ -164,15 +164,23 @@ struct dadgpt_gpt2 {
 
 namespace {
 
-int attention_prefill(dadgpt_gpt2* m, int n, int S, float scale) {
-  const int BH = n * m->c.n_heads;
+// Prefill attention over n padded prompts of S rows. fp32: split heads [n*H, S, dh] in
+// m->qh/kh/vh -> m->ao (merged afterwards). bf16: Q heads from m->qh, K and V read in place
+// from the layer's cache (rows 0..S-1 of [max_batch, H, ctx, dh]), and the output written
+// token-major into m->a, the Wo GEMM's input: no split K/V copies and no merge pass.
+int attention_prefill(dadgpt_gpt2* m, int layer, int n, int S, float scale) {
+  const int H = m->c.n_heads, dh = m->dh;
   if (m->fp32)
     return dadgpt_flash_attention_forward_async((float*)m->ao, m->lse, (const float*)m->qh,
-                                                (const float*)m->kh, (const float*)m->vh, BH, S,
-                                                m->dh, scale, m->stream);
-  return dadgpt_flash_attention_forward_bf16((uint16_t*)m->ao, m->lse, (const uint16_t*)m->qh,
-                                             (const uint16_t*)m->kh, (const uint16_t*)m->vh, BH,
-                                             S, m->dh, scale, m->stream);
+                                                (const float*)m->kh, (const float*)m->vh, n * H,
+                                                S, dh, scale, m->stream);
+  const int64_t ctx = m->c.ctx_len, d = (int64_t)H * dh;
+  const dadgpt_head_strides heads{d * S, (int64_t)S * dh, dh}, cache{d * ctx, ctx * dh, dh},
+      tokens{d * S, dh, d};
+  const dadgpt_head_strides st[4] = {heads, cache, cache, tokens};
+  return dadgpt_flash_attention_forward_bf16_strided(
+      (uint16_t*)m->a, m->lse, (const uint16_t*)m->qh, (const uint16_t*)m->kc[layer],
+      (const uint16_t*)m->vc[layer], n, H, S, dh, scale, st, m->stream);
 }
 
 int attention_decode(dadgpt_gpt2* m, int layer, int n, float scale) {
@@ -218,16 +226,15 @@ int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev
                                (float*)m->vc[l], m->qkv, m->bqkv[l], m->pos0, m->nvalid, n, S, H,
                                dh, c.ctx_len, s),
               "qkv_split");
-    else
-      TRY_HIP(qkv_split<bf16>((bf16*)m->qh, (bf16*)m->kh, (bf16*)m->vh, (bf16*)m->kc[l],
-                              (bf16*)m->vc[l], m->qkv, m->bqkv[l], m->pos0, m->nvalid, n, S, H,
-                              dh, c.ctx_len, s),
+    else  // Q heads and the cache append only
+      TRY_HIP(qkv_split<bf16>((bf16*)m->qh, nullptr, nullptr, (bf16*)m->kc[l], (bf16*)m->vc[l],
+                              m->qkv, m->bqkv[l], m->pos0, m->nvalid, n, S, H, dh, c.ctx_len,
+                              s),
               "qkv_split");
-    if (int st = attention_prefill(m, n, S, scale)) return attn_fail(st, "prefill attention");
+    if (int st = attention_prefill(m, l, n, S, scale))
+      return attn_fail(st, "prefill attention");
     if (m->fp32)
       TRY_HIP(merge_heads<float>(m->a, (const float*)m->ao, n, S, H, dh, s), "merge_heads");
-    else
-      TRY_HIP(merge_heads<bf16>(m->a, (const bf16*)m->ao, n, S, H, dh, s), "merge_heads");
   } else {
     if (m->fp32)
       TRY_HIP(qkv_split<float>((float*)m->qh, nullptr, nullptr, (float*)m->kc[l],
@@ -525,6 +532,11 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       return bail(st);
     if (int st = m->alloc(&m->kc[l], cache, "k cache")) return bail(st);
     if (int st = m->alloc(&m->vc[l], cache, "v cache")) return bail(st);
+    // zero rows past a prompt: the bf16 prefill reads K and V from the cache, and padded
+    // queries (discarded) see rows no prompt wrote
+    if (hipMemsetAsync(m->kc[l], 0, cache, m->stream) != hipSuccess ||
+        hipMemsetAsync(m->vc[l], 0, cache, m->stream) != hipSuccess)
+      return bail(fail(DADGPT_ERR_HIP, "dadgpt_gpt2_create: cache clear failed"));
   }
   const size_t ab = m->esz;
   int st = DADGPT_OK;
@@ -538,8 +550,9 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       (st = m->alloc_n(&m->h, rows * d, "ln out")) || (st = m->alloc_n(&m->a, rows * d, "attn in")) ||
       (st = m->alloc_n(&m->g, rows * c.d_ff, "gelu out")) ||
       (st = m->alloc(&m->qh, rows * d * ab, "q heads")) ||
-      (st = m->alloc(&m->kh, rows * d * ab, "k heads")) ||
-      (st = m->alloc(&m->vh, rows * d * ab, "v heads")) ||
+      // split K and V heads: fp32 attention only (bf16 reads them from the cache)
+      (m->fp32 && (st = m->alloc(&m->kh, rows * d * ab, "k heads"))) ||
+      (m->fp32 && (st = m->alloc(&m->vh, rows * d * ab, "v heads"))) ||
       (st = m->alloc(&m->ao, rows * d * ab, "attn out")) ||
       (st = m->alloc_n(&m->tok_in, rows, "tokens")) ||
       (st = m->alloc_n(&m->pos0, max_batch, "pos0")) ||

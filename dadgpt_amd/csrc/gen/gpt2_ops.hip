@@ -314,7 +314,6 @@ hipError_t merge_heads(bf16* out, const T* heads, int n, int S, int H, int dh, h
   merge_heads_kernel<T><<<n * S, 256, 0, s>>>(out, heads, S, H, dh);
   return hipGetLastError();
 }
-template hipError_t merge_heads<bf16>(bf16*, const bf16*, int, int, int, int, hipStream_t);
 template hipError_t merge_heads<float>(bf16*, const float*, int, int, int, int, hipStream_t);
 
 hipError_t to_bf16(bf16* out, const float* in, size_t count, hipStream_t s) {

@@ -11,9 +11,46 @@ namespace dadgpt {
 
 typedef __bf16 bf16;
 
-// Causal flash forward, bf16 in/out, fp32 logsumexp (natural log). [BH,S,D], D in {32,64}.
+// Where the rows of one (b, h) slice of a bf16 attention tensor lie: row s of slice
+// bh = b * n_heads + h starts at element b * batch + h * head + s * row, and its D elements
+// are contiguous. A contiguous [BH, S, D] tensor is {S * D, 0, D} with n_heads = 1; the
+// token-major [B * S, H * D] layout of the projections is {S * H * D, D, H * D}. The host
+// keeps every stride a multiple of 8 elements (16 bytes) and row below 2^24.
+struct HeadStrides {
+  long long batch, head;
+  int row;
+};
+enum AttnTensor { kTQ, kTK, kTV, kTO, kTDO, kTDQ, kTDK, kTDV, kAttnTensors };
+struct AttnLayout {
+  int n_heads;
+  HeadStrides t[kAttnTensors];
+};
+
+inline AttnLayout contiguous_layout(int S, int D) {
+  AttnLayout L{};
+  L.n_heads = 1;
+  for (auto& t : L.t) t = HeadStrides{(long long)S * D, 0, D};
+  return L;
+}
+
+// Whether `L` places every tensor as contiguous [BH, S, D] (the kernels then use their
+// compile-time contiguous addressing). Unit-stride heads count: b * H * S * D + h * S * D is
+// the same element as bh * S * D.
+inline bool is_contiguous(const AttnLayout& L, int S, int D) {
+  const long long slice = (long long)S * D;
+  for (const auto& t : L.t)
+    if (t.row != D || t.head != slice || t.batch != slice * L.n_heads) {
+      if (L.n_heads == 1 && t.row == D && t.batch == slice) continue;  // head unused
+      return false;
+    }
+  return true;
+}
+
+// Causal flash forward, bf16 in/out, fp32 logsumexp (natural log) [BH, S]. q, k, v, out as
+// `layout` places them (tensors kTQ, kTK, kTV, kTO), D in {32,64}.
 hipError_t launch_fwd_bf16(bf16* out, float* lse, const bf16* q, const bf16* k, const bf16* v,
-                           int BH, int S, int D, float scale, hipStream_t stream);
+                           int BH, int S, int D, float scale, const AttnLayout& layout,
+                           hipStream_t stream);
 
 // Causal flash backward, bf16 in/out. delta [BH,S] fp32 is written (scratch, as the
 // reference's). dq/dk/dv are overwritten. `phases` selects the kernels launched, in order:
@@ -21,8 +58,8 @@ hipError_t launch_fwd_bf16(bf16* out, float* lse, const bf16* q, const bf16* k, 
 constexpr int kBwdDelta = 1, kBwdDq = 2, kBwdDkdv = 4, kBwdAll = 7;
 hipError_t launch_bwd_bf16(bf16* dq, bf16* dk, bf16* dv, float* delta, const bf16* dout,
                            const bf16* out, const float* lse, const bf16* q, const bf16* k,
-                           const bf16* v, int BH, int S, int D, float scale, hipStream_t stream,
-                           int phases = kBwdAll);
+                           const bf16* v, int BH, int S, int D, float scale,
+                           const AttnLayout& layout, hipStream_t stream, int phases = kBwdAll);
 
 // fp32 flash forward/backward (the reference's own precision).
 hipError_t launch_fwd_f32(float* out, float* lse, const float* q, const float* k,

@@ -1,5 +1,5 @@
-// Global -> register -> LDS staging of 64-row tiles of a [S, D] bf16 matrix, and the two ways
-// the MFMA kernels read them back:
+// Direct global -> LDS staging of 64-row tiles of an [S, D] bf16 matrix (rows at any pitch),
+// and the two ways the MFMA kernels read them back:
 //   row operands        one ds_read_b128: 8 consecutive columns of one row (along D)
 //   transposed operands two ds_read_b64_tr_b16: 8 consecutive rows of one column (along the
 //                       64 tile rows), so the tile never has to be stored transposed
@@ -11,10 +11,37 @@
 #pragma once
 
 #include "common.hpp"
+#include "kernels.hpp"
 
 namespace dadgpt {
 
 constexpr int kTileRows = 64;
+
+// Where tensor t's rows of slice bh lie. STRIDED = false is the contiguous [BH, S, D] layout
+// with every offset a compile-time multiple of D; STRIDED = true reads the layout (kernels.hpp).
+template <int D, bool STRIDED>
+struct Slice {
+  const AttnLayout& L;
+  int bh, S, b, h;
+  __device__ __forceinline__ Slice(const AttnLayout& layout, int bh_, int S_)
+      : L(layout), bh(bh_), S(S_), b(STRIDED ? bh_ / layout.n_heads : bh_),
+        h(STRIDED ? bh_ - b * layout.n_heads : 0) {}
+  // row pitch (elements) of tensor t
+  __device__ __forceinline__ int pitch(int t) const { return STRIDED ? L.t[t].row : D; }
+  // first element of tensor t's slice
+  template <typename T>
+  __device__ __forceinline__ T* base(T* p, int t) const {
+    if constexpr (STRIDED)
+      return p + (b * L.t[t].batch + h * L.t[t].head);
+    else
+      return p + (size_t)bh * S * D;
+  }
+  // element `row` of tensor t's slice
+  template <typename T>
+  __device__ __forceinline__ T* row(T* p, int t, int r) const {
+    return base(p, t) + (size_t)r * pitch(t);
+  }
+};
 
 __device__ __forceinline__ constexpr int parity(int x) { return __builtin_popcount(x) & 1; }
 
@@ -64,44 +91,6 @@ __device__ __forceinline__ bf16x8 lds_tr_op(const bf16* tile, int row0, int col0
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// A 64-row tile staged as 16-byte chunks: unit u -> row u / (D/8), chunk u % (D/8).
-// Consecutive threads read consecutive 16-byte pieces of a row (fully used 64-byte segments).
-// With more threads than units (D=32 and 512 threads) the surplus threads stage nothing.
-template <int D, int NT>
-struct RowTile {
-  static constexpr int C = D / 8;
-  static constexpr int UNITS = kTileRows * C;
-  static constexpr int PER = UNITS >= NT ? UNITS / NT : 1;
-  static_assert(UNITS % NT == 0 || NT % UNITS == 0, "units divide evenly over threads");
-  u32x4 a[PER];
-
-  __device__ __forceinline__ static bool active(int tid) { return UNITS >= NT || tid < UNITS; }
-
-  __device__ __forceinline__ void load(const bf16* g, int row0, int S, int tid) {
-    if (!active(tid)) return;
-    const bf16* p = g + (size_t)row0 * D + (tid / C) * D + (tid % C) * 8;
-    if (row0 + kTileRows <= S) {  // whole tile in bounds (uniform branch)
-#pragma unroll
-      for (int i = 0; i < PER; ++i) a[i] = ld_g128u(p + (size_t)i * (NT / C) * D);
-    } else {
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int row = (tid + i * NT) / C;
-        a[i] = u32x4{0, 0, 0, 0};
-        if (row0 + row < S) a[i] = ld_g128u(p + (size_t)i * (NT / C) * D);
-      }
-    }
-  }
-  __device__ __forceinline__ void store(bf16* lds, int tid) const {
-    if (!active(tid)) return;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = tid + i * NT;
-      *reinterpret_cast<u32x4*>(lds + rm_off<D>(u / C, u % C)) = a[i];
-    }
-  }
-};
-
 // Direct global -> LDS staging (global_load_lds_dwordx4): lane i of a wave-instruction writes
 // its 16 bytes to LDS at (M0 + 16*i), so the swizzle is applied on the global side: the lane
 // that fills LDS slot (row, physical chunk c) reads logical chunk c ^ swz(row). No registers
@@ -122,23 +111,9 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(uintptr_t)p;
 }
 
-__device__ __forceinline__ void dma_lds(const void* gsrc, const void* lds_dst, int bytes) {
-  const uint32_t lds = lds_offset(lds_dst);
-  const uint32_t base = __builtin_amdgcn_readfirstlane(lds);  // wave-uniform destination
-  if (bytes == 16)
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :
-                 : "s"(base), "v"(gsrc)
-                 : "memory");
-  else
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
-                 :
-                 : "s"(base), "v"(gsrc)
-                 : "memory");
-}
-
-// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset
-// (the instruction's saddr form): a tile loop moves only the scalar base.
+// One 16-byte (or 4-byte) piece per lane: a wave-uniform 64-bit base in SGPRs plus a 32-bit
+// per-lane byte offset (the instruction's saddr form), so a tile loop moves only the scalar
+// base.
 __device__ __forceinline__ void dma_lds16_sbase(const void* gbase, uint32_t voff,
                                                 const void* lds_dst) {
   const uint32_t lds = lds_offset(lds_dst);
@@ -178,45 +153,35 @@ struct DmaTile {
   static_assert(SLOTS % (64 * WAVES) == 0 || (64 * WAVES) % SLOTS == 0,
                 "whole wave-instructions per tile");
 
-  __device__ __forceinline__ static void load(bf16* lds_tile, const bf16* g, int row0, int S,
-                                              int wave, int lane) {
-    if (wave >= ACTIVE) return;
-#pragma unroll
-    for (int n = 0; n < PER_WAVE; ++n) {
-      const int slot0 = (wave * PER_WAVE + n) * 64;
-      const int slot = slot0 + lane;
-      const int row = slot / C;
-      const int chunk = (slot % C) ^ swz<D>(row);
-      const int grow = min(row0 + row, S - 1);
-      dma_lds(g + (size_t)grow * D + chunk * 8, lds_tile + slot0 * 8, 16);
-    }
-  }
-
   // Byte offset, from the tile's first row, of the global piece that fills this lane's slot
-  // of wave-instruction n (fixed for the whole kernel).
-  __device__ __forceinline__ static void offsets(uint32_t (&off)[PER_WAVE], int wave, int lane) {
+  // of wave-instruction n (fixed for the whole kernel). Rows are `pitch` elements apart in
+  // global memory (D for a contiguous [S, D] matrix; the caller keeps 64 * pitch * 2 bytes
+  // within 32 bits).
+  __device__ __forceinline__ static void offsets(uint32_t (&off)[PER_WAVE], int wave, int lane,
+                                                 int pitch) {
 #pragma unroll
     for (int n = 0; n < PER_WAVE; ++n) {
       const int slot = (wave * PER_WAVE + n) * 64 + lane;
       const int row = slot / C;
-      off[n] = (uint32_t)(row * D + ((slot % C) ^ swz<D>(row)) * 8) * 2u;
+      off[n] = (uint32_t)(row * pitch + ((slot % C) ^ swz<D>(row)) * 8) * 2u;
     }
   }
 
-  // Either form: a tile that crosses S moves the offsets of rows past S back to row S-1
+  // Tile rows row0 .. row0+63 of g (rows `pitch` elements apart, offsets from offsets() with
+  // the same pitch). A tile that crosses S moves the offsets of rows past S back to row S-1
   // (the slot's chunk swizzle is kept; it is the destination's).
   __device__ __forceinline__ static void load_any(bf16* lds_tile, const bf16* g, int row0, int S,
                                                   const uint32_t (&off)[PER_WAVE], int wave,
-                                                  int lane) {
+                                                  int lane, int pitch) {
     if (wave >= ACTIVE) return;
     const int rows_left = S - row0;  // wave-uniform
-    const bf16* base = g + (size_t)row0 * D;
+    const bf16* base = g + (size_t)row0 * pitch;
 #pragma unroll
     for (int n = 0; n < PER_WAVE; ++n) {
       uint32_t o = off[n];
       if (rows_left < kTileRows) {
         const int r = (wave * PER_WAVE + n) * (64 / C) + lane / C;
-        if (r >= rows_left) o -= (uint32_t)((r - rows_left + 1) * D * 2);
+        if (r >= rows_left) o -= (uint32_t)((r - rows_left + 1) * pitch * 2);
       }
       dma_lds16_sbase(base, o, lds_tile + (wave * PER_WAVE + n) * 64 * 8);
     }

@@ -10,9 +10,9 @@
  * Conventions (shared by every entry point):
  *  - All tensor pointers are device pointers owned by the caller, 16-byte aligned (checked);
  *    the library allocates nothing in these calls. Layout [BH, S, d_head] contiguous, heads
- *    already split
- *    (cuda/attention.cu:6); lse and delta are [BH, S] fp32; lse is the natural-log
- *    logsumexp of the scaled scores (cuda/attention.cu:71).
+ *    already split (cuda/attention.cu:6), except for the _strided and _tokens calls; lse
+ *    and delta are [BH, S] fp32; lse is the natural-log logsumexp of the scaled scores
+ *    (cuda/attention.cu:71).
  *  - bf16 tensors are passed as uint16_t* holding IEEE bfloat16 bit patterns.
  *  - Outputs are overwritten, never accumulated (cuda/gpu_ops.cuh:118).
  *  - Arguments are validated on the host before any HIP call; a failing call returns a
@@ -102,6 +102,69 @@ int dadgpt_flash_attention_backward_bf16_phase(int phase, uint16_t* dq, uint16_t
                                                const float* lse, const uint16_t* q,
                                                const uint16_t* k, const uint16_t* v, int BH,
                                                int S, int d_head, float scale, void* stream);
+
+/* ---- Attention over strided layouts (no reference counterpart). The reference splits the
+ * projections' token-major [B*S, H*d_head] rows into [B*H, S, d_head] before the fused kernel
+ * and merges the outputs and gradients back (gpu_split_heads / gpu_merge_heads,
+ * cuda/gpu_ops.cu:426-474, called at src/model.cpp:384-387,423-424 in the forward and
+ * :564-565,619-624 in the backward). These entry points read and write the tensors where they
+ * lie, so those six permutation passes disappear. Same arithmetic, lse/delta layout
+ * ([B*H, S] fp32, natural log) and overwrite semantics as the contiguous bf16 calls. */
+
+/* Placement of one bf16 tensor viewed as [B, H, S, d_head]: row s of head h of batch b
+ * starts at element b*batch + h*head + s*row of its pointer; the d_head elements of a row are
+ * contiguous. Every stride is in elements, non-negative and a multiple of 8 (16 bytes);
+ * row >= d_head and row <= 2^24. Contiguous [B*H, S, d_head] is {H*S*d_head, S*d_head,
+ * d_head}; token-major [B*S, H*d_head] is {S*H*d_head, d_head, H*d_head}. */
+typedef struct dadgpt_head_strides {
+  int64_t batch, head, row;
+} dadgpt_head_strides;
+
+/* Index of each tensor in the strides arrays below. */
+enum {
+  DADGPT_T_Q = 0, DADGPT_T_K, DADGPT_T_V, DADGPT_T_OUT, /* forward: strides[4] */
+  DADGPT_T_DOUT, DADGPT_T_DQ, DADGPT_T_DK, DADGPT_T_DV  /* backward: strides[8] */
+};
+
+/* Forward with q, k, v, out placed by strides[DADGPT_T_Q .. DADGPT_T_OUT]; lse [B*H, S].
+ * Outputs must not overlap each other or the inputs. */
+int dadgpt_flash_attention_forward_bf16_strided(uint16_t* out, float* lse, const uint16_t* q,
+                                                const uint16_t* k, const uint16_t* v, int B,
+                                                int H, int S, int d_head, float scale,
+                                                const dadgpt_head_strides* strides,
+                                                void* stream);
+
+/* Backward with every tensor placed by strides[0 .. 7] (order above); delta [B*H, S] fp32
+ * scratch, written. dq, dk, dv may share one buffer (e.g. the gradient of a fused QKV
+ * projection output) as long as their rows do not overlap. */
+int dadgpt_flash_attention_backward_bf16_strided(uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                                                 float* delta, const uint16_t* dout,
+                                                 const uint16_t* out, const float* lse,
+                                                 const uint16_t* q, const uint16_t* k,
+                                                 const uint16_t* v, int B, int H, int S,
+                                                 int d_head, float scale,
+                                                 const dadgpt_head_strides* strides,
+                                                 void* stream);
+
+/* Token-major forms: row t = b*S + s of every tensor holds the H heads' d_head values side by
+ * side, as the QKV projection produces them and the Wo projection consumes them. ld_qkv is
+ * the row pitch (elements) of q, k and v: H*d_head for three separate [B*S, H*d_head]
+ * tensors (the reference's la.q/la.k/la.v), 3*H*d_head for one fused [B*S, 3*H*d_head]
+ * projection output with k = q + H*d_head and v = q + 2*H*d_head. ld_out is the pitch of out
+ * and dout, ld_dqkv that of dq, dk, dv. Replace split_heads -> flash forward -> merge_heads
+ * (src/model.cpp:384-392,423-424) and split_heads -> flash backward -> 3x merge_heads
+ * (src/model.cpp:564-576,619-624). */
+int dadgpt_flash_attention_forward_bf16_tokens(uint16_t* out, int64_t ld_out, float* lse,
+                                               const uint16_t* q, const uint16_t* k,
+                                               const uint16_t* v, int64_t ld_qkv, int B, int H,
+                                               int S, int d_head, float scale, void* stream);
+int dadgpt_flash_attention_backward_bf16_tokens(uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                                                int64_t ld_dqkv, float* delta,
+                                                const uint16_t* dout, const uint16_t* out,
+                                                int64_t ld_out, const float* lse,
+                                                const uint16_t* q, const uint16_t* k,
+                                                const uint16_t* v, int64_t ld_qkv, int B, int H,
+                                                int S, int d_head, float scale, void* stream);
 
 /* Bytes of decode workspace for a cache shape, valid for both element types. It is 0 when
  * max_len fits one workgroup chunk (256 keys fp32 and 512 bf16 at d_head 64; 512 and 1024 at

@@ -91,6 +91,60 @@ def test_backward_phase_validation():
     assert f(1, *[FAKE] * 10, 4, 64, 40, 0.125, None) == 2
 
 
+def _strides(n, batch=1 << 16, head=64, row=768):
+    return (A.HeadStrides * n)(*[A.HeadStrides(batch, head, row) for _ in range(n)])
+
+
+def test_strided_validation():
+    L = A.lib()
+    fwd, bwd = (L.dadgpt_flash_attention_forward_bf16_strided,
+                L.dadgpt_flash_attention_backward_bf16_strided)
+    ok4, ok8 = _strides(4), _strides(8)
+    # shape and pointer checks as in the contiguous calls
+    assert fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 12, 64, 48, 0.125, ok4, None) == 2
+    assert fwd(None, FAKE, FAKE, FAKE, FAKE, 2, 12, 64, 64, 0.125, ok4, None) == 1
+    assert fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 12, 64, 64, 0.125, ok4, None) == 1
+    assert fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 0, 64, 64, 0.125, ok4, None) == 1
+    assert fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 12, 64, 64, 0.125, None, None) == 1
+    assert "strides is null" in A.last_error()
+    assert bwd(*[FAKE] * 10, 2, 12, 64, 64, 0.125, None, None) == 1
+    # every stride: a non-negative multiple of 8 with d_head <= row <= 2^24
+    for field, value in (("batch", 12), ("head", -64), ("row", 60), ("row", 776 + 4),
+                         ("row", 1 << 25)):
+        for idx in range(4):
+            st = _strides(4)
+            setattr(st[idx], field, value)
+            assert fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 12, 64, 64, 0.125, st, None) == 1
+            assert ("q", "k", "v", "out")[idx] in A.last_error()
+        st = _strides(8)
+        setattr(st[7], field, value)
+        assert bwd(*[FAKE] * 10, 2, 12, 64, 64, 0.125, st, None) == 1
+        assert "strides of dv" in A.last_error()
+    for i in range(10):
+        bad = [FAKE] * 10
+        bad[i] = None
+        assert bwd(*bad, 2, 12, 64, 64, 0.125, ok8, None) == 1
+
+
+def test_tokens_validation():
+    L = A.lib()
+    fwd, bwd = (L.dadgpt_flash_attention_forward_bf16_tokens,
+                L.dadgpt_flash_attention_backward_bf16_tokens)
+    # leading dimensions below H*d_head (heads would overlap) or not multiples of 8
+    assert fwd(FAKE, 768, FAKE, FAKE, FAKE, FAKE, 760, 2, 12, 64, 64, 0.125, None) == 1
+    assert "leading dimension 760" in A.last_error()
+    assert fwd(FAKE, 700, FAKE, FAKE, FAKE, FAKE, 2304, 2, 12, 64, 64, 0.125, None) == 1
+    assert fwd(FAKE, 772, FAKE, FAKE, FAKE, FAKE, 2304, 2, 12, 64, 64, 0.125, None) == 1
+    assert "multiple of 8" in A.last_error()
+    assert fwd(FAKE, 768, FAKE, FAKE, FAKE, FAKE, 2304, 2, 12, 64, 48, 0.125, None) == 2
+    args = lambda ld_g=2304, ld_o=768, ld_in=2304, d=64: (
+        [FAKE, FAKE, FAKE, ld_g, FAKE, FAKE, FAKE, ld_o, FAKE, FAKE, FAKE, FAKE, ld_in, 2, 12,
+         64, d, 0.125, None])
+    assert bwd(*args(ld_g=512)) == 1
+    assert bwd(*args(ld_o=1 << 25)) == 1
+    assert bwd(*args(d=40)) == 2
+
+
 def expected_ws(n, h, max_len, d):
     """One uint32 arrival counter per (sequence, head), the region padded to 256 bytes, then
     fp32 partials (max, sum, o[d]) per chunk, when the cache needs more than one chunk. fp32
