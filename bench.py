@@ -221,7 +221,7 @@ def profile_sample(wl, reps):
     import torch
     for _ in range(reps):
         wl.fwd()
-    for p in (0, 1, 2):
+    for p in (1, 2):
         run = wl.phase(p)
         for _ in range(reps):
             run()
@@ -348,7 +348,6 @@ def main():
     # per-kernel averages (same stream, back-to-back launches)
     kern_ms = {
         "fwd": event_time_ms(wl.fwd, args.reps, stream),
-        "bwd_delta": event_time_ms(wl.phase(0), args.reps, stream),
         "bwd_dq": event_time_ms(wl.phase(1), args.reps, stream),
         "bwd_dkdv": event_time_ms(wl.phase(2), args.reps, stream),
     }

@@ -2,12 +2,14 @@
 // from the saved natural-log logsumexp. Covers what cuda/attention.cu:75-205 does in fp32
 // (delta, dK/dV, dQ), restructured for MFMA:
 //
-//   delta kernel   delta[r] = sum_d dO[r,d] * O[r,d]                  (attention.cu:75-85)
+//   dQ kernel      query-major; per 32-key chunk:  S^T = K Q^T, dP^T = V dO^T,
+//                  dQ^T += K^T dS^T                                   (attention.cu:154-205)
+//                  and, first, delta[r] = sum_d dO[r,d] * O[r,d] of its rows, written for
+//                  the dK/dV kernel                                   (attention.cu:75-85)
 //   dK/dV kernel   key-major; per 32-query block:  S = Q K^T, dP = dO V^T,
 //                  P = exp(S*scale - lse), dS = P (dP - delta),
 //                  dV^T += dO^T P, dK^T += Q^T dS                    (attention.cu:87-152)
-//   dQ kernel      query-major; per 32-key chunk:  S^T = K Q^T, dP^T = V dO^T,
-//                  dQ^T += K^T dS^T                                   (attention.cu:154-205)
+//   delta kernel   delta as a pass of its own (profiling and the phase API)
 //
 // Both MFMA kernels own their outputs outright (no atomics, bitwise repeatable). The score
 // tiles use the same sigma32 row permutation as the forward so that P and dS feed the next
@@ -354,11 +356,15 @@ __device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (
   }
 }
 
+// dQ for one query block per wave; the kernel also computes delta = rowsum(dO * O) of its
+// rows (from the dO operands it holds and one load of O) and writes it for the dK/dV kernel,
+// so the backward needs no separate delta pass.
 template <int D, bool STRIDED>
 __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
-    bf16* __restrict__ dq, const bf16* __restrict__ q, const bf16* __restrict__ k,
-    const bf16* __restrict__ v, const bf16* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ delta, int S, float scale_log2, float scale, const AttnLayout L) {
+    bf16* __restrict__ dq, float* __restrict__ delta, const bf16* __restrict__ q,
+    const bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ dout,
+    const bf16* __restrict__ out, const float* __restrict__ lse, int S, float scale_log2,
+    float scale, const AttnLayout L) {
   constexpr int QB = kQW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
   // K and V tiles, double-buffered (constant buffer indices; see the forward kernel).
@@ -380,18 +386,18 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
   const int wg_last = min(S, (qblk + 1) * QB) - 1;
   const int n_tiles = wg_last / kTileRows + 1;
 
-  bf16x8 qop[DS], doop[DS];
+  // lane holds row qrow, columns 16*ds + 8*hi + 0..7 of Q, dO and O (zeros past S)
+  bf16x8 qop[DS], doop[DS], oop[DS];
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) {
     const bool in = qrow < S;
-    qop[ds] = in ? ld_g128(sl.row(q, kTQ, qrow) + 16 * ds + 8 * hi)
-                 : as_bf16x8(u32x4{0, 0, 0, 0});
-    doop[ds] = in ? ld_g128(sl.row(dout, kTDO, qrow) + 16 * ds + 8 * hi)
-                  : as_bf16x8(u32x4{0, 0, 0, 0});
+    const u32x4 z{0, 0, 0, 0};
+    qop[ds] = in ? ld_g128(sl.row(q, kTQ, qrow) + 16 * ds + 8 * hi) : as_bf16x8(z);
+    doop[ds] = in ? ld_g128(sl.row(dout, kTDO, qrow) + 16 * ds + 8 * hi) : as_bf16x8(z);
+    oop[ds] = in ? ld_g128(sl.row(out, kTO, qrow) + 16 * ds + 8 * hi) : as_bf16x8(z);
   }
-  // (rows past S read row S-1: finite values for rows that are never stored)
+  // (rows past S read row S-1: a finite value for rows that are never stored)
   float lse_q = lse[(size_t)bh * S + min(qrow, S - 1)];
-  float dlt = delta[(size_t)bh * S + min(qrow, S - 1)];
 
   f32x16 dqacc[DB];
 #pragma unroll
@@ -408,9 +414,21 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
   Dma::load_any(sv[0], vg, 0, S, voff, wave, lane, vp);
   wait_vm_lds<0>();
   __builtin_amdgcn_s_barrier();
-  // Use the two statistics only from here on, so their load shares the wait above.
-  asm volatile("" : "+v"(lse_q), "+v"(dlt));
+  // Use the loaded values only from here on, so their loads share the wait above.
+  asm volatile("" : "+v"(lse_q));
   const float lse2 = lse_q * kLog2e;
+  // delta of this lane's row: its 32 columns, then the other lane half's
+  float dpart = 0.f;
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    asm volatile("" : "+v"(oop[ds]));
+    const u32x4 a = as_u32x4(doop[ds]), o = as_u32x4(oop[ds]);
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      dpart += bf16_lo(a[w]) * bf16_lo(o[w]) + bf16_hi(a[w]) * bf16_hi(o[w]);
+  }
+  const float dlt = sum_halves(dpart);
+  if (hi == 0 && qrow < S) delta[(size_t)bh * S + qrow] = dlt;
 
   auto tile = [&](int t, const bf16* ck, const bf16* cv, bf16* nk, bf16* nv) {
     const int k0 = t * kTileRows;
@@ -466,11 +484,11 @@ hipError_t launch_bwd_bf16_t(bf16* dq, bf16* dk, bf16* dv, float* delta, const b
     constexpr int QB = kQW * kWaves;
     const dim3 grid(BH, (S + QB - 1) / QB);
     if (contiguous)
-      dq_bf16_kernel<D, false><<<grid, 64 * kWaves, 0, stream>>>(dq, q, k, v, dout, lse, delta,
-                                                                  S, sl2, scale, L);
+      dq_bf16_kernel<D, false><<<grid, 64 * kWaves, 0, stream>>>(dq, delta, q, k, v, dout, out,
+                                                                  lse, S, sl2, scale, L);
     else
-      dq_bf16_kernel<D, true><<<grid, 64 * kWaves, 0, stream>>>(dq, q, k, v, dout, lse, delta,
-                                                                 S, sl2, scale, L);
+      dq_bf16_kernel<D, true><<<grid, 64 * kWaves, 0, stream>>>(dq, delta, q, k, v, dout, out,
+                                                                 lse, S, sl2, scale, L);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (phases & kBwdDkdv) {

@@ -54,8 +54,10 @@ hipError_t launch_fwd_bf16(bf16* out, float* lse, const bf16* q, const bf16* k, 
 
 // Causal flash backward, bf16 in/out. delta [BH,S] fp32 is written (scratch, as the
 // reference's). dq/dk/dv are overwritten. `phases` selects the kernels launched, in order:
-// bit 0 delta, bit 1 dQ, bit 2 dK/dV (kBwdAll for the whole backward).
-constexpr int kBwdDelta = 1, kBwdDq = 2, kBwdDkdv = 4, kBwdAll = 7;
+// bit 1 dQ (which also computes and writes delta), bit 2 dK/dV (reads delta); kBwdAll is the
+// whole backward. Bit 0 launches the standalone delta kernel (a separate pass, equal up to
+// fp32 summation order; not part of kBwdAll).
+constexpr int kBwdDelta = 1, kBwdDq = 2, kBwdDkdv = 4, kBwdAll = kBwdDq | kBwdDkdv;
 hipError_t launch_bwd_bf16(bf16* dq, bf16* dk, bf16* dv, float* delta, const bf16* dout,
                            const bf16* out, const float* lse, const bf16* q, const bf16* k,
                            const bf16* v, int BH, int S, int D, float scale,

@@ -111,6 +111,15 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(uintptr_t)p;
 }
 
+// A wave-uniform pointer as the compiler's SGPR value (a no-op for a value already known to
+// be uniform; otherwise it reads lane 0).
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 // One 16-byte (or 4-byte) piece per lane: a wave-uniform 64-bit base in SGPRs plus a 32-bit
 // per-lane byte offset (the instruction's saddr form), so a tile loop moves only the scalar
 // base.
@@ -120,7 +129,7 @@ __device__ __forceinline__ void dma_lds16_sbase(const void* gbase, uint32_t voff
   const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
-               : "s"(base), "v"(voff), "s"(gbase)
+               : "s"(base), "v"(voff), "s"(uniform_ptr(gbase))
                : "memory");
 }
 __device__ __forceinline__ void dma_lds4_sbase(const void* gbase, uint32_t voff,
@@ -129,7 +138,7 @@ __device__ __forceinline__ void dma_lds4_sbase(const void* gbase, uint32_t voff,
   const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
                :
-               : "s"(base), "v"(voff), "s"(gbase)
+               : "s"(base), "v"(voff), "s"(uniform_ptr(gbase))
                : "memory");
 }
 

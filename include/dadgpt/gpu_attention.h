@@ -94,8 +94,9 @@ int dadgpt_flash_attention_backward_bf16(uint16_t* dq, uint16_t* dk, uint16_t* d
                                          float scale, void* stream);
 
 /* One kernel of dadgpt_flash_attention_backward_bf16, for per-kernel timing and profiling
- * (no reference counterpart). phase 0: delta = rowsum(dout * out); 1: dq (reads delta);
- * 2: dk, dv (reads delta). Running phases 0, 1, 2 in order equals the full backward. */
+ * (no reference counterpart). phase 1: dq, and delta = rowsum(dout * out) of the same rows;
+ * 2: dk, dv (reads delta). Running phases 1, 2 in order equals the full backward. phase 0
+ * computes delta alone in a separate pass (equal to phase 1's up to fp32 summation order). */
 int dadgpt_flash_attention_backward_bf16_phase(int phase, uint16_t* dq, uint16_t* dk,
                                                uint16_t* dv, float* delta,
                                                const uint16_t* dout, const uint16_t* out,
