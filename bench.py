@@ -184,6 +184,21 @@ class Workload:
         self.fwd()
         self.bwd()
 
+    def dropout(self, p=0.1, seed=7):
+        """Forward and backward with attention-probability dropout at rate p (the keep bits
+        regenerated inside the kernels)."""
+        A = self.A
+
+        def fwd():
+            A.flash_attention_forward_bf16_dropout(self.out, self.lse, self.q, self.k, self.v,
+                                                   BH, T, D, SCALE, p, seed)
+
+        def bwd():
+            A.flash_attention_backward_bf16_dropout(self.dq, self.dk, self.dv, self.delta,
+                                                    self.g, self.out, self.lse, self.q,
+                                                    self.k, self.v, BH, T, D, SCALE, p, seed)
+        return fwd, bwd
+
     def tokens(self):
         """Forward and backward over the token-major layout of a fused QKV projection
         ([B*T, 3*H*D] in, [B*T, H*D] out, gradient [B*T, 3*H*D]): the same kernels reading and
@@ -357,6 +372,13 @@ def main():
         tok_fwd()
         tok_bwd()
     tok_ms = (event_time_ms(tok_fwd, args.reps, stream), event_time_ms(tok_bwd, args.reps, stream))
+    drop_fwd, drop_bwd = wl.dropout()
+    for _ in range(3):
+        drop_fwd()
+        drop_bwd()
+    drop_ms = (event_time_ms(drop_fwd, args.reps, stream),
+               event_time_ms(drop_bwd, args.reps, stream))
+    wl.step()  # leave the undropped results in the buffers
     print(f"[bench] kernels {json.dumps({k: round(x, 4) for k, x in kern_ms.items()})}",
           file=sys.stderr, flush=True)
 
@@ -401,6 +423,10 @@ def main():
         "bwd_tflops": round(BWD_FLOPS / (tok_ms[1] * 1e-3) / 1e12, 2),
         "layout": "q,k,v in one token-major [B*T, 3*H*D] buffer, out/dout [B*T, H*D], "
                   "dq,dk,dv into one [B*T, 3*H*D] buffer"}
+    comps["dropout"] = {
+        "p": 0.1, "fwd_ms": round(drop_ms[0], 5), "bwd_ms": round(drop_ms[1], 5),
+        "fwd_tflops": round(FWD_FLOPS / (drop_ms[0] * 1e-3) / 1e12, 2),
+        "bwd_tflops": round(BWD_FLOPS / (drop_ms[1] * 1e-3) / 1e12, 2)}
     comps["decode"] = {"us_per_launch": round(dec_ms * 1e3, 3), "bytes": wl.dec_bytes,
                        "gbps": round(dec_gbps, 1),
                        "frac_hbm_peak": round(dec_gbps / PEAK_HBM_GBPS, 4),

@@ -34,6 +34,8 @@ C_SYMBOLS = (
     "dadgpt_flash_attention_forward_bf16",
     "dadgpt_flash_attention_backward_bf16",
     "dadgpt_flash_attention_backward_bf16_phase",
+    "dadgpt_flash_attention_forward_bf16_dropout",
+    "dadgpt_flash_attention_backward_bf16_dropout",
     "dadgpt_flash_attention_forward_bf16_strided",
     "dadgpt_flash_attention_backward_bf16_strided",
     "dadgpt_flash_attention_forward_bf16_tokens",
@@ -97,6 +99,10 @@ def lib():
     L.dadgpt_flash_attention_forward_bf16.argtypes = [vp] * 5 + [i, i, i, f, vp]
     L.dadgpt_flash_attention_backward_bf16.argtypes = [vp] * 10 + [i, i, i, f, vp]
     L.dadgpt_flash_attention_backward_bf16_phase.argtypes = [i] + [vp] * 10 + [i, i, i, f, vp]
+    u64 = ctypes.c_uint64
+    L.dadgpt_flash_attention_forward_bf16_dropout.argtypes = [vp] * 5 + [i, i, i, f, f, u64, vp]
+    L.dadgpt_flash_attention_backward_bf16_dropout.argtypes = [vp] * 10 + [i, i, i, f, f, u64,
+                                                                          vp]
     i64, hs = ctypes.c_int64, ctypes.POINTER(HeadStrides)
     L.dadgpt_flash_attention_forward_bf16_strided.argtypes = [vp] * 5 + [i, i, i, i, f, hs, vp]
     L.dadgpt_flash_attention_backward_bf16_strided.argtypes = [vp] * 10 + [i, i, i, i, f, hs,
@@ -207,6 +213,36 @@ def flash_attention_backward_bf16(dq, dk, dv, delta, dout, out, lse, q, k, v, BH
     _check(lib().dadgpt_flash_attention_backward_bf16(
         _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta), _ptr(dout), _ptr(out), _ptr(lse), _ptr(q),
         _ptr(k), _ptr(v), BH, S, d_head, scale, _stream_ptr(stream)))
+
+
+def flash_attention_forward_bf16_dropout(out, lse, q, k, v, BH: int, S: int, d_head: int,
+                                         scale: float, dropout_p: float, seed: int,
+                                         stream=None) -> None:
+    """bf16 forward with attention-probability dropout (the reference's materialized path
+    with dropout, src/model.cpp:406-416, fused); the mask is a function of (seed, position)."""
+    n = BH * S * d_head
+    for t, nm in ((out, "out"), (q, "q"), (k, "k"), (v, "v")):
+        _require(t, nm, torch.bfloat16, n)
+    _require(lse, "lse", torch.float32, BH * S)
+    _check(lib().dadgpt_flash_attention_forward_bf16_dropout(
+        _ptr(out), _ptr(lse), _ptr(q), _ptr(k), _ptr(v), BH, S, d_head, scale, dropout_p,
+        seed & 0xFFFFFFFFFFFFFFFF, _stream_ptr(stream)))
+
+
+def flash_attention_backward_bf16_dropout(dq, dk, dv, delta, dout, out, lse, q, k, v, BH: int,
+                                          S: int, d_head: int, scale: float, dropout_p: float,
+                                          seed: int, stream=None) -> None:
+    """The backward of flash_attention_forward_bf16_dropout with the same (dropout_p, seed)."""
+    n = BH * S * d_head
+    for t, nm in ((dq, "dq"), (dk, "dk"), (dv, "dv"), (dout, "dout"), (out, "out"),
+                  (q, "q"), (k, "k"), (v, "v")):
+        _require(t, nm, torch.bfloat16, n)
+    _require(delta, "delta", torch.float32, BH * S)
+    _require(lse, "lse", torch.float32, BH * S)
+    _check(lib().dadgpt_flash_attention_backward_bf16_dropout(
+        _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta), _ptr(dout), _ptr(out), _ptr(lse), _ptr(q),
+        _ptr(k), _ptr(v), BH, S, d_head, scale, dropout_p, seed & 0xFFFFFFFFFFFFFFFF,
+        _stream_ptr(stream)))
 
 
 def flash_attention_backward_bf16_phase(phase: int, dq, dk, dv, delta, dout, out, lse, q, k, v,

@@ -20,6 +20,7 @@
 // other blocks run branch-free. The streamed tiles (Q and dO for dK/dV, K and V for dQ) are
 // double-buffered in LDS through direct global->LDS loads, one tile ahead of the compute.
 #include "common.hpp"
+#include "dropout.hpp"
 #include "kernels.hpp"
 #include "tiles.hpp"
 
@@ -110,13 +111,16 @@ constexpr int kKW = 32;  // keys per wave
 // which leaves two multiplies and an exp2 per score on the VALU. slc holds the tile's
 // -lse/scale, sdl its -delta. MASK zeroes P for keys after the query and for tile rows past S
 // (rows_left = S - r0; those rows hold copies of row S-1).
-template <int D, bool MASK>
+//
+// With dropout (DROP; f = keep/(1-p) from bit 8j+e of `keep`): dV accumulates (P f)^T dO and
+// dS = P (dP f - delta), so dp starts from zero and -delta is read separately.
+template <int D, bool MASK, bool DROP>
 __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dvacc)[D / 32],
                                            const bf16x8 (&kop)[D / 16],
                                            const bf16x8 (&vop)[D / 16], const bf16* sq,
                                            const bf16* sdo, const float* slc, const float* sdl,
                                            int qb, int key_minus_r0, int rows_left, int lane,
-                                           float c) {
+                                           float c, uint32_t keep, float dscale) {
   constexpr int DS = D / 16, DB = D / 32;
   const int l32 = lane & 31, hi = lane >> 5;
   const int qr = 32 * qb + sigma32(l32);
@@ -149,12 +153,17 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
     bf16x8 da[DS];
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) da[ds] = lds_op(sdo, rm_off<D>(qr, 2 * ds + hi));
-    stats(sdl, dp);
+    if constexpr (DROP)
+      dp = f32x16{};
+    else
+      stats(sdl, dp);
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) dp = mfma32(da[ds], vop[ds], dp);
   }
   __builtin_amdgcn_sched_barrier(0);
   bf16x8 pb[2], dsb[2];
+  f32x16 nd;  // -delta of the block's queries (dropout only)
+  if constexpr (DROP) stats(sdl, nd);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int qt0 = 32 * qb + 16 * j + 8 * hi;
@@ -168,8 +177,14 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
         float pe = fast_exp2(s[8 * j + e] * c);
         // key > query (key - r0 > tile query index), or a row past S
         if (MASK) pe = (key_minus_r0 > qt0 + e || qt0 + e >= rows_left) ? 0.f : pe;
-        p[h] = pe;
-        d[h] = pe * dp[8 * j + e];
+        if constexpr (DROP) {
+          const float f = keep_factor(keep, 8 * j + e, dscale);
+          p[h] = pe * f;
+          d[h] = pe * fmaf(dp[8 * j + e], f, nd[8 * j + e]);
+        } else {
+          p[h] = pe;
+          d[h] = pe * dp[8 * j + e];
+        }
       }
       wp[e2] = pack_bf16x2(p[0], p[1]);
       wd[e2] = pack_bf16x2(d[0], d[1]);
@@ -203,12 +218,12 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
   }
 }
 
-template <int D, bool STRIDED>
+template <int D, bool STRIDED, bool DROP>
 __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
     bf16* __restrict__ dk, bf16* __restrict__ dv, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, float c,
-    float lse_mul, float dk_mul, const AttnLayout L) {
+    float lse_mul, float dk_mul, const AttnLayout L, const DropParams dr) {
   constexpr int KB = kKW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
   // Q and dO tiles, double-buffered (constant buffer indices in the unrolled loop; see the
@@ -288,13 +303,15 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
       for (int qb = 0; qb < 2; ++qb) {
         const int qlo = r0 + 32 * qb;  // first query of the block
         if (qlo + 31 < kw0) continue;   // every key of the wave is after every query
+        uint32_t keep = 0;
+        if constexpr (DROP) keep = keep_col16(dr, (uint64_t)bh * S + qlo, kw0, lane);
         // some key after some query, or rows past S: mask
         if (edge || qlo < kw0 + kKW - 1)
-          dkdv_block<D, true>(dkacc, dvacc, kop, vop, cq, cdo, st[cb][0], st[cb][1], qb,
-                              key - r0, S - r0, lane, c);
+          dkdv_block<D, true, DROP>(dkacc, dvacc, kop, vop, cq, cdo, st[cb][0], st[cb][1], qb,
+                                    key - r0, S - r0, lane, c, keep, dr.scale);
         else
-          dkdv_block<D, false>(dkacc, dvacc, kop, vop, cq, cdo, st[cb][0], st[cb][1], qb,
-                               key - r0, S - r0, lane, c);
+          dkdv_block<D, false, DROP>(dkacc, dvacc, kop, vop, cq, cdo, st[cb][0], st[cb][1], qb,
+                                     key - r0, S - r0, lane, c, keep, dr.scale);
       }
     }
     wait_vm_lds<0>();
@@ -315,12 +332,14 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
 constexpr int kQW = 32;  // queries per wave
 
 // One 32-key chunk (tile keys 32*kb ..) against the wave's 32 queries. Register 8j+e of lane
-// half hi holds tile key 32kb + 16j + 8hi + e.
-template <int D, bool DIAG>
+// half hi holds tile key 32kb + 16j + 8hi + e. With dropout (DROP), dS = P (dP * f - delta)
+// with f = keep/(1-p) from bit 8j+e of `keep`.
+template <int D, bool DIAG, bool DROP>
 __device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (&qop)[D / 16],
                                          const bf16x8 (&doop)[D / 16], const bf16* sk,
                                          const bf16* sv, int kb, int qrow_minus_k0, float lse2,
-                                         float dlt, int lane, float scale_log2) {
+                                         float dlt, int lane, float scale_log2, uint32_t keep,
+                                         float dscale) {
   constexpr int DS = D / 16, DB = D / 32;
   const int l32 = lane & 31, hi = lane >> 5;
   f32x16 s = f32x16{}, dp = f32x16{};
@@ -342,7 +361,10 @@ __device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (
         const int e = 2 * e2 + h;
         float p = fast_exp2(fmaf(s[8 * j + e], scale_log2, -lse2));
         if (DIAG) p = 32 * kb + 16 * j + 8 * hi + e > qrow_minus_k0 ? 0.f : p;
-        d[h] = p * (dp[8 * j + e] - dlt);
+        if constexpr (DROP)
+          d[h] = p * fmaf(dp[8 * j + e], keep_factor(keep, 8 * j + e, dscale), -dlt);
+        else
+          d[h] = p * (dp[8 * j + e] - dlt);
       }
       w[e2] = pack_bf16x2(d[0], d[1]);
     }
@@ -359,12 +381,12 @@ __device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (
 // dQ for one query block per wave; the kernel also computes delta = rowsum(dO * O) of its
 // rows (from the dO operands it holds and one load of O) and writes it for the dK/dV kernel,
 // so the backward needs no separate delta pass.
-template <int D, bool STRIDED>
+template <int D, bool STRIDED, bool DROP>
 __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
     bf16* __restrict__ dq, float* __restrict__ delta, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ dout,
     const bf16* __restrict__ out, const float* __restrict__ lse, int S, float scale_log2,
-    float scale, const AttnLayout L) {
+    float scale, const AttnLayout L, const DropParams dr) {
   constexpr int QB = kQW * kWaves;
   constexpr int DS = D / 16, DB = D / 32;
   // K and V tiles, double-buffered (constant buffer indices; see the forward kernel).
@@ -441,12 +463,14 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
       for (int kb = 0; kb < 2; ++kb) {
         const int klo = k0 + 32 * kb;        // first key of the chunk
         if (klo > q0 + kQW - 1) continue;    // every key after every query of the wave
+        uint32_t keep = 0;
+        if constexpr (DROP) keep = keep_row16(dr, (uint64_t)bh * S + qrow, klo, hi);
         if (klo + 31 > q0)                   // some key after some query: mask
-          dq_chunk<D, true>(dqacc, qop, doop, ck, cv, kb, qrow - k0, lse2, dlt, lane,
-                            scale_log2);
+          dq_chunk<D, true, DROP>(dqacc, qop, doop, ck, cv, kb, qrow - k0, lse2, dlt, lane,
+                                  scale_log2, keep, dr.scale);
         else
-          dq_chunk<D, false>(dqacc, qop, doop, ck, cv, kb, qrow - k0, lse2, dlt, lane,
-                             scale_log2);
+          dq_chunk<D, false, DROP>(dqacc, qop, doop, ck, cv, kb, qrow - k0, lse2, dlt, lane,
+                                   scale_log2, keep, dr.scale);
       }
     }
     wait_vm_lds<0>();
@@ -464,9 +488,10 @@ template <int D>
 hipError_t launch_bwd_bf16_t(bf16* dq, bf16* dk, bf16* dv, float* delta, const bf16* dout,
                              const bf16* out, const float* lse, const bf16* q, const bf16* k,
                              const bf16* v, int BH, int S, float scale, const AttnLayout& L,
-                             hipStream_t stream, int phases) {
+                             hipStream_t stream, int phases, const Dropout* drop) {
   hipError_t e = hipSuccess;
   const bool contiguous = is_contiguous(L, S, D);
+  const DropParams dr = drop_params(drop);  // dropout: contiguous layout only (caller checks)
   if (phases & kBwdDelta) {
     const long long rows = (long long)BH * S;
     const int row_blocks = (S + 31) / 32;
@@ -483,12 +508,15 @@ hipError_t launch_bwd_bf16_t(bf16* dq, bf16* dk, bf16* dv, float* delta, const b
   if (phases & kBwdDq) {
     constexpr int QB = kQW * kWaves;
     const dim3 grid(BH, (S + QB - 1) / QB);
-    if (contiguous)
-      dq_bf16_kernel<D, false><<<grid, 64 * kWaves, 0, stream>>>(dq, delta, q, k, v, dout, out,
-                                                                  lse, S, sl2, scale, L);
+    if (drop != nullptr)
+      dq_bf16_kernel<D, false, true><<<grid, 64 * kWaves, 0, stream>>>(
+          dq, delta, q, k, v, dout, out, lse, S, sl2, scale, L, dr);
+    else if (contiguous)
+      dq_bf16_kernel<D, false, false><<<grid, 64 * kWaves, 0, stream>>>(
+          dq, delta, q, k, v, dout, out, lse, S, sl2, scale, L, dr);
     else
-      dq_bf16_kernel<D, true><<<grid, 64 * kWaves, 0, stream>>>(dq, delta, q, k, v, dout, out,
-                                                                 lse, S, sl2, scale, L);
+      dq_bf16_kernel<D, true, false><<<grid, 64 * kWaves, 0, stream>>>(
+          dq, delta, q, k, v, dout, out, lse, S, sl2, scale, L, dr);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (phases & kBwdDkdv) {
@@ -497,12 +525,15 @@ hipError_t launch_bwd_bf16_t(bf16* dq, bf16* dk, bf16* dv, float* delta, const b
     // whose S*scale terms are then below fp32 resolution next to lse/scale.
     const float se = scale != 0.f ? scale : 1e-30f;
     const dim3 grid(BH, (S + KB - 1) / KB);
-    if (contiguous)
-      dkdv_bf16_kernel<D, false><<<grid, 64 * kWaves, 0, stream>>>(
-          dk, dv, q, k, v, dout, lse, delta, S, se * kLog2e, -1.0f / se, scale, L);
+    if (drop != nullptr)
+      dkdv_bf16_kernel<D, false, true><<<grid, 64 * kWaves, 0, stream>>>(
+          dk, dv, q, k, v, dout, lse, delta, S, se * kLog2e, -1.0f / se, scale, L, dr);
+    else if (contiguous)
+      dkdv_bf16_kernel<D, false, false><<<grid, 64 * kWaves, 0, stream>>>(
+          dk, dv, q, k, v, dout, lse, delta, S, se * kLog2e, -1.0f / se, scale, L, dr);
     else
-      dkdv_bf16_kernel<D, true><<<grid, 64 * kWaves, 0, stream>>>(
-          dk, dv, q, k, v, dout, lse, delta, S, se * kLog2e, -1.0f / se, scale, L);
+      dkdv_bf16_kernel<D, true, false><<<grid, 64 * kWaves, 0, stream>>>(
+          dk, dv, q, k, v, dout, lse, delta, S, se * kLog2e, -1.0f / se, scale, L, dr);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return e;
@@ -513,13 +544,14 @@ hipError_t launch_bwd_bf16_t(bf16* dq, bf16* dk, bf16* dv, float* delta, const b
 hipError_t launch_bwd_bf16(bf16* dq, bf16* dk, bf16* dv, float* delta, const bf16* dout,
                            const bf16* out, const float* lse, const bf16* q, const bf16* k,
                            const bf16* v, int BH, int S, int D, float scale,
-                           const AttnLayout& layout, hipStream_t stream, int phases) {
+                           const AttnLayout& layout, hipStream_t stream, int phases,
+                           const Dropout* drop) {
   if (D == 64)
     return launch_bwd_bf16_t<64>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale,
-                                 layout, stream, phases);
+                                 layout, stream, phases, drop);
   if (D == 32)
     return launch_bwd_bf16_t<32>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale,
-                                 layout, stream, phases);
+                                 layout, stream, phases, drop);
   return hipErrorInvalidValue;
 }
 

@@ -31,6 +31,7 @@
 // tile. (Triple buffering measured slower: the third buffer's LDS cost more than the extra
 // tile of lead gained.)
 #include "common.hpp"
+#include "dropout.hpp"
 #include "kernels.hpp"
 #include "tiles.hpp"
 
@@ -123,8 +124,11 @@ __device__ __forceinline__ void fwd_v_ops(bf16x8 (&va)[D / 32][2], const bf16* l
 }
 
 // P = exp2(s*c - m) of one chunk as bf16 B operands; returns this lane's fp32 sum of them.
+// With dropout (DROP), the operands are P * keep/(1-p) (register r kept iff bit r of keep) and
+// the sum stays that of P: the normaliser and logsumexp are those of the undropped row.
+template <bool DROP>
 __device__ __forceinline__ float fwd_exp(bf16x8 (&pb)[2], const f32x16& s, float m,
-                                         float scale_log2) {
+                                         float scale_log2, uint32_t keep, float dscale) {
   const float mneg = -m;
   float ls = 0.f;
 #pragma unroll
@@ -135,7 +139,11 @@ __device__ __forceinline__ float fwd_exp(bf16x8 (&pb)[2], const f32x16& s, float
       const int r = 8 * j + 2 * e;
       const float p0 = fast_exp2(fmaf(s[r], scale_log2, mneg));
       const float p1 = fast_exp2(fmaf(s[r + 1], scale_log2, mneg));
-      w[e] = pack_bf16x2(p0, p1);
+      if constexpr (DROP)
+        w[e] = pack_bf16x2(p0 * keep_factor(keep, r, dscale),
+                           p1 * keep_factor(keep, r + 1, dscale));
+      else
+        w[e] = pack_bf16x2(p0, p1);
       ls += p0 + p1;
     }
     pb[j] = as_bf16x8(w);
@@ -154,15 +162,16 @@ __device__ __forceinline__ float fwd_exp(bf16x8 (&pb)[2], const f32x16& s, float
 // chunk's maximum, O and l are rescaled, and the chunk's exponentials are redone. That is a
 // wave's first chunk and, for ordinary scores, almost nothing else, so the row maximum is
 // off the per-chunk path.
-template <int D, int NQB>
+template <int D, int NQB, bool DROP>
 __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[NQB][D / 32],
                                                float (&mrun)[NQB], float (&lrun)[NQB],
-                                               const bf16x8 (&va)[D / 32][2], float scale_log2) {
+                                               const bf16x8 (&va)[D / 32][2], float scale_log2,
+                                               const uint32_t (&keep)[NQB], float dscale) {
   constexpr int DB = D / 32;
   bf16x8 pb[NQB][2];
 #pragma unroll
   for (int i = 0; i < NQB; ++i) {
-    float ls = fwd_exp(pb[i], s[i], mrun[i], scale_log2);
+    float ls = fwd_exp<DROP>(pb[i], s[i], mrun[i], scale_log2, keep[i], dscale);
     if (__builtin_amdgcn_ballot_w64(!(ls < kMaxP)) != 0) {  // wave-uniform
       float mx = s[i][0];
 #pragma unroll
@@ -175,7 +184,7 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[
       lrun[i] *= corr;
 #pragma unroll
       for (int db = 0; db < DB; ++db) oacc[i][db] *= corr;
-      ls = fwd_exp(pb[i], s[i], mnew, scale_log2);
+      ls = fwd_exp<DROP>(pb[i], s[i], mnew, scale_log2, keep[i], dscale);
     }
     lrun[i] += ls;
   }
@@ -188,12 +197,12 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[
       for (int i = 0; i < NQB; ++i) oacc[i][db] = mfma32(va[db][j], pb[i][j], oacc[i][db]);
 }
 
-template <int D, bool STRIDED>
+template <int D, bool STRIDED, bool DROP>
 __global__ __launch_bounds__(64 * kWaves, kMinBlocks)
 __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_kernel(
     bf16* __restrict__ out, float* __restrict__ lse, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, int S, float scale_log2,
-    int negate_q, const AttnLayout L) {
+    int negate_q, const AttnLayout L, const DropParams dr) {
   // scale_log2 = |scale| * log2(e); a negative scale is applied by negating Q (exact in bf16),
   // so the row max of the raw scores is the row max of the scaled ones.
   constexpr int QB = kQW * kWaves;
@@ -280,6 +289,12 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
         if (c0 > q0 + kQW - 1) break;  // every key of the chunk after every query
         bf16x8 ka[DS], va[DB][2];
         f32x16 sc[kNQB];
+        uint32_t keep[kNQB] = {};
+        if constexpr (DROP) {
+#pragma unroll
+          for (int i = 0; i < kNQB; ++i)
+            keep[i] = keep_row16(dr, (uint64_t)bh * S + q0 + 32 * i + l32, c0, hi);
+        }
         fwd_k_ops<D>(ka, ck, kb, lane);
         // the chunk whose first key is the wave's first query is the one to mask
         if (c0 == q0)
@@ -289,7 +304,7 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
         // V^T operands only now (K's are dead): their latency hides under the softmax
         __builtin_amdgcn_sched_barrier(0);
         fwd_v_ops<D>(va, cv, kb, lane);
-        fwd_softmax_pv<D, kNQB>(sc, oacc, mrun, lrun, va, scale_log2);
+        fwd_softmax_pv<D, kNQB, DROP>(sc, oacc, mrun, lrun, va, scale_log2, keep, dr.scale);
       }
     }
     wait_vm_lds<0>();
@@ -326,19 +341,24 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
 template <int D>
 hipError_t launch_fwd_bf16_t(bf16* out, float* lse, const bf16* q, const bf16* k, const bf16* v,
                              int BH, int S, float scale, const AttnLayout& L,
-                             hipStream_t stream) {
+                             const Dropout* drop, hipStream_t stream) {
   constexpr int QB = kQW * kWaves;
   dim3 grid(BH, (S + QB - 1) / QB);
   // Masked scores are -inf and exponentiate as exp2(-inf * c - m), so c must be positive: a
   // zero scale (uniform attention) runs with c = 1e-30: every score below 1e22 in magnitude
   // then has |s*c - m| < 2^-25, an fp32 weight of exactly 1.
   const float c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);
-  if (is_contiguous(L, S, D))
-    fwd_bf16_kernel<D, false><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c,
-                                                                scale < 0.f, L);
-  else
-    fwd_bf16_kernel<D, true><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c,
-                                                               scale < 0.f, L);
+  const DropParams dr = drop_params(drop);
+  if (drop != nullptr) {  // contiguous layout only (checked by the caller)
+    fwd_bf16_kernel<D, false, true><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c,
+                                                                      scale < 0.f, L, dr);
+  } else if (is_contiguous(L, S, D)) {
+    fwd_bf16_kernel<D, false, false><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c,
+                                                                       scale < 0.f, L, dr);
+  } else {
+    fwd_bf16_kernel<D, true, false><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c,
+                                                                      scale < 0.f, L, dr);
+  }
   return hipGetLastError();
 }
 
@@ -346,9 +366,11 @@ hipError_t launch_fwd_bf16_t(bf16* out, float* lse, const bf16* q, const bf16* k
 
 hipError_t launch_fwd_bf16(bf16* out, float* lse, const bf16* q, const bf16* k, const bf16* v,
                            int BH, int S, int D, float scale, const AttnLayout& layout,
-                           hipStream_t stream) {
-  if (D == 64) return launch_fwd_bf16_t<64>(out, lse, q, k, v, BH, S, scale, layout, stream);
-  if (D == 32) return launch_fwd_bf16_t<32>(out, lse, q, k, v, BH, S, scale, layout, stream);
+                           hipStream_t stream, const Dropout* drop) {
+  if (D == 64)
+    return launch_fwd_bf16_t<64>(out, lse, q, k, v, BH, S, scale, layout, drop, stream);
+  if (D == 32)
+    return launch_fwd_bf16_t<32>(out, lse, q, k, v, BH, S, scale, layout, drop, stream);
   return hipErrorInvalidValue;
 }
 

@@ -92,6 +92,13 @@ int check_decode(const char* fn, int n_seq, int H, int max_len, int d_head, floa
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
+int check_dropout(const char* fn, float p) {
+  if (!(p >= 0.0f && p < 1.0f))
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: dropout_p must be in [0, 1), got %g", fn,
+                (double)p);
+  return DADGPT_OK;
+}
+
 // Strides of the strided/token-major calls: non-negative multiples of 8 elements (the kernels
 // move 16-byte pieces), rows at least d_head apart and at most 2^24 (64 rows of a tile stay
 // within a 32-bit byte offset). Converts them to the kernels' layout.
@@ -220,6 +227,39 @@ int dadgpt_flash_attention_backward_bf16(uint16_t* dq, uint16_t* dk, uint16_t* d
                                           B(q), B(k), B(v), BH, S, d_head, scale,
                                           dadgpt::contiguous_layout(S, d_head),
                                           as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_flash_attention_forward_bf16_dropout(uint16_t* out, float* lse, const uint16_t* q,
+                                                const uint16_t* k, const uint16_t* v, int BH,
+                                                int S, int d_head, float scale,
+                                                float dropout_p, uint64_t seed, void* stream) {
+  const char* fn = "dadgpt_flash_attention_forward_bf16_dropout";
+  if (int st = check_attn(fn, BH, S, d_head, scale, {out, lse, q, k, v})) return st;
+  if (int st = check_dropout(fn, dropout_p)) return st;
+  const dadgpt::Dropout drop{dropout_p, seed};
+  return from_hip(dadgpt::launch_fwd_bf16(B(out), lse, B(q), B(k), B(v), BH, S, d_head, scale,
+                                          dadgpt::contiguous_layout(S, d_head),
+                                          as_stream(stream), &drop),
+                  fn);
+}
+
+int dadgpt_flash_attention_backward_bf16_dropout(uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                                                 float* delta, const uint16_t* dout,
+                                                 const uint16_t* out, const float* lse,
+                                                 const uint16_t* q, const uint16_t* k,
+                                                 const uint16_t* v, int BH, int S, int d_head,
+                                                 float scale, float dropout_p, uint64_t seed,
+                                                 void* stream) {
+  const char* fn = "dadgpt_flash_attention_backward_bf16_dropout";
+  if (int st = check_attn(fn, BH, S, d_head, scale, {dq, dk, dv, delta, dout, out, lse, q, k, v}))
+    return st;
+  if (int st = check_dropout(fn, dropout_p)) return st;
+  const dadgpt::Dropout drop{dropout_p, seed};
+  return from_hip(dadgpt::launch_bwd_bf16(B(dq), B(dk), B(dv), delta, B(dout), B(out), lse,
+                                          B(q), B(k), B(v), BH, S, d_head, scale,
+                                          dadgpt::contiguous_layout(S, d_head),
+                                          as_stream(stream), dadgpt::kBwdAll, &drop),
                   fn);
 }
 

@@ -46,11 +46,20 @@ inline bool is_contiguous(const AttnLayout& L, int S, int D) {
   return true;
 }
 
+// Attention-probability dropout of a call: rate p in [0, 1) and the generator's seed (the
+// mask definition is in dropout.hpp). The host checks p; dropout runs on the contiguous
+// layout only.
+struct Dropout {
+  float p;
+  uint64_t seed;
+};
+
 // Causal flash forward, bf16 in/out, fp32 logsumexp (natural log) [BH, S]. q, k, v, out as
-// `layout` places them (tensors kTQ, kTK, kTV, kTO), D in {32,64}.
+// `layout` places them (tensors kTQ, kTK, kTV, kTO), D in {32,64}. With `drop`, the
+// probabilities multiplying V are dropped (the logsumexp is that of the undropped scores).
 hipError_t launch_fwd_bf16(bf16* out, float* lse, const bf16* q, const bf16* k, const bf16* v,
                            int BH, int S, int D, float scale, const AttnLayout& layout,
-                           hipStream_t stream);
+                           hipStream_t stream, const Dropout* drop = nullptr);
 
 // Causal flash backward, bf16 in/out. delta [BH,S] fp32 is written (scratch, as the
 // reference's). dq/dk/dv are overwritten. `phases` selects the kernels launched, in order:
@@ -61,7 +70,8 @@ constexpr int kBwdDelta = 1, kBwdDq = 2, kBwdDkdv = 4, kBwdAll = kBwdDq | kBwdDk
 hipError_t launch_bwd_bf16(bf16* dq, bf16* dk, bf16* dv, float* delta, const bf16* dout,
                            const bf16* out, const float* lse, const bf16* q, const bf16* k,
                            const bf16* v, int BH, int S, int D, float scale,
-                           const AttnLayout& layout, hipStream_t stream, int phases = kBwdAll);
+                           const AttnLayout& layout, hipStream_t stream, int phases = kBwdAll,
+                           const Dropout* drop = nullptr);
 
 // fp32 flash forward/backward (the reference's own precision).
 hipError_t launch_fwd_f32(float* out, float* lse, const float* q, const float* k,

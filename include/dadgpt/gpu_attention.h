@@ -93,6 +93,27 @@ int dadgpt_flash_attention_backward_bf16(uint16_t* dq, uint16_t* dk, uint16_t* d
                                          const uint16_t* v, int BH, int S, int d_head,
                                          float scale, void* stream);
 
+/* ---- Attention-probability dropout (replaces the reference's materialized path with
+ * dropout: gpu_dropout_forward on P before P V, src/model.cpp:406-416, and
+ * gpu_dropout_backward on dP, :591-596; kernels cuda/gpu_ops.cu:712-749). Fused into the
+ * flash kernels: the keep bits are regenerated in the backward, no mask is stored. Kept
+ * probabilities are scaled by 1/(1-p) (fp32), as the reference does; lse stays that of the
+ * undropped scores. The mask is not cuRAND's: probability (row = bh*S + i, key j) is kept
+ * iff (w >> 8) >= ceil(p * 2^24), w = word j%4 of Philox4x32-10 (Salmon et al., SC'11) at
+ * counter {row lo, row hi, j/4, 0} under key {seed lo, seed hi}. The backward must get the
+ * forward's (dropout_p, seed). dropout_p in [0, 1); contiguous [BH, S, d_head] layout. */
+int dadgpt_flash_attention_forward_bf16_dropout(uint16_t* out, float* lse, const uint16_t* q,
+                                                const uint16_t* k, const uint16_t* v, int BH,
+                                                int S, int d_head, float scale,
+                                                float dropout_p, uint64_t seed, void* stream);
+int dadgpt_flash_attention_backward_bf16_dropout(uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                                                 float* delta, const uint16_t* dout,
+                                                 const uint16_t* out, const float* lse,
+                                                 const uint16_t* q, const uint16_t* k,
+                                                 const uint16_t* v, int BH, int S, int d_head,
+                                                 float scale, float dropout_p, uint64_t seed,
+                                                 void* stream);
+
 /* One kernel of dadgpt_flash_attention_backward_bf16, for per-kernel timing and profiling
  * (no reference counterpart). phase 1: dq, and delta = rowsum(dout * out) of the same rows;
  * 2: dk, dv (reads delta). Running phases 1, 2 in order equals the full backward. phase 0

@@ -74,6 +74,19 @@ def lib():
         L.oracle_attn_bwd_f64.argtypes = [_dp, _dp, _dp, _dp, _dp, _dp, _dp, i, i, i, d]
         L.oracle_attn_fwd_f32_mt.argtypes = [_fp, _fp, _fp, _fp, _fp, i, i, i, f, i]
         L.oracle_attn_bwd_f32_mt.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, _fp, i, i, i, f, i]
+        u32p, u8p, u64 = (ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint8),
+                          ctypes.c_uint64)
+        L.oracle_philox4x32_10.argtypes = [u32p, u32p, u32p]
+        L.oracle_philox4x32_10.restype = None
+        L.oracle_dropout_threshold.argtypes = [f]
+        L.oracle_dropout_threshold.restype = ctypes.c_uint32
+        L.oracle_dropout_mask.argtypes = [u8p, i, i, u64, f]
+        L.oracle_dropout_mask.restype = None
+        L.oracle_attn_fwd_dropout_f32.argtypes = [_fp, _fp, _fp, _fp, _fp, i, i, i, f, f, u64]
+        L.oracle_attn_bwd_dropout_f32.argtypes = ([_fp] * 9 + [i, i, i, f, f, u64])
+        L.oracle_attn_fwd_dropout_f32_range.argtypes = [_fp] * 5 + [i, i, i, i, f, f, u64]
+        L.oracle_attn_fwd_dropout_f64.argtypes = [_dp, _dp, _dp, _dp, _dp, i, i, i, d, f, u64]
+        L.oracle_attn_bwd_dropout_f64.argtypes = [_dp] * 7 + [i, i, i, d, f, u64]
         _lib = L
     return _lib
 
@@ -209,6 +222,91 @@ def attn_bwd_f64(dout, q, k, v, scale):
     dq, dk, dv = np.empty_like(q), np.empty_like(q), np.empty_like(q)
     _check(lib().oracle_attn_bwd_f64(_d(dq), _d(dk), _d(dv), _d(dout), _d(q), _d(k), _d(v), BH,
                                      S, D, scale), "attn_bwd_f64")
+    return dq, dk, dv
+
+
+# ---- attention-probability dropout (Philox4x32-10 mask; see attn_oracle.h) ----
+
+def philox4x32_10(ctr, key):
+    """Philox4x32-10 block: ctr 4 x uint32, key 2 x uint32 -> 4 x uint32."""
+    c = np.ascontiguousarray(ctr, dtype=np.uint32)
+    k = np.ascontiguousarray(key, dtype=np.uint32)
+    out = np.empty(4, np.uint32)
+    u32p = ctypes.POINTER(ctypes.c_uint32)
+    lib().oracle_philox4x32_10(c.ctypes.data_as(u32p), k.ctypes.data_as(u32p),
+                               out.ctypes.data_as(u32p))
+    return out
+
+
+def dropout_threshold(p):
+    return int(lib().oracle_dropout_threshold(p))
+
+
+def dropout_mask(BH, S, seed, p):
+    """Keep bits [BH, S, S] (1 = kept) of the dropout mask for (seed, p)."""
+    m = np.empty((BH, S, S), np.uint8)
+    lib().oracle_dropout_mask(m.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), BH, S, seed, p)
+    return m
+
+
+def attn_fwd_dropout(q, k, v, scale, p, seed):
+    """Causal forward with dropout of the probabilities, fp32. Returns (O, lse)."""
+    q, k, v = _c32(q), _c32(k), _c32(v)
+    BH, S, D = q.shape
+    o = np.empty_like(q)
+    lse = np.empty((BH, S), np.float32)
+    _check(lib().oracle_attn_fwd_dropout_f32(_f(o), _f(lse), _f(q), _f(k), _f(v), BH, S, D,
+                                             scale, p, seed), "attn_fwd_dropout")
+    return o, lse
+
+
+def attn_fwd_dropout_slices(q, k, v, scale, p, seed, bh0, bh1):
+    """Forward with dropout over bh slices [bh0, bh1) of [BH, S, D] inputs (the mask rows keep
+    their global index). Returns O of those slices."""
+    q, k, v = _c32(q), _c32(k), _c32(v)
+    BH, S, D = q.shape
+    o = np.zeros_like(q)
+    _check(lib().oracle_attn_fwd_dropout_f32_range(_f(o), ctypes.cast(None, _fp), _f(q), _f(k),
+                                                   _f(v), bh0, bh1, S, D, scale, p, seed),
+           "attn_fwd_dropout_slices")
+    return o[bh0:bh1]
+
+
+def attn_bwd_dropout(dout, q, k, v, scale, p, seed, out=None):
+    """Causal backward with dropout, fp32. Returns (dQ, dK, dV, delta|None)."""
+    dout, q, k, v = _c32(dout), _c32(q), _c32(k), _c32(v)
+    BH, S, D = q.shape
+    dq, dk, dv = np.empty_like(q), np.empty_like(q), np.empty_like(q)
+    delta = None
+    null = ctypes.cast(None, _fp)
+    if out is not None:
+        out = _c32(out)
+        delta = np.empty((BH, S), np.float32)
+    rc = lib().oracle_attn_bwd_dropout_f32(_f(dq), _f(dk), _f(dv),
+                                           _f(delta) if delta is not None else null, _f(dout),
+                                           _f(out) if out is not None else null, _f(q), _f(k),
+                                           _f(v), BH, S, D, scale, p, seed)
+    _check(rc, "attn_bwd_dropout")
+    return dq, dk, dv, delta
+
+
+def attn_fwd_dropout_f64(q, k, v, scale, p, seed):
+    q, k, v = _c64(q), _c64(k), _c64(v)
+    BH, S, D = q.shape
+    o = np.empty_like(q)
+    lse = np.empty((BH, S), np.float64)
+    _check(lib().oracle_attn_fwd_dropout_f64(_d(o), _d(lse), _d(q), _d(k), _d(v), BH, S, D,
+                                             scale, p, seed), "attn_fwd_dropout_f64")
+    return o, lse
+
+
+def attn_bwd_dropout_f64(dout, q, k, v, scale, p, seed):
+    dout, q, k, v = _c64(dout), _c64(q), _c64(k), _c64(v)
+    BH, S, D = q.shape
+    dq, dk, dv = np.empty_like(q), np.empty_like(q), np.empty_like(q)
+    _check(lib().oracle_attn_bwd_dropout_f64(_d(dq), _d(dk), _d(dv), _d(dout), _d(q), _d(k),
+                                             _d(v), BH, S, D, scale, p, seed),
+           "attn_bwd_dropout_f64")
     return dq, dk, dv
 
 

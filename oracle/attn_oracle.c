@@ -20,6 +20,7 @@
 
 #include <math.h>
 #include <pthread.h>
+#include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -103,12 +104,85 @@ static void causal_zero_f32(float* s, int S) {
     for (int j = i + 1; j < S; ++j) s[(long)i * S + j] = 0.0f;
 }
 
+/* ---- attention-probability dropout ----
+ * The reference drops probabilities with cuRAND (cuda/gpu_ops.cu:712-733: keep iff a uniform
+ * r >= rate, kept values times 1/(1-rate) in fp32, the gradient masked and scaled the same
+ * way, :736-749). cuRAND's stream is not reproduced here; this build's mask comes from
+ * Philox4x32-10 as published (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy
+ * as 1, 2, 3", SC'11): the keep bit of probability (row = bh*S + i, key j) is word j%4 of
+ * Philox4x32-10 at counter {row lo, row hi, j/4, 0} under key {seed lo, seed hi}, kept iff
+ * (word >> 8) >= thr with thr = ceil(p * 2^24), i.e. a 24-bit uniform u >= p. */
+static uint32_t mulhilo32(uint32_t a, uint32_t b, uint32_t* hi) {
+  const uint64_t prod = (uint64_t)a * b;
+  *hi = (uint32_t)(prod >> 32);
+  return (uint32_t)prod;
+}
+
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+  uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+  uint32_t k0 = key[0], k1 = key[1];
+  for (int r = 0; r < 10; ++r) {
+    if (r > 0) { /* key schedule: Weyl increments between rounds */
+      k0 += 0x9E3779B9u;
+      k1 += 0xBB67AE85u;
+    }
+    uint32_t hi0, hi1;
+    const uint32_t lo0 = mulhilo32(0xD2511F53u, c0, &hi0);
+    const uint32_t lo1 = mulhilo32(0xCD9E8D57u, c2, &hi1);
+    const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0;
+    c1 = lo1;
+    c2 = n2;
+    c3 = lo0;
+  }
+  out[0] = c0;
+  out[1] = c1;
+  out[2] = c2;
+  out[3] = c3;
+}
+
+uint32_t oracle_dropout_threshold(float p) { return (uint32_t)ceil((double)p * 16777216.0); }
+
+int oracle_dropout_keep(uint64_t seed, uint64_t row, int j, uint32_t thr) {
+  const uint32_t ctr[4] = {(uint32_t)row, (uint32_t)(row >> 32), (uint32_t)j >> 2, 0u};
+  const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+  uint32_t w[4];
+  oracle_philox4x32_10(ctr, key, w);
+  return (w[j & 3] >> 8) >= thr;
+}
+
+void oracle_dropout_mask(uint8_t* mask, int BH, int S, uint64_t seed, float p) {
+  const uint32_t thr = oracle_dropout_threshold(p);
+  for (long row = 0; row < (long)BH * S; ++row)
+    for (int j = 0; j < S; ++j)
+      mask[row * S + j] = (uint8_t)oracle_dropout_keep(seed, (uint64_t)row, j, thr);
+}
+
+/* Dropout of one slice's probabilities (rows bh*S ..): Pd = keep ? P * (1/(1-p)) : 0, the
+ * fp32 products of gpu_dropout_forward (cuda/gpu_ops.cu:712-726); keep bits kept in `keep`. */
+typedef struct {
+  uint64_t seed;
+  uint32_t thr;
+  float scale; /* 1/(1-p) in fp32, as cuda/gpu_ops.cu:718 */
+} drop_t;
+
+static void dropout_slice_f32(float* Pd, uint8_t* keep, const float* P, int S, int bh,
+                              const drop_t* dr) {
+  for (int i = 0; i < S; ++i)
+    for (int j = 0; j < S; ++j) {
+      const long n = (long)i * S + j;
+      const int k = oracle_dropout_keep(dr->seed, (uint64_t)bh * S + i, j, dr->thr);
+      keep[n] = (uint8_t)k;
+      Pd[n] = k ? P[n] * dr->scale : 0.0f;
+    }
+}
+
 /* ---- forward ---- */
 
 /* One (b,h) slice: S = QK^T, *scale, lse (closed form over j<=i), mask, softmax, O = PV.
  * Op order of model.cpp:396-419. P is [S,S] scratch and holds the probabilities on return. */
-static void fwd_slice_f32(float* O, float* lse, const float* Q, const float* K, const float* V,
-                          int S, int D, float scale, float* P) {
+static void probs_slice_f32(float* lse, const float* Q, const float* K, int S, int D,
+                            float scale, float* P) {
   mm_bt_f32(P, Q, K, S, D, S);
   scale_f32(P, (long)S * S, scale);
   if (lse) {
@@ -124,6 +198,11 @@ static void fwd_slice_f32(float* O, float* lse, const float* Q, const float* K, 
   }
   causal_fill_f32(P, S);
   softmax_rows_f32(P, P, S, S);
+}
+
+static void fwd_slice_f32(float* O, float* lse, const float* Q, const float* K, const float* V,
+                          int S, int D, float scale, float* P) {
+  probs_slice_f32(lse, Q, K, S, D, scale, P);
   mm_f32(O, P, V, S, S, D);
 }
 
@@ -194,6 +273,75 @@ int oracle_attn_bwd_f32(float* dQ, float* dK, float* dV, float* delta, const flo
                         int S, int D, float scale) {
   if (delta) oracle_attn_delta_f32(delta, dO, O, (long)BH * S, D);
   return oracle_attn_bwd_f32_range(dQ, dK, dV, dO, Q, K, V, 0, BH, S, D, scale);
+}
+
+/* ---- forward and backward with attention-probability dropout ----
+ * Op order of the materialized path with dropout (src/model.cpp:396-419 with :406-416;
+ * :585-615 with :591-596): forward S = QK^T, *scale, mask, softmax -> P; Pd = dropout(P);
+ * O = Pd V. Backward dPd = dO V^T; dV = Pd^T dO; dP = dPd * (keep * 1/(1-p))
+ * (gpu_dropout_backward, cuda/gpu_ops.cu:736-741); dS = softmax_bwd(dP, P); zero j>i;
+ * *scale; dQ = dS K; dK = dS^T Q. lse is that of the undropped scores. */
+static int drop_params(drop_t* dr, float p, uint64_t seed) {
+  if (!(p >= 0.0f && p < 1.0f)) return -3;
+  dr->seed = seed;
+  dr->thr = oracle_dropout_threshold(p);
+  dr->scale = 1.0f / (1.0f - p);
+  return 0;
+}
+
+int oracle_attn_fwd_dropout_f32_range(float* O, float* lse, const float* Q, const float* K,
+                                      const float* V, int bh0, int bh1, int S, int D,
+                                      float scale, float p, uint64_t seed) {
+  drop_t dr;
+  if (drop_params(&dr, p, seed)) return -3;
+  const size_t ss = (size_t)S * S;
+  float* P = (float*)malloc(sizeof(float) * 2 * ss + ss);
+  if (!P) return -1;
+  float* Pd = P + ss;
+  uint8_t* keep = (uint8_t*)(P + 2 * ss);
+  for (int bh = bh0; bh < bh1; ++bh) {
+    const long o = (long)bh * S * D;
+    probs_slice_f32(lse ? lse + (long)bh * S : NULL, Q + o, K + o, S, D, scale, P);
+    dropout_slice_f32(Pd, keep, P, S, bh, &dr);
+    mm_f32(O + o, Pd, V + o, S, S, D);
+  }
+  free(P);
+  return 0;
+}
+
+int oracle_attn_fwd_dropout_f32(float* O, float* lse, const float* Q, const float* K,
+                                const float* V, int BH, int S, int D, float scale, float p,
+                                uint64_t seed) {
+  return oracle_attn_fwd_dropout_f32_range(O, lse, Q, K, V, 0, BH, S, D, scale, p, seed);
+}
+
+int oracle_attn_bwd_dropout_f32(float* dQ, float* dK, float* dV, float* delta, const float* dO,
+                                const float* O, const float* Q, const float* K, const float* V,
+                                int BH, int S, int D, float scale, float p, uint64_t seed) {
+  drop_t dr;
+  if (drop_params(&dr, p, seed)) return -3;
+  if (delta) oracle_attn_delta_f32(delta, dO, O, (long)BH * S, D);
+  const size_t ss = (size_t)S * S;
+  float* P = (float*)malloc(sizeof(float) * 4 * ss + ss);
+  if (!P) return -1;
+  float *Pd = P + ss, *dP = P + 2 * ss, *dS = P + 3 * ss;
+  uint8_t* keep = (uint8_t*)(P + 4 * ss);
+  for (int bh = 0; bh < BH; ++bh) {
+    const long o = (long)bh * S * D;
+    probs_slice_f32(NULL, Q + o, K + o, S, D, scale, P);
+    dropout_slice_f32(Pd, keep, P, S, bh, &dr);
+    mm_bt_f32(dP, dO + o, V + o, S, D, S);
+    mm_at_f32(dV + o, Pd, dO + o, S, S, D);
+    for (size_t n = 0; n < ss; ++n) dP[n] *= (float)keep[n] * dr.scale;
+    memset(dS, 0, sizeof(float) * ss);
+    softmax_bwd_rows_f32(dP, P, dS, S, S);
+    causal_zero_f32(dS, S);
+    scale_f32(dS, (long)ss, scale);
+    mm_f32(dQ + o, dS, K + o, S, S, D);
+    mm_at_f32(dK + o, dS, Q + o, S, S, D);
+  }
+  free(P);
+  return 0;
 }
 
 /* ---- decode ---- */
@@ -293,6 +441,85 @@ int oracle_attn_bwd_f64(double* dQ, double* dK, double* dV, const double* dO, co
         double av = 0.0, ak = 0.0;
         for (int i = 0; i < S; ++i) {
           av += P[(long)i * S + j] * g[(long)i * D + d];
+          ak += dS[(long)i * S + j] * q[(long)i * D + d];
+        }
+        dV[o + (long)j * D + d] = av;
+        dK[o + (long)j * D + d] = ak;
+      }
+    for (int i = 0; i < S; ++i)
+      for (int d = 0; d < D; ++d) {
+        double aq = 0.0;
+        for (int j = 0; j < S; ++j) aq += dS[(long)i * S + j] * k[(long)j * D + d];
+        dQ[o + (long)i * D + d] = aq;
+      }
+  }
+  free(P);
+  return 0;
+}
+
+/* Double-precision twins with dropout (the same keep bits; 1/(1-p) in double): forward
+ * O = Pd V with Pd = keep * P / (1-p); backward dV = Pd^T dO, dP = keep * (dO V^T) / (1-p),
+ * dS = P (dP - rowsum(P dP)) * scale, dQ = dS K, dK = dS^T Q. */
+int oracle_attn_fwd_dropout_f64(double* O, double* lse, const double* Q, const double* K,
+                                const double* V, int BH, int S, int D, double scale, float p,
+                                uint64_t seed) {
+  drop_t dr;
+  if (drop_params(&dr, p, seed)) return -3;
+  const double inv = 1.0 / (1.0 - (double)p);
+  double* P = (double*)malloc(sizeof(double) * ((size_t)S * S + (size_t)S * D));
+  if (!P) return -1;
+  double* Ot = P + (size_t)S * S;
+  for (int bh = 0; bh < BH; ++bh) {
+    const long o = (long)bh * S * D;
+    fwd_slice_f64(Ot, lse ? lse + (long)bh * S : NULL, Q + o, K + o, V + o, S, D, scale, P);
+    for (int i = 0; i < S; ++i)
+      for (int d = 0; d < D; ++d) {
+        double acc = 0.0;
+        for (int j = 0; j <= i; ++j)
+          if (oracle_dropout_keep(seed, (uint64_t)bh * S + i, j, dr.thr))
+            acc += P[(long)i * S + j] * inv * V[o + (long)j * D + d];
+        O[o + (long)i * D + d] = acc;
+      }
+  }
+  free(P);
+  return 0;
+}
+
+int oracle_attn_bwd_dropout_f64(double* dQ, double* dK, double* dV, const double* dO,
+                                const double* Q, const double* K, const double* V, int BH,
+                                int S, int D, double scale, float p, uint64_t seed) {
+  drop_t dr;
+  if (drop_params(&dr, p, seed)) return -3;
+  const double inv = 1.0 / (1.0 - (double)p);
+  const size_t ss = (size_t)S * S;
+  double* P = (double*)malloc(sizeof(double) * (3 * ss + (size_t)S * D));
+  if (!P) return -1;
+  double *Pd = P + ss, *dS = P + 2 * ss, *Ot = P + 3 * ss;
+  for (int bh = 0; bh < BH; ++bh) {
+    const long o = (long)bh * S * D;
+    const double *q = Q + o, *k = K + o, *v = V + o, *g = dO + o;
+    fwd_slice_f64(Ot, NULL, q, k, v, S, D, scale, P);
+    for (int i = 0; i < S; ++i) {
+      double dot = 0.0;
+      for (int j = 0; j < S; ++j) {
+        const long n = (long)i * S + j;
+        const int kp = j <= i && oracle_dropout_keep(seed, (uint64_t)bh * S + i, j, dr.thr);
+        Pd[n] = kp ? P[n] * inv : 0.0;
+        double dp = 0.0;
+        for (int t = 0; t < D; ++t) dp += g[(long)i * D + t] * v[(long)j * D + t];
+        dS[n] = kp ? dp * inv : 0.0; /* dP */
+        dot += dS[n] * P[n];
+      }
+      for (int j = 0; j < S; ++j) {
+        const long n = (long)i * S + j;
+        dS[n] = j <= i ? P[n] * (dS[n] - dot) * scale : 0.0;
+      }
+    }
+    for (int j = 0; j < S; ++j)
+      for (int d = 0; d < D; ++d) {
+        double av = 0.0, ak = 0.0;
+        for (int i = 0; i < S; ++i) {
+          av += Pd[(long)i * S + j] * g[(long)i * D + d];
           ak += dS[(long)i * S + j] * q[(long)i * D + d];
         }
         dV[o + (long)j * D + d] = av;

@@ -12,10 +12,13 @@
  * gpu_causal_mask_zero (cuda/gpu_ops.cu:476-503). Each function below cites the reference
  * lines it follows. Layout everywhere: [BH, S, D] row-major, lse [BH, S].
  *
- * Parity pinning (which check pins which function) is listed in oracle/README.md.
+ * Which check pins which function: tests/test_oracle.py and tests/pins.py (golden vectors from
+ * the reference's own operators, closed forms, invariants, finite differences).
  */
 #ifndef DADGPT_ATTN_ORACLE_H
 #define DADGPT_ATTN_ORACLE_H
+
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -48,6 +51,37 @@ void oracle_attn_delta_f32(float* delta, const float* dO, const float* O, long r
  * out [n_seq,H,D]. */
 int oracle_decode_f32(float* out, const float* q, const float* k_cache, const float* v_cache,
                       const int* lens, int n_seq, int H, int max_len, int D, float scale);
+
+/* Attention-probability dropout (the reference: cuda/gpu_ops.cu:712-749, applied at
+ * src/model.cpp:406-416 and :591-596). The reference draws its mask from cuRAND, whose
+ * stream is not reproduced; this build's mask is Philox4x32-10 as published (Salmon et al.,
+ * SC'11): probability (row = bh*S + i, key j) is kept iff (w >> 8) >= ceil(p * 2^24), w =
+ * word j%4 of Philox4x32-10(counter {row lo, row hi, j/4, 0}, key {seed lo, seed hi}).
+ * Kept probabilities are scaled by 1/(1-p) (fp32), as the reference does. p in [0, 1). */
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+uint32_t oracle_dropout_threshold(float p);
+int oracle_dropout_keep(uint64_t seed, uint64_t row, int j, uint32_t thr);
+/* keep bits [BH, S, S] (1 = kept) */
+void oracle_dropout_mask(uint8_t* mask, int BH, int S, uint64_t seed, float p);
+/* Forward / backward with dropout, fp32, the materialized op order with dropout
+ * (src/model.cpp:396-419 with :406-416, :585-615 with :591-596). lse is that of the undropped
+ * scores; delta (when non-NULL) is rowsum(dO * O). Return -3 for p outside [0, 1). */
+int oracle_attn_fwd_dropout_f32(float* O, float* lse, const float* Q, const float* K,
+                                const float* V, int BH, int S, int D, float scale, float p,
+                                uint64_t seed);
+/* The forward over bh slices [bh0, bh1) only (rows keep their global index bh*S + i). */
+int oracle_attn_fwd_dropout_f32_range(float* O, float* lse, const float* Q, const float* K,
+                                      const float* V, int bh0, int bh1, int S, int D,
+                                      float scale, float p, uint64_t seed);
+int oracle_attn_bwd_dropout_f32(float* dQ, float* dK, float* dV, float* delta, const float* dO,
+                                const float* O, const float* Q, const float* K, const float* V,
+                                int BH, int S, int D, float scale, float p, uint64_t seed);
+int oracle_attn_fwd_dropout_f64(double* O, double* lse, const double* Q, const double* K,
+                                const double* V, int BH, int S, int D, double scale, float p,
+                                uint64_t seed);
+int oracle_attn_bwd_dropout_f64(double* dQ, double* dK, double* dV, const double* dO,
+                                const double* Q, const double* K, const double* V, int BH,
+                                int S, int D, double scale, float p, uint64_t seed);
 
 /* Double-precision twins (tie-breakers and brute-force checks). */
 int oracle_attn_fwd_f64(double* O, double* lse, const double* Q, const double* K,

@@ -189,3 +189,91 @@ def check_dec_library(dec, seed=33):
 
 
 DEC_CHECKS = (check_dec_len1, check_dec_library)
+
+
+# ------------------------------------------------------------------------- dropout pins
+# Implementations with attention-probability dropout take (p, seed) after the scale:
+#   fwd_d(q, k, v, scale, p, seed) -> (O, lse); bwd_d(dout, q, k, v, scale, p, seed) -> grads
+# and keep(BH, S, seed, p) -> keep bits [BH, S, S] (the mask definition, pinned separately by
+# the Philox known-answer vectors). The undropped fwd/bwd are the pinned ones above.
+
+def _drop_reference_f64(q, k, v, scale, keep, p, dout=None):
+    """torch float64 on the CPU: O = (causal softmax(QK^T * scale) * keep / (1-p)) V, and with
+    dout its autograd gradients (the mask is a constant)."""
+    req = dout is not None
+    tq, tk, tv = (torch.tensor(np.asarray(x, np.float64), requires_grad=req) for x in (q, k, v))
+    S = tq.shape[1]
+    s = torch.matmul(tq, tk.transpose(1, 2).contiguous()) * float(scale)
+    s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+    pr = torch.softmax(s, dim=-1) * torch.tensor(keep, dtype=torch.float64) / (1.0 - float(p))
+    o = torch.matmul(pr, tv)
+    grads = None
+    if req:
+        o.backward(torch.tensor(np.asarray(dout, np.float64)))
+        grads = (tq.grad.numpy(), tk.grad.numpy(), tv.grad.numpy())
+    return o.detach().numpy(), grads
+
+
+def check_drop_p0_identity(fwd_d, bwd_d, fwd, bwd, BH=2, S=37, D=32, seed=41):
+    """p = 0 keeps everything with factor 1: the undropped results."""
+    q, k, v, g = synth.attn_inputs(BH, S, D, seed=seed, with_dout=True)
+    scale = 1.0 / np.sqrt(D)
+    (o, l), (ro, rl) = fwd_d(q, k, v, scale, 0.0, 7), fwd(q, k, v, scale)
+    e = [_max_abs(o, ro), _max_abs(l, rl)]
+    e += [_max_abs(a, b) for a, b in zip(bwd_d(g, q, k, v, scale, 0.0, 7), bwd(g, q, k, v, scale))]
+    return max(e) <= 1e-6, "p=0 vs undropped err " + ", ".join(f"{x:.2e}" for x in e)
+
+
+def check_drop_lse_undropped(fwd_d, fwd, BH=2, S=40, D=32, seed=42):
+    """The saved logsumexp is that of the undropped scores (the backward recomputes P)."""
+    q, k, v = synth.attn_inputs(BH, S, D, seed=seed)
+    scale = 1.0 / np.sqrt(D)
+    e = _max_abs(fwd_d(q, k, v, scale, 0.4, 3)[1], fwd(q, k, v, scale)[1])
+    return e <= 1e-5, f"lse with dropout vs without err {e:.2e}"
+
+
+def check_drop_library(fwd_d, keep, BH=2, S=45, D=32, seed=43, p=0.3, dseed=1234):
+    q, k, v = synth.attn_inputs(BH, S, D, seed=seed)
+    scale = 1.0 / np.sqrt(D)
+    ro, _ = _drop_reference_f64(q, k, v, scale, keep(BH, S, dseed, p), p)
+    e = _max_abs(fwd_d(q, k, v, scale, p, dseed)[0], ro)
+    return e <= 1e-5, f"O with dropout vs library err {e:.2e}"
+
+
+def check_drop_bwd_library(bwd_d, keep, BH=2, S=33, D=32, seed=44, p=0.3, dseed=99):
+    q, k, v, g = synth.attn_inputs(BH, S, D, seed=seed, with_dout=True)
+    scale = 1.0 / np.sqrt(D)
+    _, ref = _drop_reference_f64(q, k, v, scale, keep(BH, S, dseed, p), p, dout=g)
+    e = [_max_abs(a, b) for a, b in zip(bwd_d(g, q, k, v, scale, p, dseed), ref)]
+    return max(e) <= 1e-4, "dQ/dK/dV with dropout err " + ", ".join(f"{x:.2e}" for x in e)
+
+
+def check_drop_unbiased(fwd_d, fwd, BH=1, S=24, D=16, seed=45, p=0.25, n=300):
+    """E[keep / (1-p)] = 1 (p = 0.25 is exactly representable as a 24-bit threshold), so the
+    mean output over seeds tends to the undropped output: within 6 standard errors."""
+    q, k, v = synth.attn_inputs(BH, S, D, seed=seed)
+    scale = 1.0 / np.sqrt(D)
+    outs = np.stack([np.asarray(fwd_d(q, k, v, scale, p, 1000 + i)[0], np.float64)
+                     for i in range(n)])
+    ro = np.asarray(fwd(q, k, v, scale)[0], np.float64)
+    se = outs.std(0) / np.sqrt(n)
+    z = np.abs(outs.mean(0) - ro) / np.maximum(se, 1e-12)
+    return float(z.max()) <= 6.0, f"max |mean - undropped| / std.err {float(z.max()):.2f}"
+
+
+def check_drop_bwd_fd(fwd64_d, bwd64_d, BH=1, S=6, D=4, seed=46, p=0.3, dseed=5, h=1e-6):
+    """Central finite differences of L = sum(O * dO) at a fixed mask."""
+    q, k, v, g = (x.astype(np.float64) for x in
+                  synth.attn_inputs(BH, S, D, seed=seed, with_dout=True))
+    scale = 0.7
+    grads = bwd64_d(g, q, k, v, scale, p, dseed)
+    worst = 0.0
+    for which, grad in enumerate(grads):
+        for idx in np.ndindex(q.shape):
+            args = [q.copy(), k.copy(), v.copy()]
+            args[which][idx] += h
+            lp = float(np.sum(fwd64_d(*args, scale, p, dseed)[0] * g))
+            args[which][idx] -= 2 * h
+            lm = float(np.sum(fwd64_d(*args, scale, p, dseed)[0] * g))
+            worst = max(worst, abs((lp - lm) / (2 * h) - float(grad[idx])))
+    return worst <= 1e-6, f"finite-difference err {worst:.2e}"

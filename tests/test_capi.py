@@ -145,6 +145,19 @@ def test_tokens_validation():
     assert bwd(*args(d=40)) == 2
 
 
+def test_dropout_validation():
+    L = A.lib()
+    fwd, bwd = (L.dadgpt_flash_attention_forward_bf16_dropout,
+                L.dadgpt_flash_attention_backward_bf16_dropout)
+    for p in (1.0, -0.01, float("nan"), float("inf"), 1.5):
+        assert fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 64, 0.125, p, 7, None) == 1
+        assert "dropout_p" in A.last_error()
+        assert bwd(*[FAKE] * 10, 4, 64, 64, 0.125, p, 7, None) == 1
+    assert fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 48, 0.125, 0.1, 7, None) == 2
+    assert fwd(None, FAKE, FAKE, FAKE, FAKE, 4, 64, 64, 0.125, 0.1, 7, None) == 1
+    assert bwd(*[FAKE] * 10, 4, 0, 64, 0.125, 0.1, 7, None) == 1
+
+
 def expected_ws(n, h, max_len, d):
     """One uint32 arrival counter per (sequence, head), the region padded to 256 bytes, then
     fp32 partials (max, sum, o[d]) per chunk, when the cache needs more than one chunk. fp32

@@ -136,3 +136,99 @@ def test_oracle_threaded_equals_serial():
     b = oracle.attn_bwd(g, q, k, v, 0.2, threads=4)[:3]
     for x, y in zip(a, b):
         assert np.array_equal(x, y)
+
+
+# ---- attention-probability dropout ----
+
+# Published known-answer vectors of Philox4x32-10 (Random123's kat_vectors, "philox4x32 10"
+# lines): (counter, key) -> output.
+PHILOX_KAT = [
+    ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF,) * 4, (0xFFFFFFFF,) * 2, (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+]
+
+
+@pytest.mark.parametrize("ctr,key,expect", PHILOX_KAT)
+def test_philox_known_answers(ctr, key, expect):
+    assert [int(x) for x in oracle.philox4x32_10(ctr, key)] == list(expect)
+
+
+def test_dropout_mask_definition():
+    """Keep bit of (row, j) = word j%4 of Philox at counter {row lo, row hi, j/4, 0}, key
+    {seed lo, seed hi}, compared as a 24-bit uniform; spot-checked against the block
+    function itself."""
+    seed, p, BH, S = 0x1234_5678_9ABC_DEF0, 0.3, 3, 37
+    m = oracle.dropout_mask(BH, S, seed, p)
+    thr = oracle.dropout_threshold(p)
+    assert thr == int(np.ceil(np.float32(p) * 2.0 ** 24))
+    rng = np.random.default_rng(0)
+    for _ in range(50):
+        bh, i, j = int(rng.integers(BH)), int(rng.integers(S)), int(rng.integers(S))
+        row = bh * S + i
+        w = oracle.philox4x32_10((row & 0xFFFFFFFF, row >> 32, j >> 2, 0),
+                                 (seed & 0xFFFFFFFF, seed >> 32))
+        assert m[bh, i, j] == int((int(w[j & 3]) >> 8) >= thr)
+
+
+@pytest.mark.parametrize("p", [0.0, 0.1, 0.5, 0.9])
+def test_dropout_mask_rate(p):
+    m = oracle.dropout_mask(8, 256, 77, p)
+    keep = 1.0 - oracle.dropout_threshold(p) / 2.0 ** 24
+    n = m.size
+    sigma = np.sqrt(max(keep * (1 - keep), 1e-12) / n)
+    assert abs(m.mean() - keep) <= 5 * sigma + 1e-12
+    if p == 0.0:
+        assert m.all()
+    # rows and columns are not correlated with position: halves agree to 5 sigma
+    assert abs(m[:, :, :128].mean() - m[:, :, 128:].mean()) <= 10 * sigma + 1e-12
+
+
+def _fwd_d32(q, k, v, scale, p, seed):
+    return oracle.attn_fwd_dropout(q, k, v, float(scale), p, seed)
+
+
+def _bwd_d32(g, q, k, v, scale, p, seed):
+    return oracle.attn_bwd_dropout(g, q, k, v, float(scale), p, seed)[:3]
+
+
+def test_oracle_dropout_pins():
+    for ok, detail in (
+            pins.check_drop_p0_identity(_fwd_d32, _bwd_d32, _fwd32, _bwd32),
+            pins.check_drop_lse_undropped(_fwd_d32, _fwd32),
+            pins.check_drop_library(_fwd_d32, oracle.dropout_mask),
+            pins.check_drop_bwd_library(_bwd_d32, oracle.dropout_mask),
+            pins.check_drop_unbiased(_fwd_d32, _fwd32)):
+        assert ok, detail
+
+
+def test_oracle_dropout_p0_is_bitwise_undropped():
+    q, k, v, g = synth.attn_inputs(3, 50, 32, seed=8, with_dout=True)
+    o, lse = oracle.attn_fwd(q, k, v, 0.17)
+    od, ld = oracle.attn_fwd_dropout(q, k, v, 0.17, 0.0, 11)
+    assert np.array_equal(o, od) and np.array_equal(lse, ld)
+    a = oracle.attn_bwd(g, q, k, v, 0.17, out=o)
+    b = oracle.attn_bwd_dropout(g, q, k, v, 0.17, 0.0, 11, out=o)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+
+
+def test_oracle_dropout_f64_finite_differences_and_twin():
+    ok, detail = pins.check_drop_bwd_fd(oracle.attn_fwd_dropout_f64, oracle.attn_bwd_dropout_f64)
+    assert ok, detail
+    q, k, v, g = synth.attn_inputs(3, 48, 32, seed=9, with_dout=True)
+    s = 1 / np.sqrt(32)
+    o, lse = oracle.attn_fwd_dropout(q, k, v, s, 0.2, 21)
+    o64, l64 = oracle.attn_fwd_dropout_f64(q, k, v, s, 0.2, 21)
+    assert np.max(np.abs(o - o64)) < 1e-5 and np.max(np.abs(lse - l64)) < 1e-5
+    for a, b in zip(oracle.attn_bwd_dropout(g, q, k, v, s, 0.2, 21)[:3],
+                    oracle.attn_bwd_dropout_f64(g, q, k, v, s, 0.2, 21)):
+        assert np.max(np.abs(a - b)) < 1e-5
+
+
+def test_oracle_dropout_rejects_bad_rate():
+    q, k, v = synth.attn_inputs(1, 8, 32, seed=1)
+    for p in (1.0, -0.1, float("nan")):
+        with pytest.raises(RuntimeError):
+            oracle.attn_fwd_dropout(q, k, v, 0.1, p, 1)

@@ -130,3 +130,91 @@ def test_decode_mistake_is_caught(bug):
     with np.errstate(all="ignore"):
         failed, results = _fails_some(pins.DEC_CHECKS, _dec_factory(bug))
     assert failed, f"planted decode mistake {bug!r} passed every pin: {results}"
+
+
+# ---- dropout: a float64 stand-in with the mask of oracle.dropout_mask ----
+
+def _keep(BH, S, seed, p):
+    import oracle
+    return oracle.dropout_mask(BH, S, seed, p).astype(np.float64)
+
+
+def _drop_fwd_factory(bug=None):
+    def fwd(q, k, v, scale, p, seed):
+        q, k, v = (np.asarray(x, np.float64) for x in (q, k, v))
+        BH, S, _ = q.shape
+        s = np.einsum("bid,bjd->bij", q, k) * scale
+        s = np.where(np.tril(np.ones((S, S), bool))[None], s, -np.inf)
+        keep = _keep(BH, S, seed, p)
+        if bug == "mask_before_softmax":  # drops scores and renormalises over the kept ones
+            s = np.where(keep > 0, s, -np.inf)
+        m = s.max(-1, keepdims=True)
+        e = np.exp(s - m)
+        lse = (np.log(e.sum(-1, keepdims=True)) + m)[..., 0]
+        pr = e / e.sum(-1, keepdims=True)
+        pd = pr * keep / (1.0 if bug == "no_rescale" else 1.0 - p)
+        if bug == "lse_of_kept":
+            lse = np.log(np.where(keep > 0, e, 0).sum(-1) + 1e-300) + m[..., 0]
+        return np.einsum("bij,bjd->bid", pd, v), lse
+    return fwd
+
+
+def _drop_bwd_factory(bug=None):
+    def bwd(g, q, k, v, scale, p, seed):
+        g, q, k, v = (np.asarray(x, np.float64) for x in (g, q, k, v))
+        BH, S, _ = q.shape
+        s = np.einsum("bid,bjd->bij", q, k) * scale
+        vis = np.tril(np.ones((S, S), bool))[None]
+        s = np.where(vis, s, -np.inf)
+        pr = np.exp(s - s.max(-1, keepdims=True))
+        pr = pr / pr.sum(-1, keepdims=True)
+        keep = _keep(BH, S, seed, p)
+        f = keep / (1.0 - p)
+        pd = pr * f
+        dpd = np.einsum("bid,bjd->bij", g, v)
+        dv = np.einsum("bij,bid->bjd", pr if bug == "dv_undropped" else pd, g)
+        dp = dpd if bug == "dp_unmasked" else dpd * f
+        if bug == "dp_scaled_twice":
+            dp = dp / (1.0 - p)
+        delta = (pr * dp).sum(-1, keepdims=True)
+        if bug == "delta_undropped":
+            delta = (pr * dpd).sum(-1, keepdims=True)
+        ds = pr * (dp - delta) * scale
+        return np.einsum("bij,bjd->bid", ds, k), np.einsum("bij,bid->bjd", ds, q), dv
+    return bwd
+
+
+def _drop_fwd_checks(fwd_d):
+    return [pins.check_drop_p0_identity(fwd_d, _drop_bwd_factory(), _fwd_factory(),
+                                        _bwd_factory()),
+            pins.check_drop_lse_undropped(fwd_d, _fwd_factory()),
+            pins.check_drop_library(fwd_d, _keep),
+            pins.check_drop_unbiased(fwd_d, _fwd_factory(), n=200)]
+
+
+def _drop_bwd_checks(bwd_d):
+    return [pins.check_drop_p0_identity(_drop_fwd_factory(), bwd_d, _fwd_factory(),
+                                        _bwd_factory()),
+            pins.check_drop_bwd_library(bwd_d, _keep),
+            pins.check_drop_bwd_fd(_drop_fwd_factory(), bwd_d)]
+
+
+def test_unmodified_dropout_stand_in_passes_every_pin():
+    for ok, detail in _drop_fwd_checks(_drop_fwd_factory()) + _drop_bwd_checks(
+            _drop_bwd_factory()):
+        assert ok, detail
+
+
+@pytest.mark.parametrize("bug", ["mask_before_softmax", "no_rescale", "lse_of_kept"])
+def test_dropout_forward_mistake_is_caught(bug):
+    with np.errstate(all="ignore"):
+        results = _drop_fwd_checks(_drop_fwd_factory(bug))
+    assert [r for r in results if not r[0]], f"dropout mistake {bug!r} passed: {results}"
+
+
+@pytest.mark.parametrize("bug", ["dv_undropped", "dp_unmasked", "dp_scaled_twice",
+                                 "delta_undropped"])
+def test_dropout_backward_mistake_is_caught(bug):
+    with np.errstate(all="ignore"):
+        results = _drop_bwd_checks(_drop_bwd_factory(bug))
+    assert [r for r in results if not r[0]], f"dropout mistake {bug!r} passed: {results}"
