@@ -95,7 +95,7 @@ int dadgpt_flash_attention_backward_bf16(uint16_t* dq, uint16_t* dk, uint16_t* d
 
 /* ---- Attention-probability dropout (replaces the reference's materialized path with
  * dropout: gpu_dropout_forward on P before P V, src/model.cpp:406-416, and
- * gpu_dropout_backward on dP, :591-596; kernels cuda/gpu_ops.cu:712-749). Fused into the
+ * gpu_dropout_backward on dP, :594-599; kernels cuda/gpu_ops.cu:712-749). Fused into the
  * flash kernels: the keep bits are regenerated in the backward, no mask is stored. Kept
  * probabilities are scaled by 1/(1-p) (fp32), as the reference does; lse stays that of the
  * undropped scores. The mask is not cuRAND's: probability (row = bh*S + i, key j) is kept

@@ -277,7 +277,7 @@ int oracle_attn_bwd_f32(float* dQ, float* dK, float* dV, float* delta, const flo
 
 /* ---- forward and backward with attention-probability dropout ----
  * Op order of the materialized path with dropout (src/model.cpp:396-419 with :406-416;
- * :585-615 with :591-596): forward S = QK^T, *scale, mask, softmax -> P; Pd = dropout(P);
+ * :585-615 with :594-599): forward S = QK^T, *scale, mask, softmax -> P; Pd = dropout(P);
  * O = Pd V. Backward dPd = dO V^T; dV = Pd^T dO; dP = dPd * (keep * 1/(1-p))
  * (gpu_dropout_backward, cuda/gpu_ops.cu:736-741); dS = softmax_bwd(dP, P); zero j>i;
  * *scale; dQ = dS K; dK = dS^T Q. lse is that of the undropped scores. */

@@ -53,7 +53,7 @@ int oracle_decode_f32(float* out, const float* q, const float* k_cache, const fl
                       const int* lens, int n_seq, int H, int max_len, int D, float scale);
 
 /* Attention-probability dropout (the reference: cuda/gpu_ops.cu:712-749, applied at
- * src/model.cpp:406-416 and :591-596). The reference draws its mask from cuRAND, whose
+ * src/model.cpp:406-416 and :594-599). The reference draws its mask from cuRAND, whose
  * stream is not reproduced; this build's mask is Philox4x32-10 as published (Salmon et al.,
  * SC'11): probability (row = bh*S + i, key j) is kept iff (w >> 8) >= ceil(p * 2^24), w =
  * word j%4 of Philox4x32-10(counter {row lo, row hi, j/4, 0}, key {seed lo, seed hi}).
@@ -64,7 +64,7 @@ int oracle_dropout_keep(uint64_t seed, uint64_t row, int j, uint32_t thr);
 /* keep bits [BH, S, S] (1 = kept) */
 void oracle_dropout_mask(uint8_t* mask, int BH, int S, uint64_t seed, float p);
 /* Forward / backward with dropout, fp32, the materialized op order with dropout
- * (src/model.cpp:396-419 with :406-416, :585-615 with :591-596). lse is that of the undropped
+ * (src/model.cpp:396-419 with :406-416, :585-615 with :594-599). lse is that of the undropped
  * scores; delta (when non-NULL) is rowsum(dO * O). Return -3 for p outside [0, 1). */
 int oracle_attn_fwd_dropout_f32(float* O, float* lse, const float* Q, const float* K,
                                 const float* V, int BH, int S, int D, float scale, float p,
