@@ -36,6 +36,8 @@ C_SYMBOLS = (
     "dadgpt_flash_attention_backward_bf16_phase",
     "dadgpt_flash_attention_forward_bf16_dropout",
     "dadgpt_flash_attention_backward_bf16_dropout",
+    "dadgpt_flash_attention_forward_dropout",
+    "dadgpt_flash_attention_backward_dropout",
     "dadgpt_flash_attention_forward_bf16_strided",
     "dadgpt_flash_attention_backward_bf16_strided",
     "dadgpt_flash_attention_forward_bf16_tokens",
@@ -103,6 +105,8 @@ def lib():
     L.dadgpt_flash_attention_forward_bf16_dropout.argtypes = [vp] * 5 + [i, i, i, f, f, u64, vp]
     L.dadgpt_flash_attention_backward_bf16_dropout.argtypes = [vp] * 10 + [i, i, i, f, f, u64,
                                                                           vp]
+    L.dadgpt_flash_attention_forward_dropout.argtypes = [vp] * 5 + [i, i, i, f, f, u64, vp]
+    L.dadgpt_flash_attention_backward_dropout.argtypes = [vp] * 10 + [i, i, i, f, f, u64, vp]
     i64, hs = ctypes.c_int64, ctypes.POINTER(HeadStrides)
     L.dadgpt_flash_attention_forward_bf16_strided.argtypes = [vp] * 5 + [i, i, i, i, f, hs, vp]
     L.dadgpt_flash_attention_backward_bf16_strided.argtypes = [vp] * 10 + [i, i, i, i, f, hs,
@@ -213,6 +217,35 @@ def flash_attention_backward_bf16(dq, dk, dv, delta, dout, out, lse, q, k, v, BH
     _check(lib().dadgpt_flash_attention_backward_bf16(
         _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta), _ptr(dout), _ptr(out), _ptr(lse), _ptr(q),
         _ptr(k), _ptr(v), BH, S, d_head, scale, _stream_ptr(stream)))
+
+
+def flash_attention_forward_dropout(out, lse, q, k, v, BH: int, S: int, d_head: int,
+                                    scale: float, dropout_p: float, seed: int,
+                                    stream=None) -> None:
+    """fp32 forward with attention-probability dropout (the reference's precision)."""
+    n = BH * S * d_head
+    for t, nm in ((out, "out"), (q, "q"), (k, "k"), (v, "v")):
+        _require(t, nm, torch.float32, n)
+    _require(lse, "lse", torch.float32, BH * S)
+    _check(lib().dadgpt_flash_attention_forward_dropout(
+        _ptr(out), _ptr(lse), _ptr(q), _ptr(k), _ptr(v), BH, S, d_head, scale, dropout_p,
+        seed & 0xFFFFFFFFFFFFFFFF, _stream_ptr(stream)))
+
+
+def flash_attention_backward_dropout(dq, dk, dv, delta, dout, out, lse, q, k, v, BH: int,
+                                     S: int, d_head: int, scale: float, dropout_p: float,
+                                     seed: int, stream=None) -> None:
+    """fp32 backward of flash_attention_forward_dropout with the same (dropout_p, seed)."""
+    n = BH * S * d_head
+    for t, nm in ((dq, "dq"), (dk, "dk"), (dv, "dv"), (dout, "dout"), (out, "out"),
+                  (q, "q"), (k, "k"), (v, "v")):
+        _require(t, nm, torch.float32, n)
+    _require(delta, "delta", torch.float32, BH * S)
+    _require(lse, "lse", torch.float32, BH * S)
+    _check(lib().dadgpt_flash_attention_backward_dropout(
+        _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta), _ptr(dout), _ptr(out), _ptr(lse), _ptr(q),
+        _ptr(k), _ptr(v), BH, S, d_head, scale, dropout_p, seed & 0xFFFFFFFFFFFFFFFF,
+        _stream_ptr(stream)))
 
 
 def flash_attention_forward_bf16_dropout(out, lse, q, k, v, BH: int, S: int, d_head: int,

@@ -1,11 +1,13 @@
 // fp32 causal flash attention (the reference's precision, cuda/attention.cu:1): forward with
 // online softmax and saved natural-log logsumexp, backward recomputing P from it. Accurate
-// expf/logf, fp32 FMA; the result matches the fp32 CPU path to ~1e-6.
+// expf/logf, fp32 FMA; the result matches the fp32 CPU path to ~1e-6. The DROP instantiations
+// add attention-probability dropout with the keep bits of dropout.hpp.
 //
 // gfx950 has no fp32 MFMA rate worth the layout work at this precision's use (tests, greedy
 // parity), so these are SIMT kernels: one lane per query row (forward, dQ) or key row
 // (dK/dV), 64-row tiles of the other operand staged in LDS and read as broadcast float4.
 #include "common.hpp"
+#include "dropout.hpp"
 #include "kernels.hpp"
 
 namespace dadgpt {
@@ -40,13 +42,13 @@ __device__ __forceinline__ float dot_row(const float* a, const float (*tile)[D],
   return acc;
 }
 
-template <int D>
+template <int D, bool DROP>
 __global__ __launch_bounds__(kT) void fwd_f32_kernel(float* __restrict__ out,
                                                      float* __restrict__ lse,
                                                      const float* __restrict__ q,
                                                      const float* __restrict__ k,
                                                      const float* __restrict__ v, int S,
-                                                     float scale) {
+                                                     float scale, const DropParams dr) {
   __shared__ __attribute__((aligned(16))) float sk[kT][D];
   __shared__ __attribute__((aligned(16))) float sv[kT][D];
   const int bh = blockIdx.x;
@@ -71,6 +73,12 @@ __global__ __launch_bounds__(kT) void fwd_f32_kernel(float* __restrict__ out,
     if (!valid) continue;
     const int nj = min(kT, row - k0 + 1);  // keys k0 .. row are visible
     if (nj <= 0) continue;
+    uint64_t keep = 0;  // keep bits of keys k0 .. k0+63 of this row
+    if constexpr (DROP) {
+#pragma unroll 1
+      for (int j4 = 0; j4 < nj; j4 += 4)
+        keep |= (uint64_t)keep4(dr, (uint64_t)bh * S + row, (uint32_t)(k0 + j4) >> 2) << j4;
+    }
     float s[kT];
     float mx = neg_inf();
 #pragma unroll
@@ -87,9 +95,11 @@ __global__ __launch_bounds__(kT) void fwd_f32_kernel(float* __restrict__ out,
     for (int j = 0; j < kT; ++j) {
       if (j < nj) {
         const float p = expf(s[j] - mnew);
-        l += p;
+        l += p;  // the normaliser of the undropped row
+        float pv = p;
+        if constexpr (DROP) pv = p * ((keep >> j) & 1u ? dr.scale : 0.0f);
 #pragma unroll
-        for (int d = 0; d < D; ++d) o[d] = fmaf(p, sv[j][d], o[d]);
+        for (int d = 0; d < D; ++d) o[d] = fmaf(pv, sv[j][d], o[d]);
       }
     }
     m = mnew;
@@ -114,11 +124,13 @@ __global__ __launch_bounds__(256) void delta_f32_kernel(float* __restrict__ delt
 }
 
 // One lane per key j: dV_j = sum_{r>=j} P_rj dO_r, dK_j = scale * sum_{r>=j} dS_rj Q_r.
-template <int D>
+// With dropout: dV_j = sum_r P_rj f_rj dO_r and dS_rj = P_rj (dP_rj f_rj - delta_r), f = keep/(1-p).
+template <int D, bool DROP>
 __global__ __launch_bounds__(kT) void dkdv_f32_kernel(
     float* __restrict__ dk, float* __restrict__ dv, const float* __restrict__ q,
     const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, int S, float scale) {
+    const float* __restrict__ lse, const float* __restrict__ delta, int S, float scale,
+    const DropParams dr) {
   __shared__ __attribute__((aligned(16))) float sq[kT][D];
   __shared__ __attribute__((aligned(16))) float sdo[kT][D];
   __shared__ float slse[kT], sdel[kT];
@@ -144,6 +156,26 @@ __global__ __launch_bounds__(kT) void dkdv_f32_kernel(
       sdel[threadIdx.x] = r < S ? delta[(size_t)bh * S + r] : 0.f;
     }
     __syncthreads();
+    // keep bits of this lane's key for the tile's 64 rows (every lane, before any exits: the
+    // bits of 4 rows come from one Philox block per lane of a 4-lane quad, then an exchange)
+    uint64_t keep = 0;
+    if constexpr (DROP) {
+      const int t = threadIdx.x & 3;
+      const uint32_t j4 = (uint32_t)(blk * kT + (threadIdx.x & ~3)) >> 2;
+#pragma unroll 1
+      for (int i4 = 0; i4 < kT; i4 += 4) {
+        const uint64_t row = (uint64_t)bh * S + r0 + i4 + t;
+        const u32x4 w = philox4x32_10((uint32_t)row, (uint32_t)(row >> 32), j4, 0u, dr.k0,
+                                      dr.k1);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const int c = t ^ d;
+          const uint32_t send = c == 0 ? w[0] : c == 1 ? w[1] : c == 2 ? w[2] : w[3];
+          const uint32_t got = d == 0 ? send : (uint32_t)__shfl_xor((int)send, d, 64);
+          keep |= (uint64_t)((got >> 8) >= dr.thr) << (i4 + c);
+        }
+      }
+    }
     if (!valid) continue;
     const int i_begin = max(0, key - r0);
     const int i_end = min(kT, S - r0);
@@ -151,10 +183,17 @@ __global__ __launch_bounds__(kT) void dkdv_f32_kernel(
       const float s = dot_row<D>(kr, sq, i);
       const float dp = dot_row<D>(vr, sdo, i);
       const float p = expf(s * scale - slse[i]);
-      const float ds = p * (dp - sdel[i]) * scale;
+      float pv = p, ds;
+      if constexpr (DROP) {
+        const float f = (keep >> i) & 1u ? dr.scale : 0.0f;
+        pv = p * f;
+        ds = p * (dp * f - sdel[i]) * scale;
+      } else {
+        ds = p * (dp - sdel[i]) * scale;
+      }
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        dva[d] = fmaf(p, sdo[i][d], dva[d]);
+        dva[d] = fmaf(pv, sdo[i][d], dva[d]);
         dka[d] = fmaf(ds, sq[i][d], dka[d]);
       }
     }
@@ -169,11 +208,11 @@ __global__ __launch_bounds__(kT) void dkdv_f32_kernel(
 }
 
 // One lane per query r: dQ_r = scale * sum_{j<=r} dS_rj K_j.
-template <int D>
+template <int D, bool DROP>
 __global__ __launch_bounds__(kT) void dq_f32_kernel(
     float* __restrict__ dq, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ delta, int S, float scale) {
+    const float* __restrict__ delta, int S, float scale, const DropParams dr) {
   __shared__ __attribute__((aligned(16))) float sk[kT][D];
   __shared__ __attribute__((aligned(16))) float sv[kT][D];
   const int bh = blockIdx.x;
@@ -198,11 +237,18 @@ __global__ __launch_bounds__(kT) void dq_f32_kernel(
     __syncthreads();
     if (!valid) continue;
     const int nj = min(kT, row - k0 + 1);
+    uint32_t keep = 0;
     for (int j = 0; j < nj; ++j) {
       const float s = dot_row<D>(qr, sk, j);
       const float dp = dot_row<D>(dor, sv, j);
       const float p = expf(s * scale - rl);
-      const float ds = p * (dp - rd) * scale;
+      float ds;
+      if constexpr (DROP) {
+        if ((j & 3) == 0) keep = keep4(dr, (uint64_t)bh * S + row, (uint32_t)(k0 + j) >> 2);
+        ds = p * (dp * keep_factor(keep, j & 3, dr.scale) - rd) * scale;
+      } else {
+        ds = p * (dp - rd) * scale;
+      }
 #pragma unroll
       for (int d = 0; d < D; ++d) dqa[d] = fmaf(ds, sk[j][d], dqa[d]);
     }
@@ -215,24 +261,40 @@ __global__ __launch_bounds__(kT) void dq_f32_kernel(
 
 template <int D>
 hipError_t fwd_f32_t(float* out, float* lse, const float* q, const float* k, const float* v,
-                     int BH, int S, float scale, hipStream_t stream) {
-  fwd_f32_kernel<D><<<dim3(BH, (S + kT - 1) / kT), kT, 0, stream>>>(out, lse, q, k, v, S, scale);
+                     int BH, int S, float scale, hipStream_t stream, const Dropout* drop) {
+  const dim3 grid(BH, (S + kT - 1) / kT);
+  const DropParams dr = drop_params(drop);
+  if (drop != nullptr)
+    fwd_f32_kernel<D, true><<<grid, kT, 0, stream>>>(out, lse, q, k, v, S, scale, dr);
+  else
+    fwd_f32_kernel<D, false><<<grid, kT, 0, stream>>>(out, lse, q, k, v, S, scale, dr);
   return hipGetLastError();
 }
 
 template <int D>
 hipError_t bwd_f32_t(float* dq, float* dk, float* dv, float* delta, const float* dout,
                      const float* out, const float* lse, const float* q, const float* k,
-                     const float* v, int BH, int S, float scale, hipStream_t stream) {
+                     const float* v, int BH, int S, float scale, hipStream_t stream,
+                     const Dropout* drop) {
+  const DropParams dr = drop_params(drop);
   const long rows = (long)BH * S;
   delta_f32_kernel<<<(unsigned)((rows + 255) / 256), 256, 0, stream>>>(delta, dout, out, rows, D);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 grid(BH, (S + kT - 1) / kT);
-  dkdv_f32_kernel<D><<<grid, kT, 0, stream>>>(dk, dv, q, k, v, dout, lse, delta, S, scale);
+  if (drop != nullptr)
+    dkdv_f32_kernel<D, true><<<grid, kT, 0, stream>>>(dk, dv, q, k, v, dout, lse, delta, S,
+                                                      scale, dr);
+  else
+    dkdv_f32_kernel<D, false><<<grid, kT, 0, stream>>>(dk, dv, q, k, v, dout, lse, delta, S,
+                                                       scale, dr);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  dq_f32_kernel<D><<<grid, kT, 0, stream>>>(dq, q, k, v, dout, lse, delta, S, scale);
+  if (drop != nullptr)
+    dq_f32_kernel<D, true><<<grid, kT, 0, stream>>>(dq, q, k, v, dout, lse, delta, S, scale, dr);
+  else
+    dq_f32_kernel<D, false><<<grid, kT, 0, stream>>>(dq, q, k, v, dout, lse, delta, S, scale,
+                                                     dr);
   return hipGetLastError();
 }
 
@@ -240,20 +302,22 @@ hipError_t bwd_f32_t(float* dq, float* dk, float* dv, float* delta, const float*
 
 hipError_t launch_fwd_f32(float* out, float* lse, const float* q, const float* k,
                           const float* v, int BH, int S, int D, float scale,
-                          hipStream_t stream) {
-  if (D == 64) return fwd_f32_t<64>(out, lse, q, k, v, BH, S, scale, stream);
-  if (D == 32) return fwd_f32_t<32>(out, lse, q, k, v, BH, S, scale, stream);
+                          hipStream_t stream, const Dropout* drop) {
+  if (D == 64) return fwd_f32_t<64>(out, lse, q, k, v, BH, S, scale, stream, drop);
+  if (D == 32) return fwd_f32_t<32>(out, lse, q, k, v, BH, S, scale, stream, drop);
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_bwd_f32(float* dq, float* dk, float* dv, float* delta, const float* dout,
                           const float* out, const float* lse, const float* q, const float* k,
                           const float* v, int BH, int S, int D, float scale,
-                          hipStream_t stream) {
+                          hipStream_t stream, const Dropout* drop) {
   if (D == 64)
-    return bwd_f32_t<64>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale, stream);
+    return bwd_f32_t<64>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale, stream,
+                         drop);
   if (D == 32)
-    return bwd_f32_t<32>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale, stream);
+    return bwd_f32_t<32>(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S, scale, stream,
+                         drop);
   return hipErrorInvalidValue;
 }
 

@@ -263,6 +263,35 @@ int dadgpt_flash_attention_backward_bf16_dropout(uint16_t* dq, uint16_t* dk, uin
                   fn);
 }
 
+int dadgpt_flash_attention_forward_dropout(float* out, float* lse, const float* q,
+                                           const float* k, const float* v, int BH, int S,
+                                           int d_head, float scale, float dropout_p,
+                                           uint64_t seed, void* stream) {
+  const char* fn = "dadgpt_flash_attention_forward_dropout";
+  if (int st = check_attn(fn, BH, S, d_head, scale, {out, lse, q, k, v})) return st;
+  if (int st = check_dropout(fn, dropout_p)) return st;
+  const dadgpt::Dropout drop{dropout_p, seed};
+  return from_hip(dadgpt::launch_fwd_f32(out, lse, q, k, v, BH, S, d_head, scale,
+                                         as_stream(stream), &drop),
+                  fn);
+}
+
+int dadgpt_flash_attention_backward_dropout(float* dq, float* dk, float* dv, float* delta,
+                                            const float* dout, const float* out,
+                                            const float* lse, const float* q, const float* k,
+                                            const float* v, int BH, int S, int d_head,
+                                            float scale, float dropout_p, uint64_t seed,
+                                            void* stream) {
+  const char* fn = "dadgpt_flash_attention_backward_dropout";
+  if (int st = check_attn(fn, BH, S, d_head, scale, {dq, dk, dv, delta, dout, out, lse, q, k, v}))
+    return st;
+  if (int st = check_dropout(fn, dropout_p)) return st;
+  const dadgpt::Dropout drop{dropout_p, seed};
+  return from_hip(dadgpt::launch_bwd_f32(dq, dk, dv, delta, dout, out, lse, q, k, v, BH, S,
+                                         d_head, scale, as_stream(stream), &drop),
+                  fn);
+}
+
 int dadgpt_flash_attention_backward_bf16_phase(int phase, uint16_t* dq, uint16_t* dk,
                                                uint16_t* dv, float* delta, const uint16_t* dout,
                                                const uint16_t* out, const float* lse,

@@ -73,13 +73,14 @@ hipError_t launch_bwd_bf16(bf16* dq, bf16* dk, bf16* dv, float* delta, const bf1
                            const AttnLayout& layout, hipStream_t stream, int phases = kBwdAll,
                            const Dropout* drop = nullptr);
 
-// fp32 flash forward/backward (the reference's own precision).
+// fp32 flash forward/backward (the reference's own precision), optionally with dropout.
 hipError_t launch_fwd_f32(float* out, float* lse, const float* q, const float* k,
-                          const float* v, int BH, int S, int D, float scale, hipStream_t stream);
+                          const float* v, int BH, int S, int D, float scale, hipStream_t stream,
+                          const Dropout* drop = nullptr);
 hipError_t launch_bwd_f32(float* dq, float* dk, float* dv, float* delta, const float* dout,
                           const float* out, const float* lse, const float* q, const float* k,
                           const float* v, int BH, int S, int D, float scale,
-                          hipStream_t stream);
+                          hipStream_t stream, const Dropout* drop = nullptr);
 
 // Decode over ragged KV caches [n_seq,H,max_len,D]. A cache longer than one workgroup chunk
 // (512 keys bf16, 256 fp32 at D=64) is split into chunks merged inside the kernel through the

@@ -114,6 +114,18 @@ int dadgpt_flash_attention_backward_bf16_dropout(uint16_t* dq, uint16_t* dk, uin
                                                  float scale, float dropout_p, uint64_t seed,
                                                  void* stream);
 
+/* fp32 siblings (the reference's own precision; the reference's dropout path is fp32). */
+int dadgpt_flash_attention_forward_dropout(float* out, float* lse, const float* q,
+                                           const float* k, const float* v, int BH, int S,
+                                           int d_head, float scale, float dropout_p,
+                                           uint64_t seed, void* stream);
+int dadgpt_flash_attention_backward_dropout(float* dq, float* dk, float* dv, float* delta,
+                                            const float* dout, const float* out,
+                                            const float* lse, const float* q, const float* k,
+                                            const float* v, int BH, int S, int d_head,
+                                            float scale, float dropout_p, uint64_t seed,
+                                            void* stream);
+
 /* One kernel of dadgpt_flash_attention_backward_bf16, for per-kernel timing and profiling
  * (no reference counterpart). phase 1: dq, and delta = rowsum(dout * out) of the same rows;
  * 2: dk, dv (reads delta). Running phases 1, 2 in order equals the full backward. phase 0

@@ -156,6 +156,11 @@ def test_dropout_validation():
     assert fwd(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 48, 0.125, 0.1, 7, None) == 2
     assert fwd(None, FAKE, FAKE, FAKE, FAKE, 4, 64, 64, 0.125, 0.1, 7, None) == 1
     assert bwd(*[FAKE] * 10, 4, 0, 64, 0.125, 0.1, 7, None) == 1
+    fwd32, bwd32 = (L.dadgpt_flash_attention_forward_dropout,
+                    L.dadgpt_flash_attention_backward_dropout)
+    assert fwd32(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 64, 0.125, 1.0, 7, None) == 1
+    assert bwd32(*[FAKE] * 10, 4, 64, 64, 0.125, -0.5, 7, None) == 1
+    assert fwd32(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 40, 0.125, 0.1, 7, None) == 2
 
 
 def expected_ws(n, h, max_len, d):

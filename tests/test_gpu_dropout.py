@@ -118,3 +118,53 @@ def test_dropout_cfg3_full(gpu):
     for bh in (0, 97, 191):  # the mask rows of slice bh are bh*S + i
         o_ref = oracle.attn_fwd_dropout_slices(qn, kn, vn, 0.125, p, seed, bh, bh + 1)
         assert max_abs(host(a[0][bh]), o_ref[0]) <= TOL_O
+
+
+# ---- fp32 (the reference's precision): max-abs <= 1e-5 against the oracle ----
+
+TOL_F32 = 1e-5
+
+
+def run_f32(q, k, v, g, scale, p, seed):
+    BH, S, D = q.shape
+    out = torch.empty_like(q)
+    lse = torch.empty((BH, S), dtype=torch.float32, device="cuda")
+    A.flash_attention_forward_dropout(out, lse, q, k, v, BH, S, D, scale, p, seed)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    delta = torch.empty_like(lse)
+    A.flash_attention_backward_dropout(dq, dk, dv, delta, g, out, lse, q, k, v, BH, S, D, scale,
+                                       p, seed)
+    torch.cuda.synchronize()
+    return out, lse, dq, dk, dv, delta
+
+
+@pytest.mark.parametrize("BH,S,D,p", [(2, 70, 64, 0.1), (1, 129, 32, 0.5), (2, 200, 64, 0.3),
+                                      (1, 1, 32, 0.2)])
+def test_dropout_f32_matches_oracle(gpu, BH, S, D, p):
+    case(f"fp32 dropout BH={BH} S={S} D={D} p={p}")
+    seed = 99 + S
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=700 + S + D, with_dout=True)
+    scale = float(np.float32(1.0 / math.sqrt(D)))
+    f32 = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).to("cuda")
+    q, k, v, g = (f32(x) for x in (qn, kn, vn, gn))
+    out, lse, dq, dk, dv, delta = run_f32(q, k, v, g, scale, p, seed)
+    o_ref, l_ref = oracle.attn_fwd_dropout(qn, kn, vn, scale, p, seed)
+    assert max_abs(host(out), o_ref) <= TOL_F32
+    assert max_abs(host(lse), l_ref) <= TOL_F32
+    refs = oracle.attn_bwd_dropout(gn, qn, kn, vn, scale, p, seed, out=o_ref)
+    for got, ref, nm in zip((dq, dk, dv, delta), refs, ("dq", "dk", "dv", "delta")):
+        assert max_abs(host(got), ref) <= TOL_F32, nm
+
+
+def test_dropout_f32_rate_zero_equals_plain(gpu):
+    BH, S, D = 2, 150, 64
+    case(f"fp32 dropout p=0 vs plain BH={BH} S={S}")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=711, with_dout=True)
+    f32 = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).to("cuda")
+    q, k, v, g = (f32(x) for x in (qn, kn, vn, gn))
+    a = run_f32(q, k, v, g, 0.125, 0.0, 3)
+    o2, l2 = A.attention_forward(q, k, v, 0.125)
+    dq2, dk2, dv2, d2 = A.attention_backward(g, o2, l2, q, k, v, 0.125)
+    torch.cuda.synchronize()
+    for x, y in zip(a, (o2, l2, dq2, dk2, dv2, d2)):
+        assert torch.equal(x, y)
