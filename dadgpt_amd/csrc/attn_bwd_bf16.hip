@@ -19,6 +19,8 @@
 // Masking is compiled only into the blocks that straddle the diagonal (template DIAG), so the
 // other blocks run branch-free. The streamed tiles (Q and dO for dK/dV, K and V for dQ) are
 // double-buffered in LDS through direct global->LDS loads, one tile ahead of the compute.
+// STRIDED and DROP instantiations as in the forward: per-tensor strides, and dropout with
+// the keep bits regenerated (dV from P keep/(1-p), dS = P (dP keep/(1-p) - delta)).
 #include "common.hpp"
 #include "dropout.hpp"
 #include "kernels.hpp"

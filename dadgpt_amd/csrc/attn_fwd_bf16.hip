@@ -30,6 +30,11 @@
 // instructions): tile t+1 is in flight while tile t is on the MFMA pipes; one barrier per
 // tile. (Triple buffering measured slower: the third buffer's LDS cost more than the extra
 // tile of lead gained.)
+//
+// Instantiations: STRIDED reads q, k, v and writes out at per-tensor (batch, head, row)
+// strides (the token-major layout of the projections) instead of contiguous [BH, S, D]; DROP
+// multiplies the probabilities that reach P V by keep/(1-p) (dropout.hpp), leaving the
+// normaliser and logsumexp those of the undropped row.
 #include "common.hpp"
 #include "dropout.hpp"
 #include "kernels.hpp"
@@ -39,9 +44,9 @@ namespace dadgpt {
 namespace {
 
 // Geometry: NQB 32-query blocks per wave, WAVES waves per workgroup, MINB workgroups per CU
-// (the register budget: 512 / (MINB * WAVES / 4) per lane). One wave with one query block and
-// 8 waves per workgroup keeps 4 waves on each SIMD to cover LDS and MFMA latencies; two query
-// blocks per wave halve the LDS reads per MFMA instead.
+// (the register budget: 512 / (MINB * WAVES / 4) per lane). 4 waves of one query block and 3
+// workgroups per CU (3 waves per SIMD) measured fastest; 4 per SIMD (the kernel fits 128
+// registers), 8- and 16-wave workgroups and two query blocks per wave were no faster.
 #ifndef DADGPT_FWD_NQB
 #define DADGPT_FWD_NQB 1
 #endif
