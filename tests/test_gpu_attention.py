@@ -437,3 +437,23 @@ def test_decode_matches_forward_rows(gpu):
     o = host(out)
     for i, t in enumerate(ts):
         assert max_abs(host(dec)[i], o[:, t]) <= TOL_DEC, f"row {t}"
+
+
+@pytest.mark.parametrize("D", [64, 32])
+def test_bf16_long_sequence(gpu, D):
+    """S = 2048 (twice the configs' length): rows far from their first key exercise the
+    running maximum and the fp32 sums over long rows."""
+    BH, S = 2, 2048
+    case(f"bf16 long sequence BH={BH} S={S} D={D}")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=2048 + D, with_dout=True, bf16=True)
+    scale = scale_of(D)
+    q, k, v, g = (dev(x, torch.bfloat16) for x in (qn, kn, vn, gn))
+    out, lse = A.attention_forward(q, k, v, scale)
+    dq, dk, dv, _ = A.attention_backward(g, out, lse, q, k, v, scale)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oracle.attn_fwd(qn, kn, vn, scale, threads=2)
+    assert max_abs(host(out), o_ref) <= TOL_O
+    assert max_abs(host(lse), l_ref) <= TOL_LSE
+    ref = oracle.attn_bwd(gn, qn, kn, vn, scale, threads=2)[:3]
+    for a, b, nm in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+        assert max_abs(host(a), b) <= TOL_GRAD, nm
