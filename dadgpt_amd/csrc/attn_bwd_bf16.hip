@@ -85,23 +85,6 @@ __global__ __launch_bounds__(256) void delta_bf16_kernel(float* __restrict__ del
   if (valid && part == 0) delta[drow] = acc;
 }
 
-// Stores lanes' f32x16 accumulators C[d][row] (lane = row l32, element r = d row
-// 32*db + c32_row(r, hi)) as bf16 rows of `dst`, times `mul`.
-template <int DB>
-__device__ __forceinline__ void store_rows_bf16(bf16* dst, const f32x16 (&acc)[DB], float mul,
-                                                int hi) {
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = 32 * db + c32_row(4 * g, hi);
-      u32x2 w;
-      w[0] = pack_bf16x2(acc[db][4 * g] * mul, acc[db][4 * g + 1] * mul);
-      w[1] = pack_bf16x2(acc[db][4 * g + 2] * mul, acc[db][4 * g + 3] * mul);
-      st_g64(dst + d0, w);
-    }
-}
-
 // ---------------------------------------------------------------- dK / dV
 constexpr int kKW = 32;  // keys per wave
 
@@ -235,6 +218,7 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
   __shared__ __attribute__((aligned(16))) bf16 sq[2][kTileRows * D];
   __shared__ __attribute__((aligned(16))) bf16 sdo[2][kTileRows * D];
   __shared__ __attribute__((aligned(16))) float sst[kWaves][2][2][kTileRows];
+  static_assert(kWaves * kKW <= 2 * kTileRows, "the epilogue stages every wave's rows in sq");
 
   const int bh = blockIdx.x;
   const int kblk = blockIdx.y;  // key block 0 sees the most query tiles: dispatched first
@@ -324,9 +308,13 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
     if (t + 1 < t_end) tile(t + 1, sq[1], sdo[1], 1, sq[0], sdo[0], 0);
   }
 
-  if (key < S) {
-    store_rows_bf16<DB>(sl.row(dk, kTDK, key), dkacc, dk_mul, hi);
-    store_rows_bf16<DB>(sl.row(dv, kTDV, key), dvacc, 1.0f, hi);
+  // the tiles are free after the last barrier: each wave stages its 32 rows in its quarter
+  // of sq (dK) and sdo (dV)
+  if (kw0 < S) {
+    store_rows_staged<D>(sl.row(dk, kTDK, kw0), sl.pitch(kTDK), S - kw0, dkacc, dk_mul,
+                         &sq[0][0] + wave * kKW * D, lane);
+    store_rows_staged<D>(sl.row(dv, kTDV, kw0), sl.pitch(kTDV), S - kw0, dvacc, 1.0f,
+                         &sdo[0][0] + wave * kKW * D, lane);
   }
 }
 
@@ -394,6 +382,7 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
   // K and V tiles, double-buffered (constant buffer indices; see the forward kernel).
   __shared__ __attribute__((aligned(16))) bf16 sk[2][kTileRows * D];
   __shared__ __attribute__((aligned(16))) bf16 sv[2][kTileRows * D];
+  static_assert(kWaves * kQW <= 2 * kTileRows, "the epilogue stages every wave's rows in sk");
 
   const int bh = blockIdx.x;
   const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
@@ -483,7 +472,9 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
     if (t + 1 < n_tiles) tile(t + 1, sk[1], sv[1], sk[0], sv[0]);
   }
 
-  if (qrow < S) store_rows_bf16<DB>(sl.row(dq, kTDQ, qrow), dqacc, scale, hi);
+  if (q0 < S)
+    store_rows_staged<D>(sl.row(dq, kTDQ, q0), sl.pitch(kTDQ), S - q0, dqacc, scale,
+                         &sk[0][0] + wave * kQW * D, lane);
 }
 
 template <int D>

@@ -219,6 +219,7 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
   __shared__ __attribute__((aligned(16))) bf16 sk[2][kTileRows * D];
   __shared__ __attribute__((aligned(16))) bf16 sv[2][kTileRows * D];
   __shared__ f32x4 smask[4][64];
+  static_assert(kWaves * kQW <= 2 * kTileRows, "the epilogue stages every wave's rows in sk");
 
   const int bh = blockIdx.x;
   const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
@@ -326,20 +327,11 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
     const int qrow = q0 + 32 * i + l32;
     const float l = sum_halves(lrun[i]);
     const float inv = 1.0f / l;
-    if (qrow < S) {
-      bf16* orow = sl.row(out, kTO, qrow);
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d0 = 32 * db + c32_row(4 * g, hi);
-          u32x2 w;
-          w[0] = pack_bf16x2(oacc[i][db][4 * g] * inv, oacc[i][db][4 * g + 1] * inv);
-          w[1] = pack_bf16x2(oacc[i][db][4 * g + 2] * inv, oacc[i][db][4 * g + 3] * inv);
-          st_g64(orow + d0, w);
-        }
-      if (hi == 0) lse[(size_t)bh * S + qrow] = (mrun[i] + __log2f(l)) * kLn2;
-    }
+    // the tiles are free after the last barrier: each wave stages its rows in its quarter of sk
+    if (q0 + 32 * i < S)
+      store_rows_staged<D>(sl.row(out, kTO, q0 + 32 * i), sl.pitch(kTO), S - q0 - 32 * i,
+                           oacc[i], inv, &sk[0][0] + (wave * kNQB + i) * 32 * D, lane);
+    if (qrow < S && hi == 0) lse[(size_t)bh * S + qrow] = (mrun[i] + __log2f(l)) * kLn2;
   }
 }
 

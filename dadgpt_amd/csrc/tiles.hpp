@@ -197,6 +197,37 @@ struct DmaTile {
   }
 };
 
+// Stores a wave's 32 x D result, held in MFMA accumulator layout (lane row l32; element 4g+e
+// of acc[db] is column 32db + 8g + 4hi + e), times the lane's `mul`, as bf16 rows dst[r *
+// pitch ..] for r < rows_valid. The rows pass through the wave's own `stage` (32 * D bf16 of
+// LDS no other wave touches, 16-byte chunks XOR-swizzled by row): written in accumulator
+// layout, read back row-contiguous, so every global store instruction writes whole rows
+// (64 lanes x 16 bytes) instead of 16-byte pieces of 32 rows.
+template <int D>
+__device__ __forceinline__ void store_rows_staged(bf16* dst, int pitch, int rows_valid,
+                                                  const f32x16 (&acc)[D / 32], float mul,
+                                                  bf16* stage, int lane) {
+  constexpr int C = D / 8;  // 16-byte chunks per row
+  const int l32 = lane & 31, hi = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int chunk = (32 * db + 8 * g) / 8;
+      u32x2 w;
+      w[0] = pack_bf16x2(acc[db][4 * g] * mul, acc[db][4 * g + 1] * mul);
+      w[1] = pack_bf16x2(acc[db][4 * g + 2] * mul, acc[db][4 * g + 3] * mul);
+      *reinterpret_cast<u32x2*>(stage + l32 * D + ((chunk ^ (l32 % C)) << 3) + 4 * hi) = w;
+    }
+  // the wave's own LDS writes complete before its reads (in order); no barrier needed
+#pragma unroll
+  for (int it = 0; it < 32 * C / 64; ++it) {
+    const int idx = it * 64 + lane, r = idx / C, c = idx % C;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * D + ((c ^ (r % C)) << 3));
+    if (r < rows_valid) *reinterpret_cast<u32x4*>(dst + (size_t)r * pitch + c * 8) = v;
+  }
+}
+
 // s_waitcnt: vector-memory count <= N and every LDS operation done (gfx9 encoding: vmcnt in
 // bits 3:0 and 15:14, expcnt 6:4 left at its maximum, lgkmcnt 11:8 = 0).
 template <int N>
