@@ -76,8 +76,8 @@ __global__ __launch_bounds__(kT) void fwd_f32_kernel(float* __restrict__ out,
     uint64_t keep = 0;  // keep bits of keys k0 .. k0+63 of this row
     if constexpr (DROP) {
 #pragma unroll 1
-      for (int j4 = 0; j4 < nj; j4 += 4)
-        keep |= (uint64_t)keep4(dr, (uint64_t)bh * S + row, (uint32_t)(k0 + j4) >> 2) << j4;
+      for (int j8 = 0; j8 < nj; j8 += 8)
+        keep |= (uint64_t)keep8(dr, (uint64_t)bh * S + row, (uint32_t)(k0 + j8) >> 3) << j8;
     }
     float s[kT];
     float mx = neg_inf();
@@ -157,23 +157,15 @@ __global__ __launch_bounds__(kT) void dkdv_f32_kernel(
     }
     __syncthreads();
     // keep bits of this lane's key for the tile's 64 rows (every lane, before any exits: the
-    // bits of 4 rows come from one Philox block per lane of a 4-lane quad, then an exchange)
+    // bits of 8 rows come from one Philox block per lane of an 8-lane group, then a transpose)
     uint64_t keep = 0;
     if constexpr (DROP) {
-      const int t = threadIdx.x & 3;
-      const uint32_t j4 = (uint32_t)(blk * kT + (threadIdx.x & ~3)) >> 2;
+      const int t = threadIdx.x & 7;
+      const uint32_t j8 = (uint32_t)(blk * kT + (threadIdx.x & ~7)) >> 3;
 #pragma unroll 1
-      for (int i4 = 0; i4 < kT; i4 += 4) {
-        const uint64_t row = (uint64_t)bh * S + r0 + i4 + t;
-        const u32x4 w = philox4x32_10((uint32_t)row, (uint32_t)(row >> 32), j4, 0u, dr.k0,
-                                      dr.k1);
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const int c = t ^ d;
-          const uint32_t send = c == 0 ? w[0] : c == 1 ? w[1] : c == 2 ? w[2] : w[3];
-          const uint32_t got = d == 0 ? send : (uint32_t)__shfl_xor((int)send, d, 64);
-          keep |= (uint64_t)((got >> 8) >= dr.thr) << (i4 + c);
-        }
+      for (int i8 = 0; i8 < kT; i8 += 8) {
+        const uint32_t m = keep8(dr, (uint64_t)bh * S + r0 + i8 + t, j8);  // row i8 + t
+        keep |= (uint64_t)transpose8_bits(m, t) << i8;  // bit e: row i8 + e, this lane's key
       }
     }
     if (!valid) continue;
@@ -244,8 +236,8 @@ __global__ __launch_bounds__(kT) void dq_f32_kernel(
       const float p = expf(s * scale - rl);
       float ds;
       if constexpr (DROP) {
-        if ((j & 3) == 0) keep = keep4(dr, (uint64_t)bh * S + row, (uint32_t)(k0 + j) >> 2);
-        ds = p * (dp * keep_factor(keep, j & 3, dr.scale) - rd) * scale;
+        if ((j & 7) == 0) keep = keep8(dr, (uint64_t)bh * S + row, (uint32_t)(k0 + j) >> 3);
+        ds = p * (dp * keep_factor(keep, j & 7, dr.scale) - rd) * scale;
       } else {
         ds = p * (dp - rd) * scale;
       }

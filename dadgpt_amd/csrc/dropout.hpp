@@ -3,11 +3,12 @@
 // counter-based generator, so no mask is stored.
 //
 // Generator: Philox4x32-10 as published (Salmon, Moraes, Dror, Shaw, "Parallel random
-// numbers: as easy as 1, 2, 3", SC'11). Keep bit of (row, j) = word j%4 of the block at
-// counter {row lo, row hi, j/4, 0} under key {seed lo, seed hi}, kept iff (word >> 8) >= thr
-// with thr = ceil(p * 2^24) (a 24-bit uniform u >= p). Kept probabilities are scaled by
-// 1/(1-p) in fp32, as the reference's dropout (cuda/gpu_ops.cu:712-749); its cuRAND stream is
-// not reproduced, so masks match this definition, not the reference's.
+// numbers: as easy as 1, 2, 3", SC'11). One block gives 8 keys: the keep bit of (row, j) is
+// 16-bit half j%2 (low half first) of word (j%8)/2 of the block at counter
+// {row lo, row hi, j/8, 0} under key {seed lo, seed hi}, kept iff that 16-bit uniform is
+// >= thr = ceil(p * 2^16). Kept probabilities are scaled by 1/(1-p) in fp32, as the
+// reference's dropout (cuda/gpu_ops.cu:712-749); its cuRAND stream is not reproduced, so
+// masks match this definition, not the reference's.
 #pragma once
 
 #include <math.h>
@@ -20,7 +21,7 @@ namespace dadgpt {
 // Kernel argument: the key (seed), the keep threshold and the scale of kept values.
 struct DropParams {
   uint32_t k0, k1;  // seed lo, hi
-  uint32_t thr;     // keep iff (word >> 8) >= thr
+  uint32_t thr;     // keep iff the 16-bit uniform >= thr
   float scale;      // 1 / (1 - p)
 };
 
@@ -30,7 +31,7 @@ inline DropParams drop_params(const Dropout* d) {
   if (d != nullptr) {
     r.k0 = (uint32_t)d->seed;
     r.k1 = (uint32_t)(d->seed >> 32);
-    r.thr = (uint32_t)ceil((double)d->p * 16777216.0);
+    r.thr = (uint32_t)ceil((double)d->p * 65536.0);
     r.scale = 1.0f / (1.0f - d->p);
   }
   return r;
@@ -55,56 +56,60 @@ __device__ __forceinline__ u32x4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_
   return u32x4{c0, c1, c2, c3};
 }
 
-// Keep bits of keys 4*j4 .. 4*j4+3 of `row` (bit e: key 4*j4 + e).
-__device__ __forceinline__ uint32_t keep4(const DropParams& dr, uint64_t row, uint32_t j4) {
-  const u32x4 w = philox4x32_10((uint32_t)row, (uint32_t)(row >> 32), j4, 0u, dr.k0, dr.k1);
+// Keep bits of keys 8*j8 .. 8*j8+7 of `row` (bit e: key 8*j8 + e).
+__device__ __forceinline__ uint32_t keep8(const DropParams& dr, uint64_t row, uint32_t j8) {
+  const u32x4 w = philox4x32_10((uint32_t)row, (uint32_t)(row >> 32), j8, 0u, dr.k0, dr.k1);
   uint32_t bits = 0;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) bits |= (uint32_t)((w[e] >> 8) >= dr.thr) << e;
+  for (int e = 0; e < 4; ++e) {
+    bits |= (uint32_t)((w[e] & 0xFFFFu) >= dr.thr) << (2 * e);
+    bits |= (uint32_t)((w[e] >> 16) >= dr.thr) << (2 * e + 1);
+  }
   return bits;
 }
 
 // Keep bits for the score layout with a fixed row per lane and keys along the registers:
-// register 8j + e of lane half hi holds key key0 + 16j + 8hi + e (j < 2, e < 8), i.e. four
-// groups of 4 consecutive keys. Bit 8j + e of the result = register 8j + e.
+// register 8j + e of lane half hi holds key key0 + 16j + 8hi + e (j < 2, e < 8; key0 a
+// multiple of 8), i.e. two groups of 8 consecutive keys, one Philox block each. Bit 8j + e of
+// the result = register 8j + e.
 __device__ __forceinline__ uint32_t keep_row16(const DropParams& dr, uint64_t row, int key0,
                                                int hi) {
   uint32_t bits = 0;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int j = g >> 1, u = g & 1;
-    const int kb = key0 + 16 * j + 8 * hi + 4 * u;  // a multiple of 4
-    bits |= keep4(dr, row, (uint32_t)kb >> 2) << (8 * j + 4 * u);
-  }
+  for (int j = 0; j < 2; ++j) bits |= keep8(dr, row, (uint32_t)(key0 + 16 * j + 8 * hi) >> 3) << (8 * j);
   return bits;
 }
 
+// Bit-matrix transpose across the 8 lanes of a group, for each byte of x (bits 8j .. 8j+7)
+// independently: on entry lane t holds row t of an 8x8 bit matrix in each byte (bit k =
+// column k), on exit column t (bit e = row e). Butterflies of distance 4, 2, 1: at each, the
+// lanes of the lower half keep their low-half columns and take the partner's low-half
+// columns into their high half, and the upper lanes the reverse (three lane shuffles).
+template <int S>
+__device__ __forceinline__ uint32_t transpose8_step(uint32_t x, int t) {
+  constexpr uint32_t hi_cols = S == 4 ? 0xF0F0u : S == 2 ? 0xCCCCu : 0xAAAAu;  // column bit S set
+  constexpr uint32_t lo_cols = hi_cols ^ 0xFFFFu;
+  const uint32_t y = (uint32_t)__shfl_xor((int)x, S, 64);
+  return (t & S) ? (x & hi_cols) | ((y & hi_cols) >> S) : (x & lo_cols) | ((y & lo_cols) << S);
+}
+__device__ __forceinline__ uint32_t transpose8_bits(uint32_t x, int t) {
+  return transpose8_step<1>(transpose8_step<2>(transpose8_step<4>(x, t), t), t);
+}
+
 // Keep bits for the transposed layout (a fixed key per lane, rows along the registers):
-// lane (l32, hi) holds key key0 + l32 (key0 a multiple of 4) and register 8j + e holds row
-// row0 + 16j + 8hi + e. Each group of 4 rows needs the 4 consecutive keys of a lane quad, which
-// one Philox block gives: lane t of the quad computes the block of row (group + t), and a
-// 4x4 exchange across the quad hands every lane its own key's word of all 4 rows. Bit 8j + e
-// of the result = register 8j + e.
+// lane (l32, hi) holds key key0 + l32 (key0 a multiple of 8) and register 8j + e holds row
+// row0 + 16j + 8hi + e. The 8 lanes of a group hold 8 consecutive keys, which one Philox
+// block per row gives: lane t of the group computes the blocks of rows e = t (j = 0 and 1),
+// and a bit transpose across the group hands every lane its own key's bit of all 16 rows.
+// Bit 8j + e of the result = register 8j + e.
 __device__ __forceinline__ uint32_t keep_col16(const DropParams& dr, uint64_t row0, int key0,
                                                int lane) {
-  const int l32 = lane & 31, hi = lane >> 5, t = l32 & 3;
-  const uint32_t j4 = (uint32_t)(key0 + (l32 & ~3)) >> 2;
-  uint32_t bits = 0;
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int j = g >> 1, u = g & 1;
-    const uint64_t row = row0 + 16 * j + 8 * hi + 4 * u + t;
-    const u32x4 w = philox4x32_10((uint32_t)row, (uint32_t)(row >> 32), j4, 0u, dr.k0, dr.k1);
-    // round d: send word (t ^ d), receive the word of this lane's key (t) of row t ^ d
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const int c = t ^ d;
-      const uint32_t send = c == 0 ? w[0] : c == 1 ? w[1] : c == 2 ? w[2] : w[3];
-      const uint32_t got = d == 0 ? send : (uint32_t)__shfl_xor((int)send, d, 64);
-      bits |= (uint32_t)((got >> 8) >= dr.thr) << (8 * j + 4 * u + (t ^ d));
-    }
-  }
-  return bits;
+  const int l32 = lane & 31, hi = lane >> 5, t = l32 & 7;
+  const uint32_t j8 = (uint32_t)(key0 + (l32 & ~7)) >> 3;
+  const uint64_t r = row0 + 8 * hi + t;
+  // byte j, bit k: key k of the group in row row0 + 16j + 8hi + t
+  const uint32_t m = keep8(dr, r, j8) | (keep8(dr, r + 16, j8) << 8);
+  return transpose8_bits(m, t);
 }
 
 // The factor of a probability: scale if kept, 0 if dropped.

@@ -99,8 +99,9 @@ int dadgpt_flash_attention_backward_bf16(uint16_t* dq, uint16_t* dk, uint16_t* d
  * flash kernels: the keep bits are regenerated in the backward, no mask is stored. Kept
  * probabilities are scaled by 1/(1-p) (fp32), as the reference does; lse stays that of the
  * undropped scores. The mask is not cuRAND's: probability (row = bh*S + i, key j) is kept
- * iff (w >> 8) >= ceil(p * 2^24), w = word j%4 of Philox4x32-10 (Salmon et al., SC'11) at
- * counter {row lo, row hi, j/4, 0} under key {seed lo, seed hi}. The backward must get the
+ * iff u >= ceil(p * 2^16), u = 16-bit half j%2 (low first) of word (j%8)/2 of Philox4x32-10
+ * (Salmon et al., SC'11) at counter {row lo, row hi, j/8, 0} under key {seed lo, seed hi}.
+ * The backward must get the
  * forward's (dropout_p, seed). dropout_p in [0, 1); contiguous [BH, S, d_head] layout. */
 int dadgpt_flash_attention_forward_bf16_dropout(uint16_t* out, float* lse, const uint16_t* q,
                                                 const uint16_t* k, const uint16_t* v, int BH,

@@ -109,9 +109,10 @@ static void causal_zero_f32(float* s, int S) {
  * r >= rate, kept values times 1/(1-rate) in fp32, the gradient masked and scaled the same
  * way, :736-749). cuRAND's stream is not reproduced here; this build's mask comes from
  * Philox4x32-10 as published (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy
- * as 1, 2, 3", SC'11): the keep bit of probability (row = bh*S + i, key j) is word j%4 of
- * Philox4x32-10 at counter {row lo, row hi, j/4, 0} under key {seed lo, seed hi}, kept iff
- * (word >> 8) >= thr with thr = ceil(p * 2^24), i.e. a 24-bit uniform u >= p. */
+ * as 1, 2, 3", SC'11), one block per 8 keys: the keep bit of probability (row = bh*S + i,
+ * key j) is 16-bit half j%2 (low half first) of word (j%8)/2 of Philox4x32-10 at counter
+ * {row lo, row hi, j/8, 0} under key {seed lo, seed hi}, kept iff that half >= thr with
+ * thr = ceil(p * 2^16), i.e. a 16-bit uniform u >= p. */
 static uint32_t mulhilo32(uint32_t a, uint32_t b, uint32_t* hi) {
   const uint64_t prod = (uint64_t)a * b;
   *hi = (uint32_t)(prod >> 32);
@@ -141,14 +142,15 @@ void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t
   out[3] = c3;
 }
 
-uint32_t oracle_dropout_threshold(float p) { return (uint32_t)ceil((double)p * 16777216.0); }
+uint32_t oracle_dropout_threshold(float p) { return (uint32_t)ceil((double)p * 65536.0); }
 
 int oracle_dropout_keep(uint64_t seed, uint64_t row, int j, uint32_t thr) {
-  const uint32_t ctr[4] = {(uint32_t)row, (uint32_t)(row >> 32), (uint32_t)j >> 2, 0u};
+  const uint32_t ctr[4] = {(uint32_t)row, (uint32_t)(row >> 32), (uint32_t)j >> 3, 0u};
   const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
   uint32_t w[4];
   oracle_philox4x32_10(ctr, key, w);
-  return (w[j & 3] >> 8) >= thr;
+  const uint32_t u = (w[(j & 7) >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+  return u >= thr;
 }
 
 void oracle_dropout_mask(uint8_t* mask, int BH, int S, uint64_t seed, float p) {

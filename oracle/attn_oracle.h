@@ -55,8 +55,9 @@ int oracle_decode_f32(float* out, const float* q, const float* k_cache, const fl
 /* Attention-probability dropout (the reference: cuda/gpu_ops.cu:712-749, applied at
  * src/model.cpp:406-416 and :594-599). The reference draws its mask from cuRAND, whose
  * stream is not reproduced; this build's mask is Philox4x32-10 as published (Salmon et al.,
- * SC'11): probability (row = bh*S + i, key j) is kept iff (w >> 8) >= ceil(p * 2^24), w =
- * word j%4 of Philox4x32-10(counter {row lo, row hi, j/4, 0}, key {seed lo, seed hi}).
+ * SC'11): probability (row = bh*S + i, key j) is kept iff u >= ceil(p * 2^16), u = 16-bit
+ * half j%2 (low first) of word (j%8)/2 of Philox4x32-10(counter {row lo, row hi, j/8, 0},
+ * key {seed lo, seed hi}).
  * Kept probabilities are scaled by 1/(1-p) (fp32), as the reference does. p in [0, 1). */
 void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 uint32_t oracle_dropout_threshold(float p);

@@ -249,7 +249,7 @@ def check_drop_bwd_library(bwd_d, keep, BH=2, S=33, D=32, seed=44, p=0.3, dseed=
 
 
 def check_drop_unbiased(fwd_d, fwd, BH=1, S=24, D=16, seed=45, p=0.25, n=300):
-    """E[keep / (1-p)] = 1 (p = 0.25 is exactly representable as a 24-bit threshold), so the
+    """E[keep / (1-p)] = 1 (p = 0.25 is exactly representable as a 16-bit threshold), so the
     mean output over seeds tends to the undropped output: within 6 standard errors."""
     q, k, v = synth.attn_inputs(BH, S, D, seed=seed)
     scale = 1.0 / np.sqrt(D)

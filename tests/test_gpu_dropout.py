@@ -4,7 +4,12 @@ The keep bits are a fixed function of (seed, bh*S + query, key) (Philox4x32-10; 
 oracle implements the same definition and is pinned by the generator's published
 known-answer vectors), so for a given seed the GPU kernels and the oracle drop the same
 probabilities, and the results are compared at the bf16 tolerances: O <= 2e-2, lse <= 1e-3,
-dQ/dK/dV <= 5e-2 (max-abs, against the fp32 oracle on the same bf16-rounded inputs).
+dQ/dK/dV <= 5e-2 (max-abs, against the fp32 oracle on the same bf16-rounded inputs). Kept
+probabilities are scaled by 1/(1-p), and so are O, dP's kept terms, dS and the gradients
+built from them, together with every bf16 rounding of those values on the way (P f as the
+P V operand, dS as the dQ and dK operands, the stored outputs): at p = 0.9, |O| reaches 16,
+where storing it in bf16 alone moves it by up to 0.03. O and the gradients are therefore held
+to the tolerance times 1/(1-p), the factor their values carry; lse carries no factor.
 """
 import math
 
@@ -25,6 +30,12 @@ TOL_GRAD = 5e-2
 
 def case(msg):
     print(f"[case] {msg}", flush=True)
+
+
+def within_scaled(got, ref, tol, p, what):
+    """max |got - ref| <= tol / (1 - p): the bf16 tolerance at the magnitude dropout scales to."""
+    err = max_abs(got, ref)
+    assert err <= tol / (1.0 - p), f"{what}: max-abs {err:.3e} > {tol / (1.0 - p):.3e}"
 
 
 def dev(x):
@@ -62,12 +73,12 @@ def test_dropout_matches_oracle(gpu, BH, S, D, p):
     q, k, v, g = (dev(x) for x in (qn, kn, vn, gn))
     out, lse, dq, dk, dv, _ = run(q, k, v, g, scale, p, seed)
     o_ref, l_ref = oracle.attn_fwd_dropout(qn, kn, vn, scale, p, seed)
-    assert max_abs(host(out), o_ref) <= TOL_O
+    within_scaled(host(out), o_ref, TOL_O, p, "out")
     assert max_abs(host(lse), l_ref) <= TOL_LSE
     # the backward from the GPU's own O (delta uses it), as the reference's caller would
     refs = oracle.attn_bwd_dropout(gn, qn, kn, vn, scale, p, seed)[:3]
     for got, ref, nm in zip((dq, dk, dv), refs, ("dq", "dk", "dv")):
-        assert max_abs(host(got), ref) <= TOL_GRAD, nm
+        within_scaled(host(got), ref, TOL_GRAD, p, nm)
 
 
 def test_dropout_rate_zero_equals_plain(gpu):

@@ -156,26 +156,27 @@ def test_philox_known_answers(ctr, key, expect):
 
 
 def test_dropout_mask_definition():
-    """Keep bit of (row, j) = word j%4 of Philox at counter {row lo, row hi, j/4, 0}, key
-    {seed lo, seed hi}, compared as a 24-bit uniform; spot-checked against the block
-    function itself."""
+    """Keep bit of (row, j) = 16-bit half j%2 (low first) of word (j%8)/2 of Philox at counter
+    {row lo, row hi, j/8, 0}, key {seed lo, seed hi}, compared as a 16-bit uniform;
+    spot-checked against the block function itself."""
     seed, p, BH, S = 0x1234_5678_9ABC_DEF0, 0.3, 3, 37
     m = oracle.dropout_mask(BH, S, seed, p)
     thr = oracle.dropout_threshold(p)
-    assert thr == int(np.ceil(np.float32(p) * 2.0 ** 24))
+    assert thr == int(np.ceil(np.float32(p) * 2.0 ** 16))
     rng = np.random.default_rng(0)
     for _ in range(50):
         bh, i, j = int(rng.integers(BH)), int(rng.integers(S)), int(rng.integers(S))
         row = bh * S + i
-        w = oracle.philox4x32_10((row & 0xFFFFFFFF, row >> 32, j >> 2, 0),
+        w = oracle.philox4x32_10((row & 0xFFFFFFFF, row >> 32, j >> 3, 0),
                                  (seed & 0xFFFFFFFF, seed >> 32))
-        assert m[bh, i, j] == int((int(w[j & 3]) >> 8) >= thr)
+        u = (int(w[(j & 7) >> 1]) >> (16 * (j & 1))) & 0xFFFF
+        assert m[bh, i, j] == int(u >= thr)
 
 
 @pytest.mark.parametrize("p", [0.0, 0.1, 0.5, 0.9])
 def test_dropout_mask_rate(p):
     m = oracle.dropout_mask(8, 256, 77, p)
-    keep = 1.0 - oracle.dropout_threshold(p) / 2.0 ** 24
+    keep = 1.0 - oracle.dropout_threshold(p) / 2.0 ** 16
     n = m.size
     sigma = np.sqrt(max(keep * (1 - keep), 1e-12) / n)
     assert abs(m.mean() - keep) <= 5 * sigma + 1e-12
