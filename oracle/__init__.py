@@ -85,6 +85,7 @@ def lib():
         L.oracle_attn_fwd_dropout_f32.argtypes = [_fp, _fp, _fp, _fp, _fp, i, i, i, f, f, u64]
         L.oracle_attn_bwd_dropout_f32.argtypes = ([_fp] * 9 + [i, i, i, f, f, u64])
         L.oracle_attn_fwd_dropout_f32_range.argtypes = [_fp] * 5 + [i, i, i, i, f, f, u64]
+        L.oracle_attn_bwd_dropout_f32_range.argtypes = [_fp] * 7 + [i, i, i, i, f, f, u64]
         L.oracle_attn_fwd_dropout_f64.argtypes = [_dp, _dp, _dp, _dp, _dp, i, i, i, d, f, u64]
         L.oracle_attn_bwd_dropout_f64.argtypes = [_dp] * 7 + [i, i, i, d, f, u64]
         _lib = L
@@ -288,6 +289,18 @@ def attn_bwd_dropout(dout, q, k, v, scale, p, seed, out=None):
                                            _f(v), BH, S, D, scale, p, seed)
     _check(rc, "attn_bwd_dropout")
     return dq, dk, dv, delta
+
+
+def attn_bwd_dropout_slices(dout, q, k, v, scale, p, seed, bh0, bh1):
+    """Backward with dropout over bh slices [bh0, bh1) of [BH, S, D] inputs (the mask rows
+    keep their global index). Returns (dQ, dK, dV) of those slices."""
+    dout, q, k, v = _c32(dout), _c32(q), _c32(k), _c32(v)
+    BH, S, D = q.shape
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(q), np.zeros_like(q)
+    _check(lib().oracle_attn_bwd_dropout_f32_range(_f(dq), _f(dk), _f(dv), _f(dout), _f(q), _f(k),
+                                                   _f(v), bh0, bh1, S, D, scale, p, seed),
+           "attn_bwd_dropout_slices")
+    return dq[bh0:bh1], dk[bh0:bh1], dv[bh0:bh1]
 
 
 def attn_fwd_dropout_f64(q, k, v, scale, p, seed):

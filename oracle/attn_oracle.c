@@ -317,18 +317,18 @@ int oracle_attn_fwd_dropout_f32(float* O, float* lse, const float* Q, const floa
   return oracle_attn_fwd_dropout_f32_range(O, lse, Q, K, V, 0, BH, S, D, scale, p, seed);
 }
 
-int oracle_attn_bwd_dropout_f32(float* dQ, float* dK, float* dV, float* delta, const float* dO,
-                                const float* O, const float* Q, const float* K, const float* V,
-                                int BH, int S, int D, float scale, float p, uint64_t seed) {
+int oracle_attn_bwd_dropout_f32_range(float* dQ, float* dK, float* dV, const float* dO,
+                                      const float* Q, const float* K, const float* V, int bh0,
+                                      int bh1, int S, int D, float scale, float p,
+                                      uint64_t seed) {
   drop_t dr;
   if (drop_params(&dr, p, seed)) return -3;
-  if (delta) oracle_attn_delta_f32(delta, dO, O, (long)BH * S, D);
   const size_t ss = (size_t)S * S;
   float* P = (float*)malloc(sizeof(float) * 4 * ss + ss);
   if (!P) return -1;
   float *Pd = P + ss, *dP = P + 2 * ss, *dS = P + 3 * ss;
   uint8_t* keep = (uint8_t*)(P + 4 * ss);
-  for (int bh = 0; bh < BH; ++bh) {
+  for (int bh = bh0; bh < bh1; ++bh) {
     const long o = (long)bh * S * D;
     probs_slice_f32(NULL, Q + o, K + o, S, D, scale, P);
     dropout_slice_f32(Pd, keep, P, S, bh, &dr);
@@ -344,6 +344,16 @@ int oracle_attn_bwd_dropout_f32(float* dQ, float* dK, float* dV, float* delta, c
   }
   free(P);
   return 0;
+}
+
+int oracle_attn_bwd_dropout_f32(float* dQ, float* dK, float* dV, float* delta, const float* dO,
+                                const float* O, const float* Q, const float* K, const float* V,
+                                int BH, int S, int D, float scale, float p, uint64_t seed) {
+  drop_t dr;
+  if (drop_params(&dr, p, seed)) return -3;
+  if (delta) oracle_attn_delta_f32(delta, dO, O, (long)BH * S, D);
+  return oracle_attn_bwd_dropout_f32_range(dQ, dK, dV, dO, Q, K, V, 0, BH, S, D, scale, p,
+                                           seed);
 }
 
 /* ---- decode ---- */

@@ -77,6 +77,11 @@ int oracle_attn_fwd_dropout_f32_range(float* O, float* lse, const float* Q, cons
 int oracle_attn_bwd_dropout_f32(float* dQ, float* dK, float* dV, float* delta, const float* dO,
                                 const float* O, const float* Q, const float* K, const float* V,
                                 int BH, int S, int D, float scale, float p, uint64_t seed);
+/* The backward over slices [bh0, bh1) only (the mask rows keep their global index bh*S + i). */
+int oracle_attn_bwd_dropout_f32_range(float* dQ, float* dK, float* dV, const float* dO,
+                                      const float* Q, const float* K, const float* V, int bh0,
+                                      int bh1, int S, int D, float scale, float p,
+                                      uint64_t seed);
 int oracle_attn_fwd_dropout_f64(double* O, double* lse, const double* Q, const double* K,
                                 const double* V, int BH, int S, int D, double scale, float p,
                                 uint64_t seed);

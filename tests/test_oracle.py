@@ -233,3 +233,17 @@ def test_oracle_dropout_rejects_bad_rate():
     for p in (1.0, -0.1, float("nan")):
         with pytest.raises(RuntimeError):
             oracle.attn_fwd_dropout(q, k, v, 0.1, p, 1)
+
+
+def test_dropout_slice_ranges_equal_full():
+    """The slice-range forward and backward with dropout keep each slice's global mask rows:
+    they equal the corresponding slices of the full computation exactly."""
+    BH, S, D, p, seed = 4, 45, 16, 0.3, 99
+    q, k, v, g = synth.attn_inputs(BH, S, D, seed=5, with_dout=True)
+    o_full = oracle.attn_fwd_dropout(q, k, v, 0.25, p, seed)[0]
+    grads = oracle.attn_bwd_dropout(g, q, k, v, 0.25, p, seed)[:3]
+    o_part = oracle.attn_fwd_dropout_slices(q, k, v, 0.25, p, seed, 1, 3)
+    g_part = oracle.attn_bwd_dropout_slices(g, q, k, v, 0.25, p, seed, 1, 3)
+    assert np.array_equal(o_full[1:3], o_part)
+    for a, b in zip(grads, g_part):
+        assert np.array_equal(a[1:3], b)
