@@ -51,18 +51,21 @@ int check_ptrs(const char* fn, std::initializer_list<const void*> ptrs) {
   return DADGPT_OK;
 }
 
-// Largest S for one grid row: the kernels index rows with int and grid.y <= 65535 blocks.
+// Launch limits. Row and stride arithmetic in the kernels is 32-bit (row counts up to 2^24);
+// every attention grid is (BH, ceil(S / tile)) with tiles of at least 64 rows and
+// grid.y <= 65535; a dispatch counts its work-items along x in 32 bits (BH workgroups of at
+// most 256 lanes; 8 lanes per row in the delta kernel).
 constexpr long kMaxRows = 1L << 24;
+constexpr long kMaxSeq = 65535L * 64;
 
 int check_attn(const char* fn, int BH, int S, int d_head, float scale,
                std::initializer_list<const void*> ptrs) {
   if (int st = check_ptrs(fn, ptrs)) return st;
   if (BH < 1 || S < 1)
     return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: BH=%d and S=%d must be positive", fn, BH, S);
-  if (S > kMaxRows) return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: S=%d too large", fn, S);
-  // grids: BH workgroups of 256 lanes along x, 8 lanes per row in the delta kernel (the
-  // dispatch packet counts work-items in 32 bits)
-  if (BH > kMaxRows || (long long)BH * S > (1LL << 29))
+  if (S > kMaxSeq)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: S=%d exceeds %ld", fn, S, kMaxSeq);
+  if (BH >= kMaxRows || (long long)BH * S > (1LL << 29))
     return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: BH=%d x S=%d too large", fn, BH, S);
   if (!supported(d_head))
     return fail(DADGPT_ERR_UNSUPPORTED, "flash attention: unsupported d_head %d", d_head);
@@ -71,18 +74,28 @@ int check_attn(const char* fn, int BH, int S, int d_head, float scale,
   return DADGPT_OK;
 }
 
-int check_decode(const char* fn, int n_seq, int H, int max_len, int d_head, float scale,
-                 const void* ws, size_t ws_bytes, std::initializer_list<const void*> ptrs) {
+// Decode shape: grid (n_seq * H, chunks) of 512-lane workgroups, so n_seq * H * 512 < 2^32
+// work-items and at most 65535 chunks of the shortest chunk (256 keys, fp32 at d_head 64).
+int check_decode_shape(const char* fn, int n_seq, int H, int max_len, int d_head, float scale,
+                       std::initializer_list<const void*> ptrs) {
   if (int st = check_ptrs(fn, ptrs)) return st;
   if (n_seq < 1 || H < 1 || max_len < 1)
     return fail(DADGPT_ERR_INVALID_ARGUMENT,
                 "%s: n_seq=%d, n_heads=%d, max_len=%d must be positive", fn, n_seq, H, max_len);
-  if (n_seq > 65535 || H > 65535 || max_len > kMaxRows)
-    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: shape exceeds launch limits", fn);
+  if ((long long)n_seq * H >= (1LL << 23) || max_len > 65535L * 256)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                "%s: n_seq=%d x n_heads=%d or max_len=%d exceeds the launch limits", fn, n_seq,
+                H, max_len);
   if (!supported(d_head))
     return fail(DADGPT_ERR_UNSUPPORTED, "decode attention: unsupported d_head %d", d_head);
   if (!std::isfinite(scale))
     return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: scale must be finite", fn);
+  return DADGPT_OK;
+}
+
+int check_decode(const char* fn, int n_seq, int H, int max_len, int d_head, float scale,
+                 const void* ws, size_t ws_bytes, std::initializer_list<const void*> ptrs) {
+  if (int st = check_decode_shape(fn, n_seq, H, max_len, d_head, scale, ptrs)) return st;
   const size_t need = dadgpt::decode_workspace_bytes(n_seq, H, max_len, d_head);
   if (need > 0 && (ws == nullptr || ws_bytes < need))
     return fail(DADGPT_ERR_WORKSPACE, "%s: workspace of %zu bytes given, %zu needed", fn,

@@ -200,11 +200,36 @@ def test_decode_validation(fn):
     assert f(*args(lens=None)) == 1
     assert f(*args(n=0)) == 1
     assert f(*args(L=0)) == 1
-    assert f(*args(n=70000)) == 1
+    assert f(*args(n=1 << 22)) == 1  # 2^22 x 2 heads: 2^23 caches of 512 lanes
     assert f(*args(scale=float("nan"))) == 1
     assert f(*args(ws=None)) == 4
     assert f(*args(wsb=need - 1)) == 4
     assert "needed" in A.last_error()
+
+
+def test_decode_launch_limits():
+    """Grid limits of the decode launch: (n_seq * n_heads) workgroups of 512 lanes must count
+    fewer than 2^32 work-items, and the chunk count (256-key fp32 chunks at d_head 64) must
+    fit grid.y <= 65535; both are refused on the host."""
+    for fn in ("dadgpt_decode_attention_bf16", "dadgpt_decode_attention_f32"):
+        f = getattr(A.lib(), fn)
+        big = [FAKE, FAKE, FAKE, FAKE, FAKE]
+        assert f(*big, 1 << 12, 1 << 11, 64, 64, 0.125, None, 0, None) == 1  # 2^23 caches
+        assert "launch limits" in A.last_error()
+        assert f(*big, 1, 1, 65535 * 256 + 1, 64, 0.125, FAKE, 1 << 40, None) == 1
+        assert "launch limits" in A.last_error()
+
+
+def test_attention_launch_limits():
+    """Attention grids are (BH, ceil(S / 64)) at the smallest tile: S above 65535 * 64 and
+    BH = 2^24 (2^32 work-items of 256-lane workgroups) are refused on the host."""
+    L = A.lib()
+    f = L.dadgpt_flash_attention_forward_bf16
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 1, 65535 * 64 + 1, 64, 0.125, None) == 1
+    assert "exceeds" in A.last_error()
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 24, 1, 64, 0.125, None) == 1
+    g = L.dadgpt_flash_attention_forward
+    assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 1, 65535 * 64 + 1, 64, 0.125) == 1
 
 
 def test_cxx_reference_names_link_and_throw(tmp_path):
