@@ -44,6 +44,7 @@ C_SYMBOLS = (
     "dadgpt_flash_attention_backward_bf16_tokens",
     "dadgpt_decode_workspace_bytes",
     "dadgpt_decode_attention_bf16",
+    "dadgpt_decode_attention_bf16_noalloc",
     "dadgpt_decode_attention_f32",
 )
 CXX_SYMBOLS = (
@@ -120,6 +121,7 @@ def lib():
     L.dadgpt_decode_workspace_bytes.argtypes = [i, i, i, i]
     L.dadgpt_decode_attention_bf16.argtypes = [vp] * 5 + [i, i, i, i, f, vp, sz, vp]
     L.dadgpt_decode_attention_f32.argtypes = [vp] * 5 + [i, i, i, i, f, vp, sz, vp]
+    L.dadgpt_decode_attention_bf16_noalloc.argtypes = [vp] * 5 + [i, i, i, i, f, vp]
     _lib = L
     return L
 
@@ -387,6 +389,27 @@ def decode_attention(out, q, k_cache, v_cache, lens, n_seq, n_heads, max_len, d_
 
 
 # --------------------------------------------------------------- allocating conveniences
+
+# Scratch each device holds for decode_attention_noalloc (the header's
+# DADGPT_DECODE_NOALLOC_SCRATCH_BYTES).
+DECODE_NOALLOC_SCRATCH_BYTES = 4 << 20
+
+
+def decode_attention_noalloc(out, q, k_cache, v_cache, lens, n_seq, n_heads, max_len, d_head,
+                             scale, stream=None) -> None:
+    """bf16 decode without a workspace argument: the library's fixed per-device scratch
+    (DECODE_NOALLOC_SCRATCH_BYTES) holds the split-cache partials, so the call allocates
+    nothing. Calls that overlap in time on one device race on that scratch."""
+    dt = torch.bfloat16
+    _require(q, "q", dt, n_seq * n_heads * d_head)
+    _require(out, "out", dt, n_seq * n_heads * d_head)
+    _require(k_cache, "k_cache", dt, n_seq * n_heads * max_len * d_head)
+    _require(v_cache, "v_cache", dt, n_seq * n_heads * max_len * d_head)
+    _require(lens, "lens", torch.int32, n_seq)
+    _check(lib().dadgpt_decode_attention_bf16_noalloc(
+        _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(lens), n_seq, n_heads, max_len,
+        d_head, scale, _stream_ptr(stream)))
+
 
 def default_scale(d_head: int) -> float:
     """1/sqrt(d_head), as src/model.cpp:389 computes it (in fp32)."""

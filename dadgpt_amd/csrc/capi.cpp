@@ -155,6 +155,9 @@ dadgpt_head_strides tokens(int64_t ld, int S, int d_head) {
   return dadgpt_head_strides{ld * S, d_head, ld};
 }
 
+static_assert(DADGPT_DECODE_NOALLOC_SCRATCH_BYTES == dadgpt::kDecodeScratchBytes,
+              "the header's scratch limit must be the kernels' own");
+
 using dadgpt::bf16;
 const bf16* B(const uint16_t* p) { return reinterpret_cast<const bf16*>(p); }
 bf16* B(uint16_t* p) { return reinterpret_cast<bf16*>(p); }
@@ -403,6 +406,28 @@ int dadgpt_decode_attention_bf16(uint16_t* out, const uint16_t* q, const uint16_
   return from_hip(dadgpt::launch_decode_bf16(B(out), B(q), B(k_cache), B(v_cache), lens, n_seq,
                                              n_heads, max_len, d_head, scale, workspace,
                                              workspace_bytes, as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_decode_attention_bf16_noalloc(uint16_t* out, const uint16_t* q,
+                                         const uint16_t* k_cache, const uint16_t* v_cache,
+                                         const int32_t* lens, int n_seq, int n_heads,
+                                         int max_len, int d_head, float scale, void* stream) {
+  const char* fn = "dadgpt_decode_attention_bf16_noalloc";
+  if (int st = check_decode_shape(fn, n_seq, n_heads, max_len, d_head, scale,
+                                  {out, q, k_cache, v_cache, lens}))
+    return st;
+  const size_t need = dadgpt::decode_workspace_bytes(n_seq, n_heads, max_len, d_head);
+  if (need > dadgpt::kDecodeScratchBytes)
+    return fail(DADGPT_ERR_WORKSPACE,
+                "%s: this shape needs %zu bytes of scratch, above the fixed %zu", fn, need,
+                dadgpt::kDecodeScratchBytes);
+  void* scratch = nullptr;
+  if (hipError_t e = dadgpt::decode_scratch(&scratch, as_stream(stream)); e != hipSuccess)
+    return from_hip(e, fn);
+  return from_hip(dadgpt::launch_decode_bf16(B(out), B(q), B(k_cache), B(v_cache), lens, n_seq,
+                                             n_heads, max_len, d_head, scale, scratch,
+                                             dadgpt::kDecodeScratchBytes, as_stream(stream)),
                   fn);
 }
 

@@ -28,6 +28,8 @@
 // before the counter is incremented. No agent-scope fence is used: on this part a release
 // fence writes back the whole L2 (the L2s of the 8 XCDs are not coherent with each other),
 // which made the first fence-based version of this kernel 17x slower.
+#include <mutex>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -289,7 +291,43 @@ hipError_t launch_decode_t(T* out, const T* q, const T* kc, const T* vc, const i
   return hipErrorInvalidValue;
 }
 
+// Scratch of the allocation-free entry point: it stands in for a caller's workspace (same
+// layout: counters at the start, partials against the end) and lives as long as the code
+// object, one copy per device. In host code `scratch` names a host-side shadow, not device
+// memory: only the address hipGetSymbolAddress returns for the current device may reach a
+// kernel or a copy.
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+__global__ void zero_words_kernel(unsigned* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
 }  // namespace
+
+hipError_t decode_scratch(void** ptr, hipStream_t stream) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = -1;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    // The arrival counters must start at zero (every call leaves them at zero again). A fill
+    // kernel, not a memset node, so that a first call made under graph capture replays right.
+    zero_words_kernel<<<256, 256, 0, stream>>>(static_cast<unsigned*>(p),
+                                               kDecodeScratchBytes / sizeof(unsigned));
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  return hipSuccess;
+}
 
 size_t decode_workspace_bytes(int n_seq, int H, int max_len, int D) {
   // fp32 chunks are shorter, so the fp32 chunk count bounds the bf16 one: the size returned

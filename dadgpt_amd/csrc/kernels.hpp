@@ -96,4 +96,11 @@ hipError_t launch_decode_f32(float* out, const float* q, const float* k_cache,
                              int max_len, int D, float scale, void* workspace,
                              size_t workspace_bytes, hipStream_t stream);
 
+// Device scratch that stands in for the decode workspace in the allocation-free entry point:
+// kDecodeScratchBytes per device, held until the process ends. decode_scratch returns the
+// current device's address, looked up (and zero-filled by a kernel on `stream`) on the first
+// call on that device.
+constexpr size_t kDecodeScratchBytes = size_t(4) << 20;
+hipError_t decode_scratch(void** ptr, hipStream_t stream);
+
 }  // namespace dadgpt

@@ -221,6 +221,23 @@ int dadgpt_decode_attention_bf16(uint16_t* out, const uint16_t* q, const uint16_
                                  const uint16_t* v_cache, const int32_t* lens, int n_seq,
                                  int n_heads, int max_len, int d_head, float scale,
                                  void* workspace, size_t workspace_bytes, void* stream);
+/* Allocation-free form of dadgpt_decode_attention_bf16. It has no counterpart in the
+ * reference: it is for callers that cannot allocate or pass a workspace (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). Same arguments minus the workspace,
+ * same kernels, bit-identical results. The split-cache partials and arrival counters live in
+ * a fixed scratch region of DADGPT_DECODE_NOALLOC_SCRATCH_BYTES per device inside the library,
+ * held until the process ends; a shape whose dadgpt_decode_workspace_bytes() exceeds it is
+ * refused with DADGPT_ERR_WORKSPACE before any HIP call (for example n_seq * n_heads = 384 at
+ * d_head 64 serves max_len up to about 10,000). The first call on a device looks the region
+ * up and zero-fills it with a kernel on `stream`; every call leaves its counters at zero.
+ * Every call on one device shares the region: calls that overlap in time on one device (two
+ * streams, two threads) race and must be serialised by the caller. */
+#define DADGPT_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+int dadgpt_decode_attention_bf16_noalloc(uint16_t* out, const uint16_t* q,
+                                         const uint16_t* k_cache, const uint16_t* v_cache,
+                                         const int32_t* lens, int n_seq, int n_heads,
+                                         int max_len, int d_head, float scale, void* stream);
+
 int dadgpt_decode_attention_f32(float* out, const float* q, const float* k_cache,
                                 const float* v_cache, const int32_t* lens, int n_seq,
                                 int n_heads, int max_len, int d_head, float scale,

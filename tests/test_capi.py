@@ -232,6 +232,35 @@ def test_attention_launch_limits():
     assert g(FAKE, FAKE, FAKE, FAKE, FAKE, 1, 65535 * 64 + 1, 64, 0.125) == 1
 
 
+def test_decode_noalloc_validation():
+    """The allocation-free decode checks the shape like the workspace form and refuses, before
+    any HIP call, a shape whose split partials would not fit the fixed per-device scratch."""
+    f = A.lib().dadgpt_decode_attention_bf16_noalloc
+    args = lambda **kw: [kw.get("out", FAKE), FAKE, FAKE, FAKE, kw.get("lens", FAKE),
+                         kw.get("n", 32), kw.get("h", 12), kw.get("L", 1024), kw.get("d", 64),
+                         kw.get("scale", 0.125), None]
+    assert f(*args(d=48)) == 2
+    assert f(*args(out=None)) == 1
+    assert f(*args(lens=None)) == 1
+    assert f(*args(n=0)) == 1
+    assert f(*args(scale=float("inf"))) == 1
+    limit = A.DECODE_NOALLOC_SCRATCH_BYTES
+    # the largest max_len that fits at 32 x 12 caches, d_head 64, and the next chunk beyond it
+    fits = max(L for L in range(256, 20000, 256) if expected_ws(32, 12, L, 64) <= limit)
+    assert expected_ws(32, 12, fits + 1, 64) > limit
+    assert f(*args(L=fits + 1)) == 4
+    assert "scratch" in A.last_error() and str(limit) in A.last_error()
+    assert f(*args(n=1 << 12, h=1 << 11)) == 1  # launch limit before the scratch check
+
+
+def test_decode_noalloc_limit_matches_header():
+    text = open(HEADER).read()
+    m = re.search(r"#define DADGPT_DECODE_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)",
+                  text)
+    assert m, "scratch limit macro not found"
+    assert int(m.group(1)) << int(m.group(2)) == A.DECODE_NOALLOC_SCRATCH_BYTES
+
+
 def test_cxx_reference_names_link_and_throw(tmp_path):
     """A C++ caller using the reference's names/signatures links and gets the reference's
     exceptions (built with g++ here; needs no GPU)."""
