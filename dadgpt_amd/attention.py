@@ -46,11 +46,26 @@ C_SYMBOLS = (
     "dadgpt_decode_attention_bf16",
     "dadgpt_decode_attention_bf16_noalloc",
     "dadgpt_decode_attention_f32",
+    "dadgpt_softmax",
+    "dadgpt_softmax_backward",
+    "dadgpt_causal_mask",
+    "dadgpt_causal_mask_zero",
+    "dadgpt_scale",
+    "dadgpt_attention_probs",
+    "dadgpt_attention_probs_backward",
+    "dadgpt_decode_probs",
+    "dadgpt_use_fused_attention",
 )
 CXX_SYMBOLS = (
     "_Z29gpu_flash_attention_supportedi",
     "_Z27gpu_flash_attention_forwardPfS_PKfS1_S1_iiif",
     "_Z28gpu_flash_attention_backwardPfS_S_S_PKfS1_S1_S1_S1_S1_iiif",
+    "_Z11gpu_softmaxPfPKfii",
+    "_Z20gpu_softmax_backwardPfPKfS1_ii",
+    "_Z15gpu_causal_maskPfii",
+    "_Z20gpu_causal_mask_zeroPfii",
+    "_Z9gpu_scalePfif",
+    "_Z19use_fused_attention13AttentionImpliib",
 )
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported", 3: "hip error", 4: "workspace"}
@@ -122,6 +137,15 @@ def lib():
     L.dadgpt_decode_attention_bf16.argtypes = [vp] * 5 + [i, i, i, i, f, vp, sz, vp]
     L.dadgpt_decode_attention_f32.argtypes = [vp] * 5 + [i, i, i, i, f, vp, sz, vp]
     L.dadgpt_decode_attention_bf16_noalloc.argtypes = [vp] * 5 + [i, i, i, i, f, vp]
+    L.dadgpt_softmax.argtypes = [vp, vp, i, i, vp]
+    L.dadgpt_softmax_backward.argtypes = [vp, vp, vp, i, i, vp]
+    L.dadgpt_causal_mask.argtypes = [vp, i, i, vp]
+    L.dadgpt_causal_mask_zero.argtypes = [vp, i, i, vp]
+    L.dadgpt_scale.argtypes = [vp, i64, f, vp]
+    L.dadgpt_attention_probs.argtypes = [vp, i, i, f, vp]
+    L.dadgpt_attention_probs_backward.argtypes = [vp, vp, vp, i, i, f, vp]
+    L.dadgpt_decode_probs.argtypes = [vp, vp, i, i, i, f, vp]
+    L.dadgpt_use_fused_attention.argtypes = [i, i, i, i]
     _lib = L
     return L
 
@@ -409,6 +433,76 @@ def decode_attention_noalloc(out, q, k_cache, v_cache, lens, n_seq, n_heads, max
     _check(lib().dadgpt_decode_attention_bf16_noalloc(
         _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(lens), n_seq, n_heads, max_len,
         d_head, scale, _stream_ptr(stream)))
+
+
+# ---------------------------------------------------------------- materialized attention
+
+# The reference's AttentionImpl (src/model.hpp:80).
+ATTENTION_IMPL = {"auto": 0, "fused": 1, "materialized": 2}
+
+
+def use_fused_attention(impl: str, d_head: int, ctx_len: int, attn_dropout: bool) -> bool:
+    """use_fused_attention (src/model.cpp:183-197): dropout or an unsupported d_head take the
+    materialized path; 'fused' / 'materialized' force theirs; 'auto' is fused from ctx 512."""
+    return bool(lib().dadgpt_use_fused_attention(ATTENTION_IMPL[impl], d_head, ctx_len,
+                                                 int(bool(attn_dropout))))
+
+
+def _rows(t, name, numel):
+    _require(t, name, torch.float32, numel)
+
+
+def softmax(out, x, rows: int, cols: int, stream=None) -> None:
+    """gpu_softmax (cuda/gpu_ops.cu:147-199): row softmax of x [rows, cols] into out."""
+    _rows(out, "out", rows * cols)
+    _rows(x, "in", rows * cols)
+    _check(lib().dadgpt_softmax(_ptr(out), _ptr(x), rows, cols, _stream_ptr(stream)))
+
+
+def softmax_backward(din, dout, out, rows: int, cols: int, stream=None) -> None:
+    """gpu_softmax_backward (cuda/gpu_ops.cu:542-569): din += out (dout - rowsum(dout out))."""
+    for t, n in ((din, "din"), (dout, "dout"), (out, "out")):
+        _rows(t, n, rows * cols)
+    _check(lib().dadgpt_softmax_backward(_ptr(din), _ptr(dout), _ptr(out), rows, cols,
+                                         _stream_ptr(stream)))
+
+
+def causal_mask(scores, n_blocks: int, S: int, zero: bool = False, stream=None) -> None:
+    """gpu_causal_mask (-1e9) or gpu_causal_mask_zero (0) above each block's diagonal
+    (cuda/gpu_ops.cu:476-511)."""
+    _rows(scores, "scores", n_blocks * S * S)
+    fn = lib().dadgpt_causal_mask_zero if zero else lib().dadgpt_causal_mask
+    _check(fn(_ptr(scores), n_blocks, S, _stream_ptr(stream)))
+
+
+def scale_(x, scale: float, stream=None) -> None:
+    """gpu_scale (cuda/gpu_ops.cu:513-525): x *= scale in place."""
+    _rows(x, "data", x.numel())
+    _check(lib().dadgpt_scale(_ptr(x), x.numel(), scale, _stream_ptr(stream)))
+
+
+def attention_probs(probs, BH: int, S: int, scale: float, stream=None) -> None:
+    """Scores [BH,S,S] -> probabilities in place (x scale, causal -1e9, row softmax)."""
+    _rows(probs, "probs", BH * S * S)
+    _check(lib().dadgpt_attention_probs(_ptr(probs), BH, S, scale, _stream_ptr(stream)))
+
+
+def attention_probs_backward(dscores, dprobs, probs, BH: int, S: int, scale: float,
+                             stream=None) -> None:
+    """d(scores) from d(probs) and probs (softmax backward, causal zero, x scale)."""
+    for t, n in ((dscores, "dscores"), (dprobs, "dprobs"), (probs, "probs")):
+        _rows(t, n, BH * S * S)
+    _check(lib().dadgpt_attention_probs_backward(_ptr(dscores), _ptr(dprobs), _ptr(probs), BH, S,
+                                                 scale, _stream_ptr(stream)))
+
+
+def decode_probs(probs, lens, n_seq: int, n_heads: int, max_len: int, scale: float,
+                 stream=None) -> None:
+    """Decode scores [n_seq*H, max_len] -> probabilities over each sequence's first lens keys."""
+    _rows(probs, "probs", n_seq * n_heads * max_len)
+    _require(lens, "lens", torch.int32, n_seq)
+    _check(lib().dadgpt_decode_probs(_ptr(probs), _ptr(lens), n_seq, n_heads, max_len, scale,
+                                     _stream_ptr(stream)))
 
 
 def default_scale(d_head: int) -> float:

@@ -103,6 +103,36 @@ int check_decode(const char* fn, int n_seq, int H, int max_len, int d_head, floa
   return DADGPT_OK;
 }
 
+// Row kernels of the materialized path: fp32 [rows, cols] matrices, 4-byte aligned, one wave
+// per row (rows / 4 workgroups of 256 lanes: rows * 64 work-items < 2^32).
+int check_rows(const char* fn, long long rows, long long cols,
+               std::initializer_list<const void*> ptrs) {
+  int i = 0;
+  for (const void* p : ptrs) {
+    if (p == nullptr)
+      return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: pointer argument %d is null", fn, i);
+    if (reinterpret_cast<uintptr_t>(p) % 4 != 0)
+      return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: pointer argument %d is not 4-byte aligned",
+                  fn, i);
+    ++i;
+  }
+  if (rows < 1 || cols < 1)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: rows=%lld and cols=%lld must be positive", fn,
+                rows, cols);
+  if (rows >= (1LL << 26) || cols > kMaxRows)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: rows=%lld x cols=%lld exceeds the launch limits",
+                fn, rows, cols);
+  return DADGPT_OK;
+}
+
+// n_blocks square S x S blocks ([BH, S, S] scores).
+int check_blocks(const char* fn, int n_blocks, int S, const void* p) {
+  if (n_blocks < 1 || S < 1)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: n_blocks=%d and S=%d must be positive", fn,
+                n_blocks, S);
+  return check_rows(fn, (long long)n_blocks * S, S, {p});
+}
+
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 int check_dropout(const char* fn, float p) {
@@ -429,6 +459,90 @@ int dadgpt_decode_attention_bf16_noalloc(uint16_t* out, const uint16_t* q,
                                              n_heads, max_len, d_head, scale, scratch,
                                              dadgpt::kDecodeScratchBytes, as_stream(stream)),
                   fn);
+}
+
+// ---- materialized attention path ----
+
+int dadgpt_softmax(float* out, const float* in, int rows, int cols, void* stream) {
+  const char* fn = "dadgpt_softmax";
+  if (int st = check_rows(fn, rows, cols, {out, in})) return st;
+  return from_hip(dadgpt::launch_softmax_rows(out, in, rows, cols, as_stream(stream)), fn);
+}
+
+int dadgpt_softmax_backward(float* din, const float* dout, const float* out, int rows, int cols,
+                            void* stream) {
+  const char* fn = "dadgpt_softmax_backward";
+  if (int st = check_rows(fn, rows, cols, {din, dout, out})) return st;
+  return from_hip(
+      dadgpt::launch_softmax_backward_rows(din, dout, out, rows, cols, as_stream(stream)), fn);
+}
+
+int dadgpt_causal_mask(float* scores, int n_blocks, int S, void* stream) {
+  const char* fn = "dadgpt_causal_mask";
+  if (int st = check_blocks(fn, n_blocks, S, scores)) return st;
+  return from_hip(dadgpt::launch_causal_fill(scores, n_blocks, S, -1e9f, as_stream(stream)), fn);
+}
+
+int dadgpt_causal_mask_zero(float* grads, int n_blocks, int S, void* stream) {
+  const char* fn = "dadgpt_causal_mask_zero";
+  if (int st = check_blocks(fn, n_blocks, S, grads)) return st;
+  return from_hip(dadgpt::launch_causal_fill(grads, n_blocks, S, 0.0f, as_stream(stream)), fn);
+}
+
+int dadgpt_scale(float* data, int64_t count, float scale, void* stream) {
+  const char* fn = "dadgpt_scale";
+  if (data == nullptr) return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: data is null", fn);
+  if (count < 0) return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: count %lld < 0", fn,
+                             (long long)count);
+  if (count == 0) return ok();
+  return from_hip(dadgpt::launch_scale(data, count, scale, as_stream(stream)), fn);
+}
+
+int dadgpt_attention_probs(float* probs, int BH, int S, float scale, void* stream) {
+  const char* fn = "dadgpt_attention_probs";
+  if (int st = check_blocks(fn, BH, S, probs)) return st;
+  if (!std::isfinite(scale))
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: scale must be finite", fn);
+  return from_hip(dadgpt::launch_attention_probs(probs, BH, S, scale, as_stream(stream)), fn);
+}
+
+int dadgpt_attention_probs_backward(float* dscores, const float* dprobs, const float* probs,
+                                    int BH, int S, float scale, void* stream) {
+  const char* fn = "dadgpt_attention_probs_backward";
+  if (int st = check_blocks(fn, BH, S, dscores)) return st;
+  if (int st = check_blocks(fn, BH, S, dprobs)) return st;
+  if (int st = check_blocks(fn, BH, S, probs)) return st;
+  if (!std::isfinite(scale))
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: scale must be finite", fn);
+  return from_hip(dadgpt::launch_attention_probs_backward(dscores, dprobs, probs, BH, S, scale,
+                                                          as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_decode_probs(float* probs, const int32_t* lens, int n_seq, int n_heads, int max_len,
+                        float scale, void* stream) {
+  const char* fn = "dadgpt_decode_probs";
+  if (probs == nullptr || lens == nullptr)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: null pointer argument", fn);
+  if (n_seq < 1 || n_heads < 1 || max_len < 1)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                "%s: n_seq=%d, n_heads=%d, max_len=%d must be positive", fn, n_seq, n_heads,
+                max_len);
+  if (int st = check_rows(fn, (long long)n_seq * n_heads, max_len, {probs})) return st;
+  if (!std::isfinite(scale))
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: scale must be finite", fn);
+  return from_hip(dadgpt::launch_decode_probs(probs, lens, n_seq, n_heads, max_len, scale,
+                                              as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_use_fused_attention(int impl, int d_head, int ctx_len, int attn_dropout) {
+  // src/model.cpp:185-197: dropout or an unsupported head size forces the materialized path;
+  // otherwise the selected implementation, and Auto picks fused from a context of 512 up.
+  if (attn_dropout || !supported(d_head)) return 0;
+  if (impl == DADGPT_ATTENTION_FUSED) return 1;
+  if (impl == DADGPT_ATTENTION_MATERIALIZED) return 0;
+  return ctx_len >= 512 ? 1 : 0;
 }
 
 int dadgpt_decode_attention_f32(float* out, const float* q, const float* k_cache,

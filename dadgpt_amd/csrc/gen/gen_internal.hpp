@@ -21,6 +21,25 @@ int check_hip(hipError_t e, const char* what);
 int gemm(dadgpt_blas* h, float* out, const bf16* a, const bf16* b, int M, int K, int N,
          bool trans_b, hipStream_t stream);
 
+// fp32 row-major GEMM (blaslt.cpp): out[M,N] = op(a) op(b) + beta out over `count` matrices
+// sa/sb/sc elements apart; op 'N', 'A' (a [K,M] transposed) or 'B' (b [N,K] transposed); the
+// multiply precision is the process-wide one (dadgpt_set_matmul_precision).
+int gemm_f32(dadgpt_blas* h, float* out, const float* a, const float* b, int M, int K, int N,
+             char op, float beta, int count, long long sa, long long sb, long long sc,
+             hipStream_t stream);
+
+// Materialized attention (materialized_attn.cpp). Forward over BH heads whose q / k and v /
+// out slices start stride_q / stride_kv / stride_o elements apart (rows of dh contiguous);
+// probs [BH, S, S] is written. Decode: scores over each cache's max_len rows masked by
+// lens[seq] (device), probs [n_seq * H, max_len] scratch, out [n_seq, H, dh].
+int materialized_forward(dadgpt_blas* h, float* out, float* probs, const float* q,
+                         const float* k, const float* v, int BH, int S, int dh, float scale,
+                         long long stride_q, long long stride_kv, long long stride_o,
+                         hipStream_t s);
+int materialized_decode(dadgpt_blas* h, float* out, float* probs, const float* q,
+                        const float* kcache, const float* vcache, const int* lens, int n_seq,
+                        int H, int max_len, int dh, float scale, hipStream_t s);
+
 // ---- kernels (gpt2_ops.hip); every launcher returns hipGetLastError() ----
 
 // p[i] = bf16(std * N(0,1)) from a counter-based splitmix64/Box-Muller stream of `seed`.

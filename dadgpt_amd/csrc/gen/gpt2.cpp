@@ -119,7 +119,8 @@ struct dadgpt_gpt2 {
   Offsets off;
   const bf16* params = nullptr;
   int max_batch = 0;
-  bool fp32 = false;
+  bool fp32 = false;          // fp32 Q/K/V, caches and attention (modes 1 and 2)
+  bool materialized = false;  // mode 2: the materialized path (GEMMs + row softmax)
   int dh = 0;
   size_t esz = 2;  // bytes per attention element (Q/K/V, caches, attention output)
   dadgpt_blas* blas = nullptr;
@@ -135,6 +136,7 @@ struct dadgpt_gpt2 {
 
   float *x = nullptr, *qkv = nullptr, *y = nullptr, *f = nullptr, *xl = nullptr;
   float *logits = nullptr, *lse = nullptr, *pick = nullptr;
+  float* probs = nullptr;  // materialized mode: [max_batch * H, ctx, ctx] probabilities
   bf16 *h = nullptr, *a = nullptr, *g = nullptr;
   void *qh = nullptr, *kh = nullptr, *vh = nullptr, *ao = nullptr;
   void* ws = nullptr;
@@ -170,6 +172,12 @@ namespace {
 // token-major into m->a, the Wo GEMM's input: no split K/V copies and no merge pass.
 int attention_prefill(dadgpt_gpt2* m, int layer, int n, int S, float scale) {
   const int H = m->c.n_heads, dh = m->dh;
+  if (m->materialized) {
+    const long long sl = (long long)S * dh;
+    return materialized_forward(m->blas, (float*)m->ao, m->probs, (const float*)m->qh,
+                                (const float*)m->kh, (const float*)m->vh, n * H, S, dh, scale,
+                                sl, sl, sl, m->stream);
+  }
   if (m->fp32)
     return dadgpt_flash_attention_forward_async((float*)m->ao, m->lse, (const float*)m->qh,
                                                 (const float*)m->kh, (const float*)m->vh, n * H,
@@ -185,6 +193,10 @@ int attention_prefill(dadgpt_gpt2* m, int layer, int n, int S, float scale) {
 
 int attention_decode(dadgpt_gpt2* m, int layer, int n, float scale) {
   const int H = m->c.n_heads, L = m->c.ctx_len;
+  if (m->materialized)
+    return materialized_decode(m->blas, (float*)m->ao, m->probs, (const float*)m->qh,
+                               (const float*)m->kc[layer], (const float*)m->vc[layer],
+                               m->cache_len, n, H, L, m->dh, scale, m->stream);
   if (m->fp32)
     return dadgpt_decode_attention_f32((float*)m->ao, (const float*)m->qh,
                                        (const float*)m->kc[layer], (const float*)m->vc[layer],
@@ -196,8 +208,10 @@ int attention_decode(dadgpt_gpt2* m, int layer, int n, float scale) {
                                       m->dh, scale, m->ws, m->ws_bytes, m->stream);
 }
 
-// The attention error of the C ABI is recorded by libdadgpt_attn; carry it over.
-int attn_fail(int st, const char* what) {
+// The attention error of the C ABI is recorded by libdadgpt_attn; carry it over (the
+// materialized path records its own, in this library).
+int attn_fail(const dadgpt_gpt2* m, int st, const char* what) {
+  if (m->materialized) return st;
   return fail(st, "%s: %s", what, dadgpt_last_error());
 }
 
@@ -232,7 +246,7 @@ int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev
                               s),
               "qkv_split");
     if (int st = attention_prefill(m, l, n, S, scale))
-      return attn_fail(st, "prefill attention");
+      return attn_fail(m, st, "prefill attention");
     if (m->fp32)
       TRY_HIP(merge_heads<float>(m->a, (const float*)m->ao, n, S, H, dh, s), "merge_heads");
   } else {
@@ -247,7 +261,7 @@ int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev
                               s),
               "qkv_split");
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[0], s), "hipEventRecord");
-    if (int st = attention_decode(m, l, n, scale)) return attn_fail(st, "decode attention");
+    if (int st = attention_decode(m, l, n, scale)) return attn_fail(m, st, "decode attention");
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[1], s), "hipEventRecord");
     // decode output [n, H, dh] is already the [n, d] row layout
     if (m->fp32)
@@ -338,7 +352,7 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
     q.H = H, q.dh = dh, q.max_len = c.ctx_len, q.qkv_fp32 = m->fp32;
     TRY_HIP(skinny_gemm(kProLn, kEpiQkv, q, s), "skinny QKV");
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[2 * l], s), "hipEventRecord");
-    if (int st = attention_decode(m, l, n, scale)) return attn_fail(st, "decode attention");
+    if (int st = attention_decode(m, l, n, scale)) return attn_fail(m, st, "decode attention");
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[2 * l + 1], s), "hipEventRecord");
     const bf16* attn_in = m->a;
     if (m->fp32)
@@ -486,18 +500,20 @@ void dadgpt_gpt2_destroy(dadgpt_gpt2* m) {
 }
 
 int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params, int max_batch,
-                       int attn_fp32, dadgpt_gpt2** out) {
-  if (!out || !params || !config_ok(config) || max_batch < 1 || config->d_model > 2048)
+                       int attn_mode, dadgpt_gpt2** out) {
+  if (!out || !params || !config_ok(config) || max_batch < 1 || config->d_model > 2048 ||
+      attn_mode < DADGPT_GPT2_ATTN_BF16 || attn_mode > DADGPT_GPT2_ATTN_FP32_MATERIALIZED)
     return fail(DADGPT_ERR_INVALID_ARGUMENT,
                 "dadgpt_gpt2_create: bad arguments (d_head must be 32 or 64, d_model <= 2048, "
-                "max_batch >= 1)");
+                "max_batch >= 1, attn_mode 0, 1 or 2)");
   *out = nullptr;
   auto* m = new dadgpt_gpt2();
   m->c = *config;
   m->off = offsets_of(m->c);
   m->params = reinterpret_cast<const bf16*>(params);
   m->max_batch = max_batch;
-  m->fp32 = attn_fp32 != 0;
+  m->fp32 = attn_mode != DADGPT_GPT2_ATTN_BF16;
+  m->materialized = attn_mode == DADGPT_GPT2_ATTN_FP32_MATERIALIZED;
   m->dh = m->c.d_model / m->c.n_heads;
   m->esz = m->fp32 ? sizeof(float) : sizeof(bf16);
   const auto& c = m->c;
@@ -563,7 +579,11 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       (st = m->alloc_n(&m->cur_pos, max_batch, "cur_pos")) ||
       (st = m->alloc_n(&m->cache_len, max_batch, "cache_len")) ||
       (st = m->alloc_n(&m->out_tok, rows, "tokens out")) ||
-      (st = m->alloc_n(&m->out_margin, rows, "margins out")))
+      (st = m->alloc_n(&m->out_margin, rows, "margins out")) ||
+      // materialized attention: the prefill's [n*H, S, S] probabilities (the decode's
+      // [n*H, ctx] rows fit in the same buffer)
+      (m->materialized && (st = m->alloc_n(&m->probs, rows * c.n_heads * c.ctx_len,
+                                           "attention probabilities"))))
     return bail(st);
   // the skinny decode path: reduction lengths the kernels are built for, LayerNorm rows that
   // fit the prologue's registers

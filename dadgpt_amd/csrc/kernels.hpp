@@ -96,6 +96,25 @@ hipError_t launch_decode_f32(float* out, const float* q, const float* k_cache,
                              int max_len, int D, float scale, void* workspace,
                              size_t workspace_bytes, hipStream_t stream);
 
+// Row kernels of the materialized attention path (materialized.hip), fp32 [rows, cols]:
+// the reference's softmax (out may be in), softmax backward (din += p (dout - rowsum(dout p))),
+// causal fill of n_blocks S x S blocks (value above the diagonal) and scale; and the fused
+// chains: attention_probs turns raw scores [BH, S, S] into probabilities in place (x scale,
+// causal mask, softmax), attention_probs_backward writes d(scores) from d(probs) and probs
+// (softmax backward, causal zero, x scale; ds may be dp), decode_probs turns decode scores
+// [n_seq * H, max_len] into probabilities over each sequence's first lens[seq] keys.
+hipError_t launch_softmax_rows(float* out, const float* in, long long rows, int cols,
+                               hipStream_t stream);
+hipError_t launch_softmax_backward_rows(float* din, const float* dout, const float* p,
+                                        long long rows, int cols, hipStream_t stream);
+hipError_t launch_causal_fill(float* m, int n_blocks, int S, float value, hipStream_t stream);
+hipError_t launch_scale(float* x, long long n, float scale, hipStream_t stream);
+hipError_t launch_attention_probs(float* p, int BH, int S, float scale, hipStream_t stream);
+hipError_t launch_attention_probs_backward(float* ds, const float* dp, const float* p, int BH,
+                                           int S, float scale, hipStream_t stream);
+hipError_t launch_decode_probs(float* p, const int* lens, int n_seq, int H, int max_len,
+                               float scale, hipStream_t stream);
+
 // Device scratch that stands in for the decode workspace in the allocation-free entry point:
 // kDecodeScratchBytes per device, held until the process ends. decode_scratch returns the
 // current device's address, looked up (and zero-filled by a kernel on `stream`) on the first

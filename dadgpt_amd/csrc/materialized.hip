@@ -1,0 +1,204 @@
+// Row kernels of the materialized attention path (the [BH, S, S] probability matrix in HBM):
+// the reference's own elementwise operators, and one-pass fusions of the chains it runs
+// between its batched GEMMs (src/model.cpp:395-420 forward, :575-616 backward, :765-790
+// decode).
+//
+// Every kernel walks rows with one wave per row (four rows per 256-lane workgroup); a lane
+// holds columns lane, lane + 64, ... (16-byte pieces 4 floats wide when the row allows), so
+// each load instruction of a wave covers 256 or 1024 contiguous bytes. Row maxima and sums
+// are wave reductions through lane shuffles. The matrices are fp32, as the reference's.
+//
+// Arithmetic order per element follows the reference's operators: scores are multiplied by
+// the scale, then masked to -1e9 (src/model.cpp:407-408; cuda/gpu_ops.cu:476-525), the
+// softmax subtracts the row max, exponentiates with expf and divides by the row sum
+// (cuda/gpu_ops.cu:147-193), and the softmax backward is p * (dp - sum(dp * p))
+// (cuda/gpu_ops.cu:542-563), masked, then scaled (src/model.cpp:601-607). Only the order of
+// the row sums differs (a wave tree instead of a block tree).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace dadgpt {
+namespace {
+
+constexpr int kRowsPerBlock = 4;
+constexpr float kMaskValue = -1e9f;  // cuda/gpu_ops.cu:482
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+template <int V, typename F>
+__device__ __forceinline__ void read_row(const float* row, int cols, int lane, F f) {
+  if constexpr (V == 4) {
+    for (int c = lane * 4; c < cols; c += 256) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(row + c);
+      f(c, v.x), f(c + 1, v.y), f(c + 2, v.z), f(c + 3, v.w);
+    }
+  } else {
+    for (int c = lane; c < cols; c += 64) f(c, row[c]);
+  }
+}
+
+// What a softmax row sees of its input: the raw value (kPlain), scale then causal mask
+// (kCausal: row r of a head is query r % S), or scale then a length mask (kLength: keys at or
+// past lens[r / H] are masked; an empty cache gives a zero row).
+enum RowMode { kPlain, kCausal, kLength };
+
+template <int MODE, int V>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void softmax_rows_kernel(
+    float* out, const float* in, long long rows, int cols, int S,
+    float scale, const int* __restrict__ lens, int H) {
+  const int lane = threadIdx.x & 63;
+  const long long r = (long long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* src = in + r * cols;
+  float* dst = out + r * cols;
+  int limit = cols;  // columns at or past `limit` are masked
+  if constexpr (MODE == kCausal) limit = (int)(r % S) + 1;
+  if constexpr (MODE == kLength) {
+    const int L = lens[r / H];
+    limit = L < 0 ? 0 : (L > cols ? cols : L);
+    if (limit == 0) {  // no keys: a zero row (o = 0, as the decode kernel returns)
+      for (int c = lane; c < cols; c += 64) dst[c] = 0.f;
+      return;
+    }
+  }
+  auto value = [&](int c, float x) {
+    if constexpr (MODE == kPlain) return x;
+    const float s = x * scale;
+    return c < limit ? s : kMaskValue;
+  };
+  float mx = -1e30f;  // the reference's initial max (cuda/gpu_ops.cu:156)
+  read_row<V>(src, cols, lane, [&](int c, float x) { mx = fmaxf(mx, value(c, x)); });
+  mx = wave_max(mx);
+  float sum = 0.f;
+  read_row<V>(src, cols, lane, [&](int c, float x) { sum += expf(value(c, x) - mx); });
+  sum = wave_sum(sum);
+  // in == out is allowed: each lane writes exactly the columns it reads, after reading them
+  if constexpr (V == 4) {
+    for (int c = lane * 4; c < cols; c += 256) {
+      f32x4 v = *reinterpret_cast<const f32x4*>(src + c);
+      v.x = expf(value(c, v.x) - mx) / sum;
+      v.y = expf(value(c + 1, v.y) - mx) / sum;
+      v.z = expf(value(c + 2, v.z) - mx) / sum;
+      v.w = expf(value(c + 3, v.w) - mx) / sum;
+      *reinterpret_cast<f32x4*>(dst + c) = v;
+    }
+  } else {
+    for (int c = lane; c < cols; c += 64) dst[c] = expf(value(c, src[c]) - mx) / sum;
+  }
+}
+
+// Softmax backward per row: g = p * (dp - sum_j dp_j p_j). ACCUMULATE: din += g (the
+// reference's operator). Otherwise the attention form: din = g, zero past the causal
+// diagonal, times scale (din may be dout).
+template <bool ACCUMULATE>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void softmax_backward_rows_kernel(
+    float* din, const float* dout, const float* __restrict__ p, long long rows, int cols, int S,
+    float scale) {
+  const int lane = threadIdx.x & 63;
+  const long long r = (long long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* g = dout + r * cols;
+  const float* pr = p + r * cols;
+  float* d = din + r * cols;
+  float dot = 0.f;
+  for (int c = lane; c < cols; c += 64) dot += g[c] * pr[c];
+  dot = wave_sum(dot);
+  const int limit = ACCUMULATE ? cols : (int)(r % S) + 1;
+  for (int c = lane; c < cols; c += 64) {
+    const float v = pr[c] * (g[c] - dot);
+    if constexpr (ACCUMULATE)
+      d[c] += v;
+    else
+      d[c] = c < limit ? v * scale : 0.0f;
+  }
+}
+
+// scores[h][i][j] = value for j > i over n_blocks blocks of S x S.
+__global__ void causal_fill_kernel(float* __restrict__ m, long long rows, int S, float value) {
+  const long long r = (long long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  float* row = m + r * S;
+  for (int c = (int)(r % S) + 1 + (threadIdx.x & 63); c < S; c += 64) row[c] = value;
+}
+
+__global__ void scale_kernel(float* __restrict__ x, long long n, float scale) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (long long)gridDim.x * blockDim.x)
+    x[i] *= scale;
+}
+
+unsigned row_blocks(long long rows) {
+  return (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+}
+
+bool vec4(const void* a, const void* b, int cols) {
+  return cols % 4 == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(b) % 16 == 0;
+}
+
+template <int MODE>
+hipError_t launch_softmax(float* out, const float* in, long long rows, int cols, int S,
+                          float scale, const int* lens, int H, hipStream_t stream) {
+  if (vec4(out, in, cols))
+    softmax_rows_kernel<MODE, 4><<<row_blocks(rows), 64 * kRowsPerBlock, 0, stream>>>(
+        out, in, rows, cols, S, scale, lens, H);
+  else
+    softmax_rows_kernel<MODE, 1><<<row_blocks(rows), 64 * kRowsPerBlock, 0, stream>>>(
+        out, in, rows, cols, S, scale, lens, H);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_softmax_rows(float* out, const float* in, long long rows, int cols,
+                               hipStream_t stream) {
+  return launch_softmax<kPlain>(out, in, rows, cols, 1, 1.0f, nullptr, 1, stream);
+}
+
+hipError_t launch_softmax_backward_rows(float* din, const float* dout, const float* p,
+                                        long long rows, int cols, hipStream_t stream) {
+  softmax_backward_rows_kernel<true><<<row_blocks(rows), 64 * kRowsPerBlock, 0, stream>>>(
+      din, dout, p, rows, cols, 1, 1.0f);
+  return hipGetLastError();
+}
+
+hipError_t launch_causal_fill(float* m, int n_blocks, int S, float value, hipStream_t stream) {
+  const long long rows = (long long)n_blocks * S;
+  causal_fill_kernel<<<row_blocks(rows), 64 * kRowsPerBlock, 0, stream>>>(m, rows, S, value);
+  return hipGetLastError();
+}
+
+hipError_t launch_scale(float* x, long long n, float scale, hipStream_t stream) {
+  const long long blocks = (n + 255) / 256;
+  scale_kernel<<<(unsigned)(blocks < 8192 ? blocks : 8192), 256, 0, stream>>>(x, n, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_probs(float* p, int BH, int S, float scale, hipStream_t stream) {
+  return launch_softmax<kCausal>(p, p, (long long)BH * S, S, S, scale, nullptr, 1, stream);
+}
+
+hipError_t launch_attention_probs_backward(float* ds, const float* dp, const float* p, int BH,
+                                           int S, float scale, hipStream_t stream) {
+  const long long rows = (long long)BH * S;
+  softmax_backward_rows_kernel<false><<<row_blocks(rows), 64 * kRowsPerBlock, 0, stream>>>(
+      ds, dp, p, rows, S, S, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_probs(float* p, const int* lens, int n_seq, int H, int max_len,
+                               float scale, hipStream_t stream) {
+  return launch_softmax<kLength>(p, p, (long long)n_seq * H, max_len, 1, scale, lens, H,
+                                 stream);
+}
+
+}  // namespace dadgpt

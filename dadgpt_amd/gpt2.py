@@ -28,10 +28,18 @@ PRESETS = {
 
 GEN_SYMBOLS = (
     "dadgpt_gen_last_error",
+    "dadgpt_blas_open",
     "dadgpt_blas_create",
     "dadgpt_blas_destroy",
+    "dadgpt_blas_library_version",
+    "dadgpt_set_matmul_precision",
+    "dadgpt_get_matmul_precision",
     "dadgpt_matmul_bf16",
     "dadgpt_matmul_transposed_b_bf16",
+    "dadgpt_matmul_f32",
+    "dadgpt_matmul_f32_strided_batched",
+    "dadgpt_attention_materialized_forward",
+    "dadgpt_attention_materialized_backward",
     "dadgpt_gpt2_param_count",
     "dadgpt_gpt2_init_params",
     "dadgpt_gpt2_create",
@@ -81,11 +89,21 @@ def gen_lib():
     cfgp = ctypes.POINTER(Config)
     L.dadgpt_gen_last_error.restype = ctypes.c_char_p
     L.dadgpt_gen_last_error.argtypes = []
+    L.dadgpt_blas_open.argtypes = []
     L.dadgpt_blas_create.argtypes = [ctypes.POINTER(vp)]
     L.dadgpt_blas_destroy.argtypes = [vp]
     L.dadgpt_blas_destroy.restype = None
     L.dadgpt_matmul_bf16.argtypes = [vp, vp, vp, vp, i, i, i, vp]
     L.dadgpt_matmul_transposed_b_bf16.argtypes = [vp, vp, vp, vp, i, i, i, vp]
+    ll = ctypes.c_longlong
+    L.dadgpt_blas_library_version.argtypes = [vp]
+    L.dadgpt_set_matmul_precision.argtypes = [i]
+    L.dadgpt_get_matmul_precision.argtypes = []
+    L.dadgpt_matmul_f32.argtypes = [vp, vp, vp, vp, i, i, i, i, f, vp]
+    L.dadgpt_matmul_f32_strided_batched.argtypes = [vp, vp, vp, vp, i, i, i, i, f, ll, ll, ll, i,
+                                                    vp]
+    L.dadgpt_attention_materialized_forward.argtypes = [vp] * 6 + [i, i, i, f, vp]
+    L.dadgpt_attention_materialized_backward.argtypes = [vp] * 10 + [i, i, i, f, vp]
     L.dadgpt_gpt2_param_count.argtypes = [cfgp]
     L.dadgpt_gpt2_param_count.restype = sz
     L.dadgpt_gpt2_init_params.argtypes = [vp, cfgp, ctypes.c_uint64, vp]
@@ -116,6 +134,21 @@ def _stream():
 
 
 # ------------------------------------------------------------------------------ GEMMs
+
+# The reference's MatmulPrecision (cuda/gpu_ops.cuh:43), process-wide.
+PRECISIONS = {"fp32": 0, "tf32": 1, "bf16": 2}
+
+
+def set_matmul_precision(name: str) -> None:
+    """gpu_set_matmul_precision (cuda/gpu_ops.cu:63-67) for the fp32 GEMMs below: 'fp32',
+    'tf32' (runs as fp32 on gfx950) or 'bf16' (inputs rounded to bf16 inside the GEMM)."""
+    _check(gen_lib().dadgpt_set_matmul_precision(PRECISIONS[name]))
+
+
+def get_matmul_precision() -> str:
+    v = gen_lib().dadgpt_get_matmul_precision()
+    return {k: n for n, k in PRECISIONS.items()}[v]
+
 
 class Blas:
     """An opaque hipBLASLt handle (the reference's cublasHandle_t, src/model.cpp:236)."""
@@ -153,6 +186,56 @@ class Blas:
             raise ValueError("inner dimensions differ")
         return self._mm(gen_lib().dadgpt_matmul_transposed_b_bf16, a, b, M, K, N)
 
+    def library_version(self) -> int:
+        """The hipBLASLt version behind the handle (major*100000 + minor*100 + patch)."""
+        return int(gen_lib().dadgpt_blas_library_version(self._h))
+
+    @staticmethod
+    def _f32(t, name):
+        if t.dtype != torch.float32 or not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 device tensor")
+
+    def matmul_f32(self, out, a, b, M: int, K: int, N: int, op: str = "N",
+                   beta: float = 0.0) -> None:
+        """fp32 GEMM into out [M,N]: op 'N' gpu_matmul (a [M,K], b [K,N]), 'A'
+        gpu_matmul_transposed_a (a [K,M]; beta 1 accumulates), 'B' gpu_matmul_transposed_b
+        (b [N,K]) (cuda/gpu_ops.cu:94-112), at the process-wide precision."""
+        for t, nm in ((out, "out"), (a, "a"), (b, "b")):
+            self._f32(t, nm)
+        _check(gen_lib().dadgpt_matmul_f32(self._h, out.data_ptr(), a.data_ptr(), b.data_ptr(),
+                                           M, K, N, ord(op), beta, _stream()))
+
+    def matmul_f32_batched(self, out, a, b, M: int, K: int, N: int, op: str, beta: float,
+                           stride_a: int, stride_b: int, stride_out: int, count: int) -> None:
+        """Strided-batched fp32 GEMM: op 'B' beta 0 gpu_matmul_strided_batched_bt, 'N' beta 0
+        gpu_matmul_strided_batched, 'A' beta 1 gpu_matmul_strided_batched_at
+        (cuda/gpu_ops.cu:117-141)."""
+        for t, nm in ((out, "out"), (a, "a"), (b, "b")):
+            self._f32(t, nm)
+        _check(gen_lib().dadgpt_matmul_f32_strided_batched(
+            self._h, out.data_ptr(), a.data_ptr(), b.data_ptr(), M, K, N, ord(op), beta,
+            stride_a, stride_b, stride_out, count, _stream()))
+
+    def attention_materialized_forward(self, out, probs, q, k, v, BH: int, S: int, d_head: int,
+                                       scale: float) -> None:
+        """The reference's materialized attention forward (src/model.cpp:395-420): probs
+        [BH,S,S] receives softmax(mask(q k^T * scale)), out = probs v."""
+        for t, nm in ((out, "out"), (probs, "probs"), (q, "q"), (k, "k"), (v, "v")):
+            self._f32(t, nm)
+        _check(gen_lib().dadgpt_attention_materialized_forward(
+            self._h, out.data_ptr(), probs.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            BH, S, d_head, scale, _stream()))
+
+    def attention_materialized_backward(self, dq, dk, dv, dscores, dout, probs, q, k, v, BH: int,
+                                        S: int, d_head: int, scale: float) -> None:
+        """Its backward (src/model.cpp:575-616): dq, dk, dv overwritten; dscores [BH,S,S]
+        scratch."""
+        ts = (dq, dk, dv, dscores, dout, probs, q, k, v)
+        for t, nm in zip(ts, ("dq", "dk", "dv", "dscores", "dout", "probs", "q", "k", "v")):
+            self._f32(t, nm)
+        _check(gen_lib().dadgpt_attention_materialized_backward(
+            self._h, *[t.data_ptr() for t in ts], BH, S, d_head, scale, _stream()))
+
 
 # ------------------------------------------------------------------------ the model
 
@@ -174,10 +257,18 @@ def init_params(cfg, seed: int, device="cuda") -> torch.Tensor:
     return params
 
 
-class GPT2:
-    """Batched greedy generation over a bf16 parameter arena (kept referenced here)."""
+# Attention of a model (include/dadgpt/gpt2_generate.h DADGPT_GPT2_ATTN_*).
+ATTENTION = {"bf16": 0, "fp32": 1, "fp32_materialized": 2}
 
-    def __init__(self, cfg, params: torch.Tensor, max_batch: int, attn_fp32: bool = False):
+
+class GPT2:
+    """Batched greedy generation over a bf16 parameter arena (kept referenced here).
+
+    attention: 'bf16' (flash prefill and decode kernels over bf16 caches), 'fp32' (the fp32
+    flash kernels over fp32 caches) or 'fp32_materialized' (the reference's materialized path
+    on fp32 GEMMs, over fp32 caches); everything else is identical."""
+
+    def __init__(self, cfg, params: torch.Tensor, max_batch: int, attention: str = "bf16"):
         self.cfg = Config.of(cfg)
         if params.dtype != torch.bfloat16 or not params.is_cuda:
             raise ValueError("params must be a bfloat16 device tensor")
@@ -188,7 +279,8 @@ class GPT2:
         self._m = ctypes.c_void_p()
         torch.cuda.synchronize()  # the arena may still be being written on torch's stream
         _check(gen_lib().dadgpt_gpt2_create(ctypes.byref(self.cfg), params.data_ptr(), max_batch,
-                                            int(attn_fp32), ctypes.byref(self._m)))
+                                            ATTENTION[attention], ctypes.byref(self._m)))
+        self.attention = attention
 
     def close(self):
         if self._m:

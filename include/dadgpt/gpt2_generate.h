@@ -13,8 +13,8 @@
  * are bf16 hipBLASLt GEMMs (<dadgpt/gpu_matmul.h>); decode projections for batches of up to 16
  * run on skinny MFMA kernels over pre-transposed weights with the residual add + LayerNorm
  * and bias + GELU fused into their prologues. The residual stream, LayerNorm statistics and
- * logits are fp32. Attention runs in bf16 (default) or in fp32 (attn_fp32 = 1: fp32 Q/K/V,
- * fp32 caches, the fp32 kernels) with everything else identical.
+ * logits are fp32. Attention runs in bf16 (default), in fp32 on the fused kernels, or in fp32
+ * on the materialized path (attn_mode below) with everything else identical.
  *
  * Status codes are those of <dadgpt/gpu_attention.h>; dadgpt_gen_last_error() describes the
  * last failure on the calling thread.
@@ -58,13 +58,26 @@ size_t dadgpt_gpt2_param_count(const dadgpt_gpt2_config* config);
 int dadgpt_gpt2_init_params(uint16_t* params, const dadgpt_gpt2_config* config, uint64_t seed,
                             void* stream);
 
+/* Attention of a model (everything else is the same in every mode):
+ *  BF16: the bf16 flash prefill and bf16 decode kernels over bf16 KV caches (the default);
+ *  FP32: the fp32 flash prefill (the reference's fused path, use_fused_attention true,
+ *        src/model.cpp:390-393) and the fp32 decode kernel over fp32 caches;
+ *  FP32_MATERIALIZED: the reference's materialized path (src/model.cpp:395-420; decode as
+ *        src/model.cpp:765-790: q K^T, x scale, softmax over the cache length, P V) on fp32
+ *        hipBLASLt GEMMs, over fp32 caches. The GPU's own fp32 reference for the others. */
+enum {
+  DADGPT_GPT2_ATTN_BF16 = 0,
+  DADGPT_GPT2_ATTN_FP32 = 1,
+  DADGPT_GPT2_ATTN_FP32_MATERIALIZED = 2
+};
+
 /* A model over a caller-owned device parameter arena (kept by pointer: it must outlive the
  * model). Allocates the fused QKV weights, transposed copies of the projection weights, the
  * KV caches [max_batch, H, ctx_len, d_head] per layer, activations for max_batch x ctx_len
- * rows, and a hipBLASLt handle. d_head must be 32
- * or 64. */
+ * rows, a hipBLASLt handle, and in FP32_MATERIALIZED mode a [max_batch * H, ctx, ctx] fp32
+ * probability buffer. d_head must be 32 or 64. attn_mode is one of the values above. */
 int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params, int max_batch,
-                       int attn_fp32, dadgpt_gpt2** out);
+                       int attn_mode, dadgpt_gpt2** out);
 void dadgpt_gpt2_destroy(dadgpt_gpt2* model);
 
 /* Decode steps after the first replay one captured HIP graph per batch size (default on);

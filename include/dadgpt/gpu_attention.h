@@ -243,6 +243,58 @@ int dadgpt_decode_attention_f32(float* out, const float* q, const float* k_cache
                                 int n_heads, int max_len, int d_head, float scale,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- Materialized attention (the reference's second attention path, src/model.cpp:395-420
+ * forward and :575-616 backward, with the [BH, S, S] probabilities in memory). Its batched
+ * GEMMs are in <dadgpt/gpu_matmul.h> (libdadgpt_gen.so), which also composes the whole path
+ * (dadgpt_attention_materialized_forward/backward). Here are its elementwise operators, fp32
+ * row-major, each one launch on `stream`:
+ *  - the reference's own, same semantics (the reference-named C++ forms are in
+ *    <dadgpt/gpu_ops_attention.hpp>);
+ *  - one-pass fusions of the chains the reference runs between its GEMMs. */
+
+/* gpu_softmax (cuda/gpu_ops.cuh:57, cuda/gpu_ops.cu:147-199): row softmax, out may be in. */
+int dadgpt_softmax(float* out, const float* in, int rows, int cols, void* stream);
+/* gpu_softmax_backward (cuda/gpu_ops.cuh:76, cuda/gpu_ops.cu:542-569): ACCUMULATES
+ * din += out * (dout - rowsum(dout * out)). */
+int dadgpt_softmax_backward(float* din, const float* dout, const float* out, int rows, int cols,
+                            void* stream);
+/* gpu_causal_mask (cuda/gpu_ops.cuh:106, cuda/gpu_ops.cu:476-493): scores[b][i][j] = -1e9 for
+ * j > i in each of n_blocks S x S blocks. */
+int dadgpt_causal_mask(float* scores, int n_blocks, int S, void* stream);
+/* gpu_causal_mask_zero (cuda/gpu_ops.cuh:108, cuda/gpu_ops.cu:495-511): 0 for j > i. */
+int dadgpt_causal_mask_zero(float* grads, int n_blocks, int S, void* stream);
+/* gpu_scale (cuda/gpu_ops.cuh:110, cuda/gpu_ops.cu:513-525): data[i] *= scale. */
+int dadgpt_scale(float* data, int64_t count, float scale, void* stream);
+
+/* scores [BH, S, S] -> probabilities in place: x scale, -1e9 above the diagonal, row softmax
+ * (gpu_scale + gpu_causal_mask + gpu_softmax, src/model.cpp:407-409, in one pass). */
+int dadgpt_attention_probs(float* probs, int BH, int S, float scale, void* stream);
+/* d(scores) [BH, S, S] from d(probs) and probs: softmax backward, 0 above the diagonal,
+ * x scale (gpu_zero + gpu_softmax_backward + gpu_causal_mask_zero + gpu_scale,
+ * src/model.cpp:601-607, in one pass). dscores may be dprobs. */
+int dadgpt_attention_probs_backward(float* dscores, const float* dprobs, const float* probs,
+                                    int BH, int S, float scale, void* stream);
+/* Decode scores [n_seq * n_heads, max_len] -> probabilities in place over each sequence's
+ * first lens[seq] keys (DEVICE int32 lens; x scale, keys at or past the length -1e9, row
+ * softmax; an empty cache gives a zero row): the gpu_scale + gpu_softmax step of the
+ * reference's decode (src/model.cpp:776-780) for a batch of ragged caches. */
+int dadgpt_decode_probs(float* probs, const int32_t* lens, int n_seq, int n_heads, int max_len,
+                        float scale, void* stream);
+
+/* The reference's choice between the two paths (AttentionImpl, src/model.hpp:80;
+ * use_fused_attention, src/model.cpp:183-197): 1 = fused flash kernels, 0 = materialized.
+ * Attention dropout or an unsupported d_head forces materialized; Fused and Materialized
+ * force their path; Auto takes fused from ctx_len 512 up. The reference takes the
+ * materialized path for dropout because its fused kernel has none; here the flash kernels
+ * carry dropout too (the _dropout entry points), so a caller may keep them, but this predicate
+ * answers exactly as the reference's does. */
+typedef enum dadgpt_attention_impl {
+  DADGPT_ATTENTION_AUTO = 0,
+  DADGPT_ATTENTION_FUSED = 1,
+  DADGPT_ATTENTION_MATERIALIZED = 2
+} dadgpt_attention_impl;
+int dadgpt_use_fused_attention(int impl, int d_head, int ctx_len, int attn_dropout);
+
 #ifdef __cplusplus
 }
 #endif

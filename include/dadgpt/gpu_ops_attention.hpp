@@ -19,3 +19,21 @@ void gpu_flash_attention_backward(float* dq, float* dk, float* dv, float* delta,
                                   const float* out, const float* lse, const float* q,
                                   const float* k, const float* v, int BH, int S, int d_head,
                                   float scale);
+
+// ---- the materialized path's elementwise operators (null stream, throw on error) ----
+
+// cuda/gpu_ops.cuh:57
+void gpu_softmax(float* out, const float* in, int rows, int cols);
+// cuda/gpu_ops.cuh:76 (accumulates into din)
+void gpu_softmax_backward(float* din, const float* dout, const float* out, int rows, int cols);
+// cuda/gpu_ops.cuh:106
+void gpu_causal_mask(float* scores, int num_blocks, int seq_len);
+// cuda/gpu_ops.cuh:108
+void gpu_causal_mask_zero(float* grads, int num_blocks, int seq_len);
+// cuda/gpu_ops.cuh:110
+void gpu_scale(float* data, int size, float scale);
+
+// src/model.hpp:80 and the predicate of src/model.cpp:183-197 without the Model: the caller
+// passes its implementation choice, head size and context length.
+enum class AttentionImpl { Auto, Fused, Materialized };
+bool use_fused_attention(AttentionImpl impl, int d_head, int ctx_len, bool attn_dropout);

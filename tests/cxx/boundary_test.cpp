@@ -1,8 +1,8 @@
 // Links against libdadgpt_attn.so through the reference's own wrapper names and C++
-// signatures (cuda/gpu_ops.cuh:112-122) and checks their host-side behaviour, which needs no
-// GPU: the supported() predicate and the std::runtime_error thrown for an unsupported d_head
-// (message as cuda/attention.cu:238,251) and for a null buffer. Built and run by
-// tests/test_capi.py.
+// signatures (cuda/gpu_ops.cuh:57,76,106-122; src/model.hpp:80) and checks their host-side
+// behaviour, which needs no GPU: the supported() and fused/materialized predicates, and the
+// std::runtime_error thrown for an unsupported d_head (message as cuda/attention.cu:238,251)
+// and for a null buffer. Built and run by tests/test_capi.py.
 #include <cstdio>
 #include <stdexcept>
 #include <string>
@@ -46,6 +46,22 @@ int main() {
   EXPECT(m.find("null") != std::string::npos);
   m = thrown([&] { gpu_flash_attention_forward(p, p, p, p, p, 0, 64, 64, 0.1f); });
   EXPECT(m.find("positive") != std::string::npos);
+
+  // the materialized path's operators and the fused/materialized choice (src/model.cpp:183-197)
+  m = thrown([&] { gpu_softmax(nullptr, p, 4, 64); });
+  EXPECT(m.find("null") != std::string::npos);
+  m = thrown([&] { gpu_causal_mask(p, 0, 64); });
+  EXPECT(m.find("positive") != std::string::npos);
+  m = thrown([&] { gpu_scale(nullptr, 10, 2.0f); });
+  EXPECT(m.find("null") != std::string::npos);
+  m = thrown([&] { gpu_softmax_backward(p, p, nullptr, 4, 64); });
+  EXPECT(m.find("null") != std::string::npos);
+  EXPECT(use_fused_attention(AttentionImpl::Fused, 64, 64, false));
+  EXPECT(!use_fused_attention(AttentionImpl::Fused, 64, 64, true));
+  EXPECT(!use_fused_attention(AttentionImpl::Fused, 48, 1024, false));
+  EXPECT(!use_fused_attention(AttentionImpl::Materialized, 64, 4096, false));
+  EXPECT(use_fused_attention(AttentionImpl::Auto, 32, 512, false));
+  EXPECT(!use_fused_attention(AttentionImpl::Auto, 32, 511, false));
 
   EXPECT(dadgpt_flash_attention_forward(p, p, p, p, p, 4, 64, 48, 0.1f) == DADGPT_ERR_UNSUPPORTED);
   EXPECT(std::string(dadgpt_last_error()) == "flash attention: unsupported d_head 48");

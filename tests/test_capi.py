@@ -261,6 +261,40 @@ def test_decode_noalloc_limit_matches_header():
     assert int(m.group(1)) << int(m.group(2)) == A.DECODE_NOALLOC_SCRATCH_BYTES
 
 
+def test_use_fused_attention_policy():
+    """The reference's choice (src/model.cpp:183-197) over every input combination:
+    dropout or an unsupported d_head -> materialized; Fused / Materialized as selected; Auto
+    -> fused from ctx_len 512."""
+    for d in (16, 32, 48, 64, 80, 128):
+        for ctx in (1, 64, 511, 512, 513, 1024, 8192):
+            for drop in (False, True):
+                for impl in ("auto", "fused", "materialized"):
+                    want = (not drop and d in (32, 64) and
+                            (impl == "fused" or (impl == "auto" and ctx >= 512)))
+                    assert A.use_fused_attention(impl, d, ctx, drop) == want, (impl, d, ctx, drop)
+
+
+def test_materialized_ops_validation():
+    L = A.lib()
+    assert L.dadgpt_softmax(None, FAKE, 4, 64, None) == 1
+    assert L.dadgpt_softmax(FAKE, FAKE, 0, 64, None) == 1
+    assert L.dadgpt_softmax(FAKE, FAKE, 4, 0, None) == 1
+    assert L.dadgpt_softmax(FAKE + 2, FAKE, 4, 64, None) == 1
+    assert "aligned" in A.last_error()
+    assert L.dadgpt_softmax(FAKE, FAKE, 1 << 26, 4, None) == 1  # rows * 64 lanes >= 2^32
+    assert L.dadgpt_softmax_backward(FAKE, FAKE, None, 4, 64, None) == 1
+    assert L.dadgpt_causal_mask(FAKE, 0, 64, None) == 1
+    assert L.dadgpt_causal_mask_zero(None, 2, 64, None) == 1
+    assert L.dadgpt_scale(None, 10, 2.0, None) == 1
+    assert L.dadgpt_scale(FAKE, -1, 2.0, None) == 1
+    assert L.dadgpt_scale(FAKE, 0, 2.0, None) == 0  # nothing to do, no launch
+    assert L.dadgpt_attention_probs(FAKE, 2, 64, float("nan"), None) == 1
+    assert L.dadgpt_attention_probs(FAKE, 0, 64, 0.125, None) == 1
+    assert L.dadgpt_attention_probs_backward(FAKE, FAKE, None, 2, 64, 0.125, None) == 1
+    assert L.dadgpt_decode_probs(FAKE, None, 2, 12, 1024, 0.125, None) == 1
+    assert L.dadgpt_decode_probs(FAKE, FAKE, 2, 0, 1024, 0.125, None) == 1
+
+
 def test_cxx_reference_names_link_and_throw(tmp_path):
     """A C++ caller using the reference's names/signatures links and gets the reference's
     exceptions (built with g++ here; needs no GPU)."""

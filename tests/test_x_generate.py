@@ -136,7 +136,7 @@ def test_gen_argument_checks_before_any_hip_call():
 
 # ------------------------------------------------------------------------------- GPU
 
-def _gpu_model(cfg, seed, max_batch, attn_fp32=False):
+def _gpu_model(cfg, seed, max_batch, attention="bf16"):
     import torch
 
     from dadgpt_amd import gpt2
@@ -144,7 +144,7 @@ def _gpu_model(cfg, seed, max_batch, attn_fp32=False):
     params = gpt2.init_params(cfg, seed)
     torch.cuda.synchronize()
     host = params.float().cpu().numpy()
-    return gpt2.GPT2(cfg, params, max_batch, attn_fp32), host
+    return gpt2.GPT2(cfg, params, max_batch, attention), host
 
 
 @pytest.mark.gpu
@@ -193,11 +193,12 @@ def _prompts(cfg, lens, seed):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("cfg,attn_fp32", [(TINY, False), (TINY, True), (TINY64, False),
-                                           (TINY64, True)])
-def test_generate_matches_oracle(gpu, cfg, attn_fp32):
-    case(f"generate vs oracle d={cfg['d_model']} H={cfg['n_heads']} fp32attn={attn_fp32}")
-    model, params = _gpu_model(cfg, seed=21, max_batch=4, attn_fp32=attn_fp32)
+@pytest.mark.parametrize("cfg,attention", [(TINY, "bf16"), (TINY, "fp32"),
+                                           (TINY, "fp32_materialized"), (TINY64, "bf16"),
+                                           (TINY64, "fp32"), (TINY64, "fp32_materialized")])
+def test_generate_matches_oracle(gpu, cfg, attention):
+    case(f"generate vs oracle d={cfg['d_model']} H={cfg['n_heads']} attention={attention}")
+    model, params = _gpu_model(cfg, seed=21, max_batch=4, attention=attention)
     prompts = _prompts(cfg, [5, 17, 1, 30], 300)
     new = 12
     out = model.generate(prompts, new, logits=True)
@@ -303,8 +304,8 @@ def test_gpt2_124m_bf16_attention_matches_fp32_attention(gpu):
 
     case("gpt2-124m bf16 vs fp32 attention, 4 prompts x 24 tokens")
     params = gpt2.init_params(GPT2, 0x5EED)
-    m16 = gpt2.GPT2(GPT2, params, 4, attn_fp32=False)
-    m32 = gpt2.GPT2(GPT2, params, 4, attn_fp32=True)
+    m16 = gpt2.GPT2(GPT2, params, 4, attention="bf16")
+    m32 = gpt2.GPT2(GPT2, params, 4, attention="fp32")
     prompts = _prompts(GPT2, [16, 100, 37, 256], 600)
     a = m16.generate(prompts, 24, logits=True)
     b = m32.generate(prompts, 24, logits=True)
