@@ -1,11 +1,27 @@
-// fp32 causal flash attention (the reference's precision, cuda/attention.cu:1): forward with
-// online softmax and saved natural-log logsumexp, backward recomputing P from it. Accurate
-// expf/logf, fp32 FMA; the result matches the fp32 CPU path to ~1e-6. The DROP instantiations
-// add attention-probability dropout with the keep bits of dropout.hpp.
+// fp32 causal flash attention on the fp32 matrix cores of gfx950 (v_mfma_f32_32x32x2_f32:
+// fp32 operands, fp32 products and accumulation). This is the reference's precision
+// (cuda/attention.cu:1): forward with online softmax and a saved natural-log logsumexp, backward
+// recomputing the probabilities from it. Softmax exponentials and logarithms use the accurate
+// expf/logf; results match the fp32 CPU path to a few 1e-7.
 //
-// gfx950 has no fp32 MFMA rate worth the layout work at this precision's use (tests, greedy
-// parity), so these are SIMT kernels: one lane per query row (forward, dQ) or key row
-// (dK/dV), 64-row tiles of the other operand staged in LDS and read as broadcast float4.
+// Work decomposition (every product a 32 x 32 MFMA tile, one wave per 32 rows):
+//  forward  a wave owns 32 queries (lane l holds query l % 32): S^T = K Q^T over each 32-key
+//           chunk with Q in registers, the online softmax per lane, O^T += V^T P^T with P taken
+//           straight from the score registers (the K rows are read through sigma32, so score
+//           register u of lane half h is the MFMA k-index u of that half: no lane exchange);
+//  dK/dV    a wave owns 32 keys (lane l holds key l % 32) and walks every later query chunk:
+//           S = Q K^T and dP = dO V^T with K and V in registers, P and dS in registers,
+//           dV^T += dO^T P and dK^T += Q^T dS; nothing is shared between waves (no atomics);
+//  dQ       a wave owns 32 queries again: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T;
+//  delta    rowsum(dO * O), a separate pass that dK/dV and dQ both read.
+// The MFMA k-index of the score products runs over d_head as (lane half h, step t) -> d =
+// h * D/2 + t, so every lane reads D/2 contiguous floats of a row. Tiles of 64 rows are
+// staged in LDS with the row pitch padded by 4 floats; the next tile is loaded into registers
+// while the current one is on the matrix cores.
+//
+// The DROP instantiations apply attention-probability dropout with the keep bits of
+// dropout.hpp: the forward and dQ hold keys along registers (keep_row16), dK/dV holds queries
+// along registers (keep_col16).
 #include "common.hpp"
 #include "dropout.hpp"
 #include "kernels.hpp"
@@ -13,253 +29,383 @@
 namespace dadgpt {
 namespace {
 
-constexpr int kT = 64;  // rows per block and per LDS tile
+constexpr int kWaves = 4;             // waves per workgroup
+constexpr int kRows = 32 * kWaves;    // rows (queries or keys) a workgroup owns
+constexpr int kTile = 64;             // rows per staged tile (two 32-row chunks)
 
+// D(32x32) += A(32x2) B(2x32), fp32. Lane l supplies A[l%32][l/32] and B[l/32][l%32] and
+// receives C[c32_row(r, l/32)][l%32] in element r.
+__device__ __forceinline__ f32x16 mfma32f(float a, float b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Row (within a 32-row chunk) that score register u of lane half h stands for, when the A
+// operand rows were read through sigma32: 16 * (u / 8) + 8 * h + u % 8.
+__device__ __forceinline__ constexpr int reg_row(int u, int h) {
+  return 16 * (u >> 3) + 8 * h + (u & 7);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// A 64-row fp32 tile in LDS (pitch D + 4 floats) and its register prefetch: 256 threads, D/16
+// 16-byte pieces each; rows at or past S read as zeros.
 template <int D>
-__device__ __forceinline__ void stage_rows_f32(float (*dst)[D], const float* src, int row0,
-                                               int S) {
-  // 64 threads, 16-byte pieces, consecutive threads on consecutive pieces.
-  constexpr int C = D / 4;
-  for (int u = threadIdx.x; u < kT * C; u += kT) {
-    const int r = u / C, c = u % C;
-    f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (row0 + r < S) x = *reinterpret_cast<const f32x4*>(src + (size_t)(row0 + r) * D + 4 * c);
-    *reinterpret_cast<f32x4*>(&dst[r][4 * c]) = x;
+struct Tile {
+  static constexpr int kPitch = D + 4;
+  static constexpr int kPieces = kTile * D / 4 / 256;
+  f32x4 r[kPieces];
+
+  __device__ __forceinline__ void load(const float* src, int row0, int S) {
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+      const int u = threadIdx.x + 256 * i, row = u / (D / 4), c = u % (D / 4);
+      r[i] = row0 + row < S ? *reinterpret_cast<const f32x4*>(src + (size_t)(row0 + row) * D +
+                                                              4 * c)
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  __device__ __forceinline__ void store(float* lds) const {
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+      const int u = threadIdx.x + 256 * i, row = u / (D / 4), c = u % (D / 4);
+      *reinterpret_cast<f32x4*>(lds + row * kPitch + 4 * c) = r[i];
+    }
+  }
+};
+
+// The D/2 floats of row `row` that lane half h supplies as score-product operands.
+template <int D>
+__device__ __forceinline__ void read_half_row(float (&x)[D / 2], const float* lds, int row,
+                                              int h) {
+  const float* p = lds + row * Tile<D>::kPitch + h * (D / 2);
+#pragma unroll
+  for (int i = 0; i < D / 8; ++i) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * i);
+    x[4 * i] = v[0], x[4 * i + 1] = v[1], x[4 * i + 2] = v[2], x[4 * i + 3] = v[3];
   }
 }
 
 template <int D>
-__device__ __forceinline__ float dot_row(const float* a, const float (*tile)[D], int j) {
-  float acc = 0.f;
+__device__ __forceinline__ void load_half_row(float (&x)[D / 2], const float* g, int h) {
 #pragma unroll
-  for (int c = 0; c < D; c += 4) {
-    const f32x4 t = *reinterpret_cast<const f32x4*>(&tile[j][c]);
-    acc = fmaf(a[c], t[0], acc);
-    acc = fmaf(a[c + 1], t[1], acc);
-    acc = fmaf(a[c + 2], t[2], acc);
-    acc = fmaf(a[c + 3], t[3], acc);
+  for (int i = 0; i < D / 8; ++i) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(g + h * (D / 2) + 4 * i);
+    x[4 * i] = v[0], x[4 * i + 1] = v[1], x[4 * i + 2] = v[2], x[4 * i + 3] = v[3];
   }
+}
+
+// acc = sum_t A_t B_t over the D/2 score steps: A rows from LDS (through sigma32), B from the
+// lane's registers.
+template <int D>
+__device__ __forceinline__ f32x16 score_tile(const float* lds, int chunk_row0,
+                                             const float (&b)[D / 2], int lane) {
+  float a[D / 2];
+  read_half_row<D>(a, lds, chunk_row0 + sigma32(lane & 31), lane >> 5);
+  f32x16 acc = zero16();
+#pragma unroll
+  for (int t = 0; t < D / 2; ++t) acc = mfma32f(a[t], b[t], acc);
   return acc;
 }
 
-template <int D, bool DROP>
-__global__ __launch_bounds__(kT) void fwd_f32_kernel(float* __restrict__ out,
-                                                     float* __restrict__ lse,
-                                                     const float* __restrict__ q,
-                                                     const float* __restrict__ k,
-                                                     const float* __restrict__ v, int S,
-                                                     float scale, const DropParams dr) {
-  __shared__ __attribute__((aligned(16))) float sk[kT][D];
-  __shared__ __attribute__((aligned(16))) float sv[kT][D];
-  const int bh = blockIdx.x;
-  const int blk = gridDim.y - 1 - blockIdx.y;
-  const int row = blk * kT + threadIdx.x;
-  const size_t base = (size_t)bh * S * D;
-  const bool valid = row < S;
-
-  float qr[D], o[D];
+// acc[db] += M^T P over one 32-row chunk: A = rows reg_row(u, h) of the LDS tile at columns
+// 32 db + lane%32 (the transposed operand read across a row), B = register u of p.
+template <int D>
+__device__ __forceinline__ void accumulate_t(f32x16 (&acc)[D / 32], const float* lds,
+                                             int chunk_row0, const f32x16& p, int lane) {
+  const int l32 = lane & 31, h = lane >> 5;
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    qr[d] = valid ? q[base + (size_t)row * D + d] : 0.f;
-    o[d] = 0.f;
-  }
-  float m = neg_inf(), l = 0.f;
-  const int last = min(S, (blk + 1) * kT) - 1;
-  for (int k0 = 0; k0 <= last; k0 += kT) {
-    __syncthreads();
-    stage_rows_f32<D>(sk, k + base, k0, S);
-    stage_rows_f32<D>(sv, v + base, k0, S);
-    __syncthreads();
-    if (!valid) continue;
-    const int nj = min(kT, row - k0 + 1);  // keys k0 .. row are visible
-    if (nj <= 0) continue;
-    uint64_t keep = 0;  // keep bits of keys k0 .. k0+63 of this row
-    if constexpr (DROP) {
-#pragma unroll 1
-      for (int j8 = 0; j8 < nj; j8 += 8)
-        keep |= (uint64_t)keep8(dr, (uint64_t)bh * S + row, (uint32_t)(k0 + j8) >> 3) << j8;
-    }
-    float s[kT];
-    float mx = neg_inf();
+  for (int u = 0; u < 16; ++u) {
+    const float* row = lds + (chunk_row0 + reg_row(u, h)) * Tile<D>::kPitch + l32;
 #pragma unroll
-    for (int j = 0; j < kT; ++j) {
-      s[j] = j < nj ? dot_row<D>(qr, sk, j) * scale : neg_inf();
-      mx = fmaxf(mx, s[j]);
-    }
-    const float mnew = fmaxf(m, mx);
-    const float corr = expf(m - mnew);
-    l *= corr;
-#pragma unroll
-    for (int d = 0; d < D; ++d) o[d] *= corr;
-#pragma unroll
-    for (int j = 0; j < kT; ++j) {
-      if (j < nj) {
-        const float p = expf(s[j] - mnew);
-        l += p;  // the normaliser of the undropped row
-        float pv = p;
-        if constexpr (DROP) pv = p * ((keep >> j) & 1u ? dr.scale : 0.0f);
-#pragma unroll
-        for (int d = 0; d < D; ++d) o[d] = fmaf(pv, sv[j][d], o[d]);
-      }
-    }
-    m = mnew;
-  }
-  if (valid) {
-    const float inv = 1.0f / l;
-#pragma unroll
-    for (int d = 0; d < D; ++d) out[base + (size_t)row * D + d] = o[d] * inv;
-    lse[(size_t)bh * S + row] = m + logf(l);
+    for (int db = 0; db < D / 32; ++db) acc[db] = mfma32f(row[32 * db], p[u], acc[db]);
   }
 }
 
+// Writes a wave's transposed accumulators (element r of lane (l32, h), block db: row l32 of
+// the wave, column 32 db + c32_row(r, h)) as 32 contiguous rows of D floats through the wave's
+// LDS slot `stage` (32 x (D + 4) floats), times `mul` (per lane).
+template <int D>
+__device__ __forceinline__ void store_rows_t(float* dst, int row0, int S,
+                                             const f32x16 (&acc)[D / 32], float mul,
+                                             float* stage, int lane) {
+  const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      stage[l32 * Tile<D>::kPitch + 32 * db + c32_row(r, h)] = acc[db][r] * mul;
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's own LDS writes are done
+  __builtin_amdgcn_wave_barrier();
+  constexpr int kPieces = 32 * D / 4 / 64;
+#pragma unroll
+  for (int i = 0; i < kPieces; ++i) {
+    const int u = lane + 64 * i, row = u / (D / 4), c = u % (D / 4);
+    if (row0 + row < S)
+      *reinterpret_cast<f32x4*>(dst + (size_t)(row0 + row) * D + 4 * c) =
+          *reinterpret_cast<const f32x4*>(stage + row * Tile<D>::kPitch + 4 * c);
+  }
+}
+
+// The epilogue staging slot of wave w: 32 rows of one of the workgroup's two 64-row tile
+// buffers (waves 0-1 in the first, 2-3 in the second), free once every wave left the tiles.
+template <int D>
+__device__ __forceinline__ float* stage_slot(float* first, float* second, int wave) {
+  return (wave < 2 ? first : second) + (wave & 1) * 32 * Tile<D>::kPitch;
+}
+
+// ------------------------------------------------------------------------------ forward
+
+template <int D, bool DROP>
+__global__ __launch_bounds__(64 * kWaves) void fwd_f32_kernel(
+    float* __restrict__ out, float* __restrict__ lse, const float* __restrict__ q,
+    const float* __restrict__ k, const float* __restrict__ v, int S, float scale,
+    const DropParams dr) {
+  __shared__ __attribute__((aligned(16))) float sk[kTile * Tile<D>::kPitch];
+  __shared__ __attribute__((aligned(16))) float sv[kTile * Tile<D>::kPitch];
+  const int bh = blockIdx.x;
+  const int blk = gridDim.y - 1 - blockIdx.y;  // longest query blocks first
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31, h = lane >> 5;
+  const size_t base = (size_t)bh * S * D;
+  const int q0 = blk * kRows + 32 * wave;  // the wave's first query
+  const int qi = q0 + l32;                 // this lane's query
+  const int last = min(S, (blk + 1) * kRows) - 1;  // the workgroup's last query
+  const int n_tiles = last / kTile + 1;
+
+  float qr[D / 2];
+  load_half_row<D>(qr, q + base + (size_t)min(qi, S - 1) * D, h);
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) o[db] = zero16();
+  float m = neg_inf(), l = 0.f;
+
+  Tile<D> tk, tv;
+  tk.load(k + base, 0, S);
+  tv.load(v + base, 0, S);
+  for (int t = 0; t < n_tiles; ++t) {
+    __syncthreads();  // the previous tile's reads are done
+    tk.store(sk);
+    tv.store(sv);
+    __syncthreads();
+    if (t + 1 < n_tiles) {  // next tile in flight during this one
+      tk.load(k + base, (t + 1) * kTile, S);
+      tv.load(v + base, (t + 1) * kTile, S);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int key0 = t * kTile + 32 * c;
+      if (key0 > q0 + 31) continue;  // wave-uniform: the whole chunk is in the future
+      f32x16 s = score_tile<D>(sk, 32 * c, qr, lane);
+      float cm = neg_inf();
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const float x = key0 + reg_row(u, h) > qi ? neg_inf() : s[u] * scale;
+        s[u] = x;
+        cm = fmaxf(cm, x);
+      }
+      const float mn = fmaxf(m, max_halves(cm));  // key 0 <= qi: finite from the first chunk
+      const float alpha = expf(m - mn);
+      m = mn;
+      float ps = 0.f;
+      uint32_t keep = 0;
+      if constexpr (DROP) keep = keep_row16(dr, (uint64_t)bh * S + qi, key0, h);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const float p = expf(s[u] - mn);
+        ps += p;
+        s[u] = DROP ? p * keep_factor(keep, u, dr.scale) : p;
+      }
+      l = l * alpha + sum_halves(ps);
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      accumulate_t<D>(o, sv, 32 * c, s, lane);
+    }
+  }
+  if (h == 0 && qi < S) lse[(size_t)bh * S + qi] = m + logf(l);
+  __syncthreads();  // every wave is done with the tiles: reuse sk as per-wave staging
+  store_rows_t<D>(out + base, q0, S, o, 1.0f / l, stage_slot<D>(sk, sv, wave), lane);
+}
+
+// ----------------------------------------------------------------------------- backward
+
+// delta[row] = sum_d dout[row][d] * out[row][d]: D/4 lanes per row, one 16-byte piece each;
+// a grid-stride loop over rows (the lanes of a row share every trip, so the row's shuffles
+// always see all of its lanes).
+template <int D>
 __global__ __launch_bounds__(256) void delta_f32_kernel(float* __restrict__ delta,
                                                         const float* __restrict__ dout,
                                                         const float* __restrict__ out,
-                                                        long rows, int D) {
-  const long r = (long)blockIdx.x * 256 + threadIdx.x;
-  if (r >= rows) return;
-  float acc = 0.f;
-  for (int d = 0; d < D; ++d) acc = fmaf(dout[r * D + d], out[r * D + d], acc);
-  delta[r] = acc;
+                                                        long long rows) {
+  constexpr int LPR = D / 4;
+  const int c = threadIdx.x % LPR;
+  const long long stride = (long long)gridDim.x * (256 / LPR);
+  for (long long row = ((long long)blockIdx.x * 256 + threadIdx.x) / LPR; row < rows;
+       row += stride) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(dout + row * D + 4 * c);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(out + row * D + 4 * c);
+    float acc = a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (c == 0) delta[row] = acc;
+  }
 }
 
-// One lane per key j: dV_j = sum_{r>=j} P_rj dO_r, dK_j = scale * sum_{r>=j} dS_rj Q_r.
-// With dropout: dV_j = sum_r P_rj f_rj dO_r and dS_rj = P_rj (dP_rj f_rj - delta_r), f = keep/(1-p).
 template <int D, bool DROP>
-__global__ __launch_bounds__(kT) void dkdv_f32_kernel(
+__global__ __launch_bounds__(64 * kWaves) void dkdv_f32_kernel(
     float* __restrict__ dk, float* __restrict__ dv, const float* __restrict__ q,
     const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, float scale,
     const DropParams dr) {
-  __shared__ __attribute__((aligned(16))) float sq[kT][D];
-  __shared__ __attribute__((aligned(16))) float sdo[kT][D];
-  __shared__ float slse[kT], sdel[kT];
-  const int bh = blockIdx.x;
-  const int blk = blockIdx.y;
-  const int key = blk * kT + threadIdx.x;
+  __shared__ __attribute__((aligned(16))) float sq[kTile * Tile<D>::kPitch];
+  __shared__ __attribute__((aligned(16))) float sg[kTile * Tile<D>::kPitch];
+  __shared__ float sl[kTile], sd[kTile];
+  const int bh = blockIdx.x, blk = blockIdx.y;  // early key blocks see the most queries: first
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31, h = lane >> 5;
   const size_t base = (size_t)bh * S * D;
-  const bool valid = key < S;
-  float kr[D], vr[D], dka[D], dva[D];
+  const int k0 = blk * kRows + 32 * wave;  // the wave's first key
+  const int kj = k0 + l32;                 // this lane's key
+  const int t0 = (blk * kRows) / kTile;    // first query tile with a query >= the first key
+  const int n_tiles = (S + kTile - 1) / kTile;
+
+  float kr[D / 2], vr[D / 2];
+  load_half_row<D>(kr, k + base + (size_t)min(kj, S - 1) * D, h);
+  load_half_row<D>(vr, v + base + (size_t)min(kj, S - 1) * D, h);
+  f32x16 dka[D / 32], dva[D / 32];
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    kr[d] = valid ? k[base + (size_t)key * D + d] : 0.f;
-    vr[d] = valid ? v[base + (size_t)key * D + d] : 0.f;
-    dka[d] = dva[d] = 0.f;
-  }
-  for (int r0 = blk * kT; r0 < S; r0 += kT) {
+  for (int db = 0; db < D / 32; ++db) dka[db] = zero16(), dva[db] = zero16();
+
+  Tile<D> tq, tg;
+  float pl = 0.f, pd = 0.f;
+  auto load_stats = [&](int row0) {
+    const int r = row0 + (threadIdx.x & 63);
+    pl = r < S ? lse[(size_t)bh * S + r] : 0.f;
+    pd = r < S ? delta[(size_t)bh * S + r] : 0.f;
+  };
+  tq.load(q + base, t0 * kTile, S);
+  tg.load(dout + base, t0 * kTile, S);
+  load_stats(t0 * kTile);
+  for (int t = t0; t < n_tiles; ++t) {
     __syncthreads();
-    stage_rows_f32<D>(sq, q + base, r0, S);
-    stage_rows_f32<D>(sdo, dout + base, r0, S);
-    {
-      const int r = r0 + threadIdx.x;
-      slse[threadIdx.x] = r < S ? lse[(size_t)bh * S + r] : 0.f;
-      sdel[threadIdx.x] = r < S ? delta[(size_t)bh * S + r] : 0.f;
-    }
+    tq.store(sq);
+    tg.store(sg);
+    if (threadIdx.x < kTile) sl[threadIdx.x] = pl, sd[threadIdx.x] = pd;
     __syncthreads();
-    // keep bits of this lane's key for the tile's 64 rows (every lane, before any exits: the
-    // bits of 8 rows come from one Philox block per lane of an 8-lane group, then a transpose)
-    uint64_t keep = 0;
-    if constexpr (DROP) {
-      const int t = threadIdx.x & 7;
-      const uint32_t j8 = (uint32_t)(blk * kT + (threadIdx.x & ~7)) >> 3;
-#pragma unroll 1
-      for (int i8 = 0; i8 < kT; i8 += 8) {
-        const uint32_t m = keep8(dr, (uint64_t)bh * S + r0 + i8 + t, j8);  // row i8 + t
-        keep |= (uint64_t)transpose8_bits(m, t) << i8;  // bit e: row i8 + e, this lane's key
-      }
+    if (t + 1 < n_tiles) {
+      tq.load(q + base, (t + 1) * kTile, S);
+      tg.load(dout + base, (t + 1) * kTile, S);
+      load_stats((t + 1) * kTile);
     }
-    if (!valid) continue;
-    const int i_begin = max(0, key - r0);
-    const int i_end = min(kT, S - r0);
-    for (int i = i_begin; i < i_end; ++i) {
-      const float s = dot_row<D>(kr, sq, i);
-      const float dp = dot_row<D>(vr, sdo, i);
-      const float p = expf(s * scale - slse[i]);
-      float pv = p, ds;
-      if constexpr (DROP) {
-        const float f = (keep >> i) & 1u ? dr.scale : 0.0f;
-        pv = p * f;
-        ds = p * (dp * f - sdel[i]) * scale;
-      } else {
-        ds = p * (dp - sdel[i]) * scale;
-      }
 #pragma unroll
-      for (int d = 0; d < D; ++d) {
-        dva[d] = fmaf(pv, sdo[i][d], dva[d]);
-        dka[d] = fmaf(ds, sq[i][d], dka[d]);
+    for (int c = 0; c < 2; ++c) {
+      const int qrow0 = t * kTile + 32 * c;
+      if (qrow0 + 31 < k0) continue;  // wave-uniform: every query of the chunk precedes every key
+      // lane (l32, h), register u: query qrow0 + reg_row(u, h), key kj
+      f32x16 s = score_tile<D>(sq, 32 * c, kr, lane);   // Q K^T
+      f32x16 dp = score_tile<D>(sg, 32 * c, vr, lane);  // dO V^T
+      uint32_t keep = 0;
+      if constexpr (DROP) keep = keep_col16(dr, (uint64_t)bh * S + qrow0, k0, lane);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int qrow = qrow0 + reg_row(u, h);
+        const int rl = 32 * c + reg_row(u, h);
+        const bool vis = kj <= qrow && qrow < S;
+        const float p = vis ? expf(s[u] * scale - sl[rl]) : 0.f;
+        float g = dp[u];
+        if constexpr (DROP) {
+          const float f = keep_factor(keep, u, dr.scale);
+          g *= f;
+          s[u] = p * f;  // the probability that multiplied V
+        } else {
+          s[u] = p;
+        }
+        dp[u] = p * (g - sd[rl]) * scale;
       }
+      accumulate_t<D>(dva, sg, 32 * c, s, lane);   // dV^T += dO^T P
+      accumulate_t<D>(dka, sq, 32 * c, dp, lane);  // dK^T += Q^T dS
     }
   }
-  if (valid) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      dk[base + (size_t)key * D + d] = dka[d];
-      dv[base + (size_t)key * D + d] = dva[d];
-    }
-  }
+  __syncthreads();
+  float* stage = stage_slot<D>(sq, sg, wave);
+  store_rows_t<D>(dk + base, k0, S, dka, 1.0f, stage, lane);
+  store_rows_t<D>(dv + base, k0, S, dva, 1.0f, stage, lane);  // after the wave's dK reads
 }
 
-// One lane per query r: dQ_r = scale * sum_{j<=r} dS_rj K_j.
 template <int D, bool DROP>
-__global__ __launch_bounds__(kT) void dq_f32_kernel(
+__global__ __launch_bounds__(64 * kWaves) void dq_f32_kernel(
     float* __restrict__ dq, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta, int S, float scale, const DropParams dr) {
-  __shared__ __attribute__((aligned(16))) float sk[kT][D];
-  __shared__ __attribute__((aligned(16))) float sv[kT][D];
+  __shared__ __attribute__((aligned(16))) float sk[kTile * Tile<D>::kPitch];
+  __shared__ __attribute__((aligned(16))) float sv[kTile * Tile<D>::kPitch];
   const int bh = blockIdx.x;
-  const int blk = gridDim.y - 1 - blockIdx.y;
-  const int row = blk * kT + threadIdx.x;
+  const int blk = gridDim.y - 1 - blockIdx.y;  // longest query blocks first
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31, h = lane >> 5;
   const size_t base = (size_t)bh * S * D;
-  const bool valid = row < S;
-  float qr[D], dor[D], dqa[D];
+  const int q0 = blk * kRows + 32 * wave;
+  const int qi = q0 + l32;
+  const int qc = min(qi, S - 1);
+  const int last = min(S, (blk + 1) * kRows) - 1;
+  const int n_tiles = last / kTile + 1;
+
+  float qr[D / 2], gr[D / 2];
+  load_half_row<D>(qr, q + base + (size_t)qc * D, h);
+  load_half_row<D>(gr, dout + base + (size_t)qc * D, h);
+  const float my_lse = lse[(size_t)bh * S + qc], my_delta = delta[(size_t)bh * S + qc];
+  f32x16 acc[D / 32];
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    qr[d] = valid ? q[base + (size_t)row * D + d] : 0.f;
-    dor[d] = valid ? dout[base + (size_t)row * D + d] : 0.f;
-    dqa[d] = 0.f;
-  }
-  const float rl = valid ? lse[(size_t)bh * S + row] : 0.f;
-  const float rd = valid ? delta[(size_t)bh * S + row] : 0.f;
-  const int last = min(S, (blk + 1) * kT) - 1;
-  for (int k0 = 0; k0 <= last; k0 += kT) {
+  for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
+
+  Tile<D> tk, tv;
+  tk.load(k + base, 0, S);
+  tv.load(v + base, 0, S);
+  for (int t = 0; t < n_tiles; ++t) {
     __syncthreads();
-    stage_rows_f32<D>(sk, k + base, k0, S);
-    stage_rows_f32<D>(sv, v + base, k0, S);
+    tk.store(sk);
+    tv.store(sv);
     __syncthreads();
-    if (!valid) continue;
-    const int nj = min(kT, row - k0 + 1);
-    uint32_t keep = 0;
-    for (int j = 0; j < nj; ++j) {
-      const float s = dot_row<D>(qr, sk, j);
-      const float dp = dot_row<D>(dor, sv, j);
-      const float p = expf(s * scale - rl);
-      float ds;
-      if constexpr (DROP) {
-        if ((j & 7) == 0) keep = keep8(dr, (uint64_t)bh * S + row, (uint32_t)(k0 + j) >> 3);
-        ds = p * (dp * keep_factor(keep, j & 7, dr.scale) - rd) * scale;
-      } else {
-        ds = p * (dp - rd) * scale;
+    if (t + 1 < n_tiles) {
+      tk.load(k + base, (t + 1) * kTile, S);
+      tv.load(v + base, (t + 1) * kTile, S);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int key0 = t * kTile + 32 * c;
+      if (key0 > q0 + 31) continue;
+      // lane (l32, h), register u: query qi, key key0 + reg_row(u, h)
+      f32x16 s = score_tile<D>(sk, 32 * c, qr, lane);   // K Q^T
+      f32x16 dp = score_tile<D>(sv, 32 * c, gr, lane);  // V dO^T
+      uint32_t keep = 0;
+      if constexpr (DROP) keep = keep_row16(dr, (uint64_t)bh * S + qi, key0, h);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const bool vis = key0 + reg_row(u, h) <= qi;
+        const float p = vis ? expf(s[u] * scale - my_lse) : 0.f;
+        float g = dp[u];
+        if constexpr (DROP) g *= keep_factor(keep, u, dr.scale);
+        s[u] = p * (g - my_delta) * scale;
       }
-#pragma unroll
-      for (int d = 0; d < D; ++d) dqa[d] = fmaf(ds, sk[j][d], dqa[d]);
+      accumulate_t<D>(acc, sk, 32 * c, s, lane);  // dQ^T += K^T dS^T
     }
   }
-  if (valid) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) dq[base + (size_t)row * D + d] = dqa[d];
-  }
+  __syncthreads();
+  store_rows_t<D>(dq + base, q0, S, acc, 1.0f, stage_slot<D>(sk, sv, wave), lane);
 }
 
 template <int D>
 hipError_t fwd_f32_t(float* out, float* lse, const float* q, const float* k, const float* v,
                      int BH, int S, float scale, hipStream_t stream, const Dropout* drop) {
-  const dim3 grid(BH, (S + kT - 1) / kT);
+  const dim3 grid(BH, (S + kRows - 1) / kRows);
   const DropParams dr = drop_params(drop);
   if (drop != nullptr)
-    fwd_f32_kernel<D, true><<<grid, kT, 0, stream>>>(out, lse, q, k, v, S, scale, dr);
+    fwd_f32_kernel<D, true><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, scale, dr);
   else
-    fwd_f32_kernel<D, false><<<grid, kT, 0, stream>>>(out, lse, q, k, v, S, scale, dr);
+    fwd_f32_kernel<D, false><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, scale, dr);
   return hipGetLastError();
 }
 
@@ -269,24 +415,27 @@ hipError_t bwd_f32_t(float* dq, float* dk, float* dv, float* delta, const float*
                      const float* v, int BH, int S, float scale, hipStream_t stream,
                      const Dropout* drop) {
   const DropParams dr = drop_params(drop);
-  const long rows = (long)BH * S;
-  delta_f32_kernel<<<(unsigned)((rows + 255) / 256), 256, 0, stream>>>(delta, dout, out, rows, D);
+  const long long rows = (long long)BH * S;
+  const long long blocks = (rows * (D / 4) + 255) / 256;
+  delta_f32_kernel<D><<<(unsigned)(blocks < 16384 ? blocks : 16384), 256, 0, stream>>>(
+      delta, dout, out, rows);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const dim3 grid(BH, (S + kT - 1) / kT);
+  const dim3 grid(BH, (S + kRows - 1) / kRows);
   if (drop != nullptr)
-    dkdv_f32_kernel<D, true><<<grid, kT, 0, stream>>>(dk, dv, q, k, v, dout, lse, delta, S,
-                                                      scale, dr);
+    dkdv_f32_kernel<D, true><<<grid, 64 * kWaves, 0, stream>>>(dk, dv, q, k, v, dout, lse,
+                                                               delta, S, scale, dr);
   else
-    dkdv_f32_kernel<D, false><<<grid, kT, 0, stream>>>(dk, dv, q, k, v, dout, lse, delta, S,
-                                                       scale, dr);
+    dkdv_f32_kernel<D, false><<<grid, 64 * kWaves, 0, stream>>>(dk, dv, q, k, v, dout, lse,
+                                                                delta, S, scale, dr);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (drop != nullptr)
-    dq_f32_kernel<D, true><<<grid, kT, 0, stream>>>(dq, q, k, v, dout, lse, delta, S, scale, dr);
+    dq_f32_kernel<D, true><<<grid, 64 * kWaves, 0, stream>>>(dq, q, k, v, dout, lse, delta, S,
+                                                             scale, dr);
   else
-    dq_f32_kernel<D, false><<<grid, kT, 0, stream>>>(dq, q, k, v, dout, lse, delta, S, scale,
-                                                     dr);
+    dq_f32_kernel<D, false><<<grid, 64 * kWaves, 0, stream>>>(dq, q, k, v, dout, lse, delta, S,
+                                                              scale, dr);
   return hipGetLastError();
 }
 
