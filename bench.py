@@ -255,7 +255,6 @@ def profile_sample(wl, reps):
           f"{COPY_BYTES} B copy", flush=True)
 
 
-GEN_N, GEN_NEW, GEN_SEED = 16, 128, 0x5EED
 
 
 def generate_cfg5():
@@ -267,10 +266,9 @@ def generate_cfg5():
 
     from dadgpt_amd import gpt2, synth
 
+    GEN_N, GEN_NEW, GEN_SEED = synth.CFG5_N, synth.CFG5_NEW, synth.CFG5_SEED
     cfg = gpt2.PRESETS["gpt2-124m"]
-    lens = synth.uniform_int(16, 256, GEN_N, GEN_SEED ^ 0x10)
-    prompts = [list(synth.uniform_int(0, cfg["vocab_size"] - 1, int(n), GEN_SEED + 0x100 + i))
-               for i, n in enumerate(lens)]
+    prompts = synth.cfg5_prompts(cfg["vocab_size"])
     params = gpt2.init_params(cfg, GEN_SEED)
     m16 = gpt2.GPT2(cfg, params, GEN_N, attention="bf16")
     m16.generate(prompts, 8)  # builds the hipBLASLt plans and captures the decode step

@@ -52,8 +52,10 @@ hipError_t embed(float* x, const int* tok, const int* pos0, const bf16* wte, con
 
 // Per row (d <= 2048): if y, x[r] += sum_{s < splits} y[s][r] + bias (the residual add of a
 // projection, y holding `splits` partial sums [splits][rows][d]); then, if w,
-// out[r] = bf16(LayerNorm(x[r]) * w + b) with eps 1e-5 (two-pass mean and variance, fp32).
-hipError_t residual_layernorm(float* x, const float* y, const bf16* bias, bf16* out,
+// out[r] = O(LayerNorm(x[r]) * w + b) with eps 1e-5 (two-pass mean and variance, fp32); O is
+// bf16 or float (the precision of the projection that reads it).
+template <typename O>
+hipError_t residual_layernorm(float* x, const float* y, const bf16* bias, O* out,
                               const bf16* w, const bf16* b, int rows, int d, hipStream_t s,
                               int splits = 1);
 
@@ -65,15 +67,17 @@ hipError_t qkv_split(T* qh, T* kh, T* vh, T* kcache, T* vcache, const float* qkv
                      const float* bqkv, const int* pos0, const int* nvalid, int n, int S, int H,
                      int dh, int max_len, hipStream_t s);
 
-// out [n*S, d] bf16 <- heads [n*H, S, dh] (T).
-template <typename T>
-hipError_t merge_heads(bf16* out, const T* heads, int n, int S, int H, int dh, hipStream_t s);
+// out [n*S, d] (O: bf16 or float) <- heads [n*H, S, dh] (T).
+template <typename T, typename O>
+hipError_t merge_heads(O* out, const T* heads, int n, int S, int H, int dh, hipStream_t s);
 
-// out[i] = bf16(in[i]).
+// out[i] = bf16(in[i]); out[i] = float(in[i]).
 hipError_t to_bf16(bf16* out, const float* in, size_t count, hipStream_t s);
+hipError_t to_f32(float* out, const bf16* in, size_t count, hipStream_t s);
 
-// out[r, c] = bf16(gelu_tanh(y[r, c] + bias[c])).
-hipError_t bias_gelu(bf16* out, const float* y, const bf16* bias, int rows, int cols,
+// out[r, c] = O(gelu_tanh(y[r, c] + bias[c])), O bf16 or float.
+template <typename O>
+hipError_t bias_gelu(O* out, const float* y, const bf16* bias, int rows, int cols,
                      hipStream_t s);
 
 // out[b] = x[b*S + len[b] - 1] (rows of d floats).

@@ -121,6 +121,7 @@ struct dadgpt_gpt2 {
   int max_batch = 0;
   bool fp32 = false;          // fp32 Q/K/V, caches and attention (modes 1 and 2)
   bool materialized = false;  // mode 2: the materialized path (GEMMs + row softmax)
+  bool proj32 = false;        // fp32 projections (fp32 activations and weights; fp32 attention)
   int dh = 0;
   size_t esz = 2;  // bytes per attention element (Q/K/V, caches, attention output)
   dadgpt_blas* blas = nullptr;
@@ -133,11 +134,15 @@ struct dadgpt_gpt2 {
   bool skinny = false;
   std::vector<bf16*> wqkv_t, wo_t, w1_t, w2_t;  // [3d, d], [d, d], [d_ff, d], [d, d_ff]
   std::vector<void*> kc, vc;  // per layer [max_batch, H, ctx, dh]
+  // fp32 projections: fp32 copies of the projection weights (exact widenings of the arena)
+  std::vector<float*> wqkv32, wo32, w1_32, w2_32;
+  float* emb32 = nullptr;
 
   float *x = nullptr, *qkv = nullptr, *y = nullptr, *f = nullptr, *xl = nullptr;
   float *logits = nullptr, *lse = nullptr, *pick = nullptr;
   float* probs = nullptr;  // materialized mode: [max_batch * H, ctx, ctx] probabilities
-  bf16 *h = nullptr, *a = nullptr, *g = nullptr;
+  bf16 *h = nullptr, *a = nullptr, *g = nullptr;  // projection inputs (bf16 projections)
+  float *h32 = nullptr, *a32 = nullptr, *g32 = nullptr;  // the same with fp32 projections
   void *qh = nullptr, *kh = nullptr, *vh = nullptr, *ao = nullptr;
   void* ws = nullptr;
   size_t ws_bytes = 0;
@@ -221,6 +226,28 @@ int attn_fail(const dadgpt_gpt2* m, int st, const char* what) {
   } while (0)
 #define TRY_HIP(expr, what) TRY(check_hip((expr), (what)))
 
+// A projection out[M,N] (fp32) = in[M,K] W[K,N] (or W[N,K]^T): bf16 operands, or with fp32
+// projections the fp32 activations and weights (the reference's default fp32 matmuls).
+int proj(dadgpt_gpt2* m, float* out, const void* in, const bf16* w, const float* w32, int M,
+         int K, int N, bool trans_b) {
+  if (m->proj32)
+    return gemm_f32(m->blas, out, static_cast<const float*>(in), w32, M, K, N,
+                    trans_b ? 'B' : 'N', 0.0f, 1, 0, 0, 0, m->stream);
+  return gemm(m->blas, out, static_cast<const bf16*>(in), w, M, K, N, trans_b, m->stream);
+}
+const void* in_h(const dadgpt_gpt2* m) { return m->proj32 ? (const void*)m->h32 : m->h; }
+const void* in_g(const dadgpt_gpt2* m) { return m->proj32 ? (const void*)m->g32 : m->g; }
+
+// x += y + bias (when y), then LayerNorm(x) * w + b (when w) into the projection input h.
+int layernorm_h(dadgpt_gpt2* m, float* x, const float* y, const bf16* bias, const bf16* w,
+                const bf16* b, int rows) {
+  const int d = m->c.d_model;
+  const hipError_t e =
+      m->proj32 ? residual_layernorm<float>(x, y, bias, m->h32, w, b, rows, d, m->stream)
+                : residual_layernorm<bf16>(x, y, bias, m->h, w, b, rows, d, m->stream);
+  return check_hip(e, "residual_layernorm");
+}
+
 // One transformer block over `rows` rows (n sequences of S rows each). prefill: the rows are
 // prompt positions 0..S-1 (K/V appended for s < len); otherwise one token per sequence at
 // cur_pos. attn_ev: optional pair of events around the attention launch.
@@ -231,9 +258,10 @@ int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev
   const float scale = 1.0f / std::sqrt(static_cast<float>(dh));  // src/model.cpp:389
   hipStream_t s = m->stream;
 
-  // m->h holds LayerNorm 1 of x (written by whichever kernel last updated x)
-  TRY(gemm(m->blas, m->qkv, m->h, m->wqkv[l], rows, d, 3 * d, false, s));
-  const bf16* attn_in = m->a;
+  // h holds LayerNorm 1 of x (written by whichever kernel last updated x)
+  TRY(proj(m, m->qkv, in_h(m), m->wqkv[l], m->proj32 ? m->wqkv32[l] : nullptr, rows, d, 3 * d,
+           false));
+  const void* attn_in = m->proj32 ? (const void*)m->a32 : m->a;
   if (prefill) {
     if (m->fp32)
       TRY_HIP(qkv_split<float>((float*)m->qh, (float*)m->kh, (float*)m->vh, (float*)m->kc[l],
@@ -247,8 +275,12 @@ int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev
               "qkv_split");
     if (int st = attention_prefill(m, l, n, S, scale))
       return attn_fail(m, st, "prefill attention");
-    if (m->fp32)
-      TRY_HIP(merge_heads<float>(m->a, (const float*)m->ao, n, S, H, dh, s), "merge_heads");
+    if (m->proj32)
+      TRY_HIP((merge_heads<float, float>(m->a32, (const float*)m->ao, n, S, H, dh, s)),
+              "merge_heads");
+    else if (m->fp32)
+      TRY_HIP((merge_heads<float, bf16>(m->a, (const float*)m->ao, n, S, H, dh, s)),
+              "merge_heads");
   } else {
     if (m->fp32)
       TRY_HIP(qkv_split<float>((float*)m->qh, nullptr, nullptr, (float*)m->kc[l],
@@ -264,18 +296,22 @@ int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev
     if (int st = attention_decode(m, l, n, scale)) return attn_fail(m, st, "decode attention");
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[1], s), "hipEventRecord");
     // decode output [n, H, dh] is already the [n, d] row layout
-    if (m->fp32)
+    if (m->proj32)
+      attn_in = m->ao;
+    else if (m->fp32)
       TRY_HIP(to_bf16(m->a, (const float*)m->ao, (size_t)n * d, s), "to_bf16");
     else
-      attn_in = (const bf16*)m->ao;
+      attn_in = m->ao;
   }
-  TRY(gemm(m->blas, m->y, attn_in, m->P(L.Wo), rows, d, d, false, s));
-  TRY_HIP(residual_layernorm(m->x, m->y, m->P(L.bo), m->h, m->P(L.ln2_w), m->P(L.ln2_b), rows,
-                             d, s),
-          "residual_layernorm");
-  TRY(gemm(m->blas, m->f, m->h, m->P(L.fc1_w), rows, d, c.d_ff, false, s));
-  TRY_HIP(bias_gelu(m->g, m->f, m->P(L.fc1_b), rows, c.d_ff, s), "bias_gelu");
-  TRY(gemm(m->blas, m->y, m->g, m->P(L.fc2_w), rows, c.d_ff, d, false, s));
+  TRY(proj(m, m->y, attn_in, m->P(L.Wo), m->proj32 ? m->wo32[l] : nullptr, rows, d, d, false));
+  TRY(layernorm_h(m, m->x, m->y, m->P(L.bo), m->P(L.ln2_w), m->P(L.ln2_b), rows));
+  TRY(proj(m, m->f, in_h(m), m->P(L.fc1_w), m->proj32 ? m->w1_32[l] : nullptr, rows, d, c.d_ff,
+           false));
+  TRY_HIP(m->proj32 ? bias_gelu<float>(m->g32, m->f, m->P(L.fc1_b), rows, c.d_ff, s)
+                    : bias_gelu<bf16>(m->g, m->f, m->P(L.fc1_b), rows, c.d_ff, s),
+          "bias_gelu");
+  TRY(proj(m, m->y, in_g(m), m->P(L.fc2_w), m->proj32 ? m->w2_32[l] : nullptr, rows, c.d_ff, d,
+           false));
   // the residual add, fused with the next LayerNorm: layer l+1's LayerNorm 1, or after the
   // last layer the final LayerNorm (decode; the prefill normalises only the gathered rows)
   const bf16 *nw = nullptr, *nb = nullptr;
@@ -286,17 +322,14 @@ int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev
     nw = m->P(m->off.lnf_w);
     nb = m->P(m->off.lnf_b);
   }
-  TRY_HIP(residual_layernorm(m->x, m->y, m->P(L.fc2_b), m->h, nw, nb, rows, d, s),
-          "residual_layernorm");
+  TRY(layernorm_h(m, m->x, m->y, m->P(L.fc2_b), nw, nb, rows));
   return DADGPT_OK;
 }
 
 // LayerNorm 1 of layer 0 over freshly embedded rows.
 int first_layernorm(dadgpt_gpt2* m, int rows) {
   const auto& L0 = m->off.layers[0];
-  return check_hip(residual_layernorm(m->x, nullptr, nullptr, m->h, m->P(L0.ln1_w),
-                                      m->P(L0.ln1_b), rows, m->c.d_model, m->stream),
-                   "residual_layernorm");
+  return layernorm_h(m, m->x, nullptr, nullptr, m->P(L0.ln1_w), m->P(L0.ln1_b), rows);
 }
 
 // Weight-tied logits of the n final-LayerNorm rows in m->h, greedy pick (stored at the step
@@ -304,7 +337,8 @@ int first_layernorm(dadgpt_gpt2* m, int rows) {
 int head(dadgpt_gpt2* m, int n) {
   const auto& c = m->c;
   hipStream_t s = m->stream;
-  TRY(gemm(m->blas, m->logits, m->h, m->P(m->off.tok_emb), n, c.d_model, c.vocab_size, true, s));
+  TRY(proj(m, m->logits, in_h(m), m->P(m->off.tok_emb), m->emb32, n, c.d_model, c.vocab_size,
+           true));
   TRY_HIP(argmax_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
                          m->lens, m->logits, m->pick, n, c.vocab_size, s),
           "argmax_advance");
@@ -354,7 +388,7 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[2 * l], s), "hipEventRecord");
     if (int st = attention_decode(m, l, n, scale)) return attn_fail(m, st, "decode attention");
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[2 * l + 1], s), "hipEventRecord");
-    const bf16* attn_in = m->a;
+    const bf16* attn_in = m->a;  // the skinny path runs with bf16 projections only
     if (m->fp32)
       TRY_HIP(to_bf16(m->a, (const float*)m->ao, (size_t)n * d, s), "to_bf16");
     else
@@ -382,8 +416,8 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
     TRY_HIP(skinny_gemm(kProRows, kEpiResidual, f2, s), "skinny fc2");
   }
   // final LayerNorm, then the tied logits
-  TRY_HIP(residual_layernorm(m->x, nullptr, nullptr, m->h, m->P(m->off.lnf_w),
-                             m->P(m->off.lnf_b), n, d, s),
+  TRY_HIP(residual_layernorm<bf16>(m->x, nullptr, nullptr, m->h, m->P(m->off.lnf_w),
+                                   m->P(m->off.lnf_b), n, d, s),
           "residual_layernorm");
   SkinnyArgs lg{};
   lg.wt = m->P(m->off.tok_emb);  // [V, d]: already W^T of the tied projection
@@ -501,19 +535,25 @@ void dadgpt_gpt2_destroy(dadgpt_gpt2* m) {
 
 int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params, int max_batch,
                        int attn_mode, dadgpt_gpt2** out) {
+  const int attn = attn_mode & 0xff;
+  const bool proj32 = (attn_mode & DADGPT_GPT2_FP32_PROJECTIONS) != 0;
   if (!out || !params || !config_ok(config) || max_batch < 1 || config->d_model > 2048 ||
-      attn_mode < DADGPT_GPT2_ATTN_BF16 || attn_mode > DADGPT_GPT2_ATTN_FP32_MATERIALIZED)
+      attn < DADGPT_GPT2_ATTN_BF16 || attn > DADGPT_GPT2_ATTN_FP32_MATERIALIZED ||
+      (attn_mode & ~(0xff | DADGPT_GPT2_FP32_PROJECTIONS)) != 0 ||
+      (proj32 && attn == DADGPT_GPT2_ATTN_BF16))
     return fail(DADGPT_ERR_INVALID_ARGUMENT,
                 "dadgpt_gpt2_create: bad arguments (d_head must be 32 or 64, d_model <= 2048, "
-                "max_batch >= 1, attn_mode 0, 1 or 2)");
+                "max_batch >= 1, attention mode 0, 1 or 2, fp32 projections only with fp32 "
+                "attention)");
   *out = nullptr;
   auto* m = new dadgpt_gpt2();
   m->c = *config;
   m->off = offsets_of(m->c);
   m->params = reinterpret_cast<const bf16*>(params);
   m->max_batch = max_batch;
-  m->fp32 = attn_mode != DADGPT_GPT2_ATTN_BF16;
-  m->materialized = attn_mode == DADGPT_GPT2_ATTN_FP32_MATERIALIZED;
+  m->fp32 = attn != DADGPT_GPT2_ATTN_BF16;
+  m->materialized = attn == DADGPT_GPT2_ATTN_FP32_MATERIALIZED;
+  m->proj32 = proj32;
   m->dh = m->c.d_model / m->c.n_heads;
   m->esz = m->fp32 ? sizeof(float) : sizeof(bf16);
   const auto& c = m->c;
@@ -563,8 +603,12 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       (st = m->alloc_n(&m->logits, (size_t)max_batch * c.vocab_size, "logits")) ||
       (st = m->alloc_n(&m->pick, pick_scratch_floats(max_batch), "pick scratch")) ||
       (st = m->alloc_n(&m->lse, rows * c.n_heads, "lse")) ||
-      (st = m->alloc_n(&m->h, rows * d, "ln out")) || (st = m->alloc_n(&m->a, rows * d, "attn in")) ||
-      (st = m->alloc_n(&m->g, rows * c.d_ff, "gelu out")) ||
+      (!proj32 && (st = m->alloc_n(&m->h, rows * d, "ln out"))) ||
+      (!proj32 && (st = m->alloc_n(&m->a, rows * d, "attn in"))) ||
+      (!proj32 && (st = m->alloc_n(&m->g, rows * c.d_ff, "gelu out"))) ||
+      (proj32 && (st = m->alloc_n(&m->h32, rows * d, "ln out"))) ||
+      (proj32 && (st = m->alloc_n(&m->a32, rows * d, "attn in"))) ||
+      (proj32 && (st = m->alloc_n(&m->g32, rows * c.d_ff, "gelu out"))) ||
       (st = m->alloc(&m->qh, rows * d * ab, "q heads")) ||
       // split K and V heads: fp32 attention only (bf16 reads them from the cache)
       (m->fp32 && (st = m->alloc(&m->kh, rows * d * ab, "k heads"))) ||
@@ -587,7 +631,28 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
     return bail(st);
   // the skinny decode path: reduction lengths the kernels are built for, LayerNorm rows that
   // fit the prologue's registers
-  m->skinny = skinny_supported(1, c.d_model) && skinny_supported(1, c.d_ff) && c.d_model <= 1024;
+  m->skinny = !proj32 && skinny_supported(1, c.d_model) && skinny_supported(1, c.d_ff) &&
+              c.d_model <= 1024;
+  if (proj32) {  // fp32 weights: widened once from the bf16 arena (exact)
+    m->wqkv32.resize(c.n_layers);
+    m->wo32.resize(c.n_layers);
+    m->w1_32.resize(c.n_layers);
+    m->w2_32.resize(c.n_layers);
+    auto widen = [&](float** dst, const bf16* src, size_t count, const char* what) {
+      if (int e = m->alloc_n(dst, count, what)) return e;
+      return check_hip(to_f32(*dst, src, count, m->stream), "to_f32");
+    };
+    for (int l = 0; l < c.n_layers; ++l) {
+      const auto& L = m->off.layers[l];
+      if ((st = widen(&m->wqkv32[l], m->wqkv[l], 3 * d * d, "wqkv fp32")) ||
+          (st = widen(&m->wo32[l], m->P(L.Wo), d * d, "wo fp32")) ||
+          (st = widen(&m->w1_32[l], m->P(L.fc1_w), d * c.d_ff, "fc1 fp32")) ||
+          (st = widen(&m->w2_32[l], m->P(L.fc2_w), (size_t)c.d_ff * d, "fc2 fp32")))
+        return bail(st);
+    }
+    if ((st = widen(&m->emb32, m->P(m->off.tok_emb), (size_t)c.vocab_size * d, "tok_emb fp32")))
+      return bail(st);
+  }
   if (m->skinny) {
     m->wqkv_t.resize(c.n_layers);
     m->wo_t.resize(c.n_layers);
@@ -691,9 +756,7 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
   TRY(first_layernorm(m, n * S));
   for (int l = 0; l < c.n_layers; ++l) TRY(block(m, l, n, S, true, nullptr));
   TRY_HIP(gather_last(m->xl, m->x, m->lens, n, S, c.d_model, s), "gather_last");
-  TRY_HIP(residual_layernorm(m->xl, nullptr, nullptr, m->h, m->P(m->off.lnf_w),
-                             m->P(m->off.lnf_b), n, c.d_model, s),
-          "residual_layernorm");
+  TRY(layernorm_h(m, m->xl, nullptr, nullptr, m->P(m->off.lnf_w), m->P(m->off.lnf_b), n));
   TRY(head(m, n));
   if (timed) TRY_HIP(hipEventRecord(ev[1], s), "hipEventRecord");
   if (logits) TRY(copy_logits(m, logits, n, 0));

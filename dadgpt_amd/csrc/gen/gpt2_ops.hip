@@ -68,11 +68,12 @@ __device__ __forceinline__ float block_sum(float v, float* sm) {
 constexpr int kLnMaxPerThread = 8;  // d <= 2048
 
 // One row per 256-thread block, the row held in registers: optionally x += y + bias (the
-// residual add of the previous projection), then out = bf16(LayerNorm(x) * w + b) with
-// eps 1e-5 and two-pass mean and variance in fp32 (src/tensor_ops.cpp:57-84). w == nullptr:
-// residual only.
+// residual add of the previous projection), then out = O(LayerNorm(x) * w + b) (O bf16 or
+// fp32) with eps 1e-5 and two-pass mean and variance in fp32 (src/tensor_ops.cpp:57-84).
+// w == nullptr: residual only.
+template <typename O>
 __global__ __launch_bounds__(256) void residual_layernorm_kernel(float* x, const float* y,
-                                                                 const bf16* bias, bf16* out,
+                                                                 const bf16* bias, O* out,
                                                                  const bf16* w, const bf16* b,
                                                                  int d, int splits) {
   __shared__ float sm[4];
@@ -103,11 +104,11 @@ __global__ __launch_bounds__(256) void residual_layernorm_kernel(float* x, const
     if (c < d) sq += (v[i] - mean) * (v[i] - mean);
   }
   const float inv_std = 1.0f / sqrtf(block_sum(sq, sm) / (float)d + 1e-5f);
-  bf16* orow = out + (size_t)blockIdx.x * d;
+  O* orow = out + (size_t)blockIdx.x * d;
 #pragma unroll
   for (int i = 0; i < kLnMaxPerThread; ++i) {
     const int c = threadIdx.x + 256 * i;
-    if (c < d) orow[c] = static_cast<bf16>((v[i] - mean) * inv_std * (float)w[c] + (float)b[c]);
+    if (c < d) orow[c] = static_cast<O>((v[i] - mean) * inv_std * (float)w[c] + (float)b[c]);
   }
 }
 
@@ -137,14 +138,20 @@ __global__ void qkv_split_kernel(T* qh, T* kh, T* vh, T* kcache, T* vcache, cons
   }
 }
 
-template <typename T>
-__global__ void merge_heads_kernel(bf16* out, const T* heads, int S, int H, int dh) {
+template <typename T, typename O>
+__global__ void merge_heads_kernel(O* out, const T* heads, int S, int H, int dh) {
   const int r = blockIdx.x, b = r / S, s = r % S;
   const int d = H * dh;
   for (int c = threadIdx.x; c < d; c += blockDim.x) {
     const int h = c / dh, e = c % dh;
-    out[(size_t)r * d + c] = static_cast<bf16>((float)heads[(((size_t)b * H + h) * S + s) * dh + e]);
+    out[(size_t)r * d + c] = static_cast<O>((float)heads[(((size_t)b * H + h) * S + s) * dh + e]);
   }
+}
+
+__global__ void to_f32_kernel(float* out, const bf16* in, size_t count) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = static_cast<float>(in[i]);
 }
 
 __global__ void to_bf16_kernel(bf16* out, const float* in, size_t count) {
@@ -159,12 +166,12 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(inner));
 }
 
-__global__ void bias_gelu_kernel(bf16* out, const float* y, const bf16* bias, int rows,
-                                 int cols) {
+template <typename O>
+__global__ void bias_gelu_kernel(O* out, const float* y, const bf16* bias, int rows, int cols) {
   const size_t n = (size_t)rows * cols;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
        i += (size_t)gridDim.x * blockDim.x)
-    out[i] = static_cast<bf16>(gelu_tanh(y[i] + (float)bias[i % cols]));
+    out[i] = static_cast<O>(gelu_tanh(y[i] + (float)bias[i % cols]));
 }
 
 __global__ void gather_last_kernel(float* out, const float* x, const int* len, int S, int d) {
@@ -286,13 +293,20 @@ hipError_t embed(float* x, const int* tok, const int* pos0, const bf16* wte, con
   return hipGetLastError();
 }
 
-hipError_t residual_layernorm(float* x, const float* y, const bf16* bias, bf16* out,
+template <typename O>
+hipError_t residual_layernorm(float* x, const float* y, const bf16* bias, O* out,
                               const bf16* w, const bf16* b, int rows, int d, hipStream_t s,
                               int splits) {
   if (d > 256 * kLnMaxPerThread) return hipErrorInvalidValue;
-  residual_layernorm_kernel<<<rows, 256, 0, s>>>(x, y, bias, out, w, b, d, splits);
+  residual_layernorm_kernel<O><<<rows, 256, 0, s>>>(x, y, bias, out, w, b, d, splits);
   return hipGetLastError();
 }
+template hipError_t residual_layernorm<bf16>(float*, const float*, const bf16*, bf16*,
+                                             const bf16*, const bf16*, int, int, hipStream_t,
+                                             int);
+template hipError_t residual_layernorm<float>(float*, const float*, const bf16*, float*,
+                                              const bf16*, const bf16*, int, int, hipStream_t,
+                                              int);
 
 template <typename T>
 hipError_t qkv_split(T* qh, T* kh, T* vh, T* kcache, T* vcache, const float* qkv,
@@ -309,23 +323,34 @@ template hipError_t qkv_split<float>(float*, float*, float*, float*, float*, con
                                      const float*, const int*, const int*, int, int, int, int,
                                      int, hipStream_t);
 
-template <typename T>
-hipError_t merge_heads(bf16* out, const T* heads, int n, int S, int H, int dh, hipStream_t s) {
-  merge_heads_kernel<T><<<n * S, 256, 0, s>>>(out, heads, S, H, dh);
+template <typename T, typename O>
+hipError_t merge_heads(O* out, const T* heads, int n, int S, int H, int dh, hipStream_t s) {
+  merge_heads_kernel<T, O><<<n * S, 256, 0, s>>>(out, heads, S, H, dh);
   return hipGetLastError();
 }
-template hipError_t merge_heads<float>(bf16*, const float*, int, int, int, int, hipStream_t);
+template hipError_t merge_heads<float, bf16>(bf16*, const float*, int, int, int, int,
+                                             hipStream_t);
+template hipError_t merge_heads<float, float>(float*, const float*, int, int, int, int,
+                                              hipStream_t);
+
+hipError_t to_f32(float* out, const bf16* in, size_t count, hipStream_t s) {
+  to_f32_kernel<<<grid_for(count), 256, 0, s>>>(out, in, count);
+  return hipGetLastError();
+}
 
 hipError_t to_bf16(bf16* out, const float* in, size_t count, hipStream_t s) {
   to_bf16_kernel<<<grid_for(count), 256, 0, s>>>(out, in, count);
   return hipGetLastError();
 }
 
-hipError_t bias_gelu(bf16* out, const float* y, const bf16* bias, int rows, int cols,
+template <typename O>
+hipError_t bias_gelu(O* out, const float* y, const bf16* bias, int rows, int cols,
                      hipStream_t s) {
-  bias_gelu_kernel<<<grid_for((size_t)rows * cols), 256, 0, s>>>(out, y, bias, rows, cols);
+  bias_gelu_kernel<O><<<grid_for((size_t)rows * cols), 256, 0, s>>>(out, y, bias, rows, cols);
   return hipGetLastError();
 }
+template hipError_t bias_gelu<bf16>(bf16*, const float*, const bf16*, int, int, hipStream_t);
+template hipError_t bias_gelu<float>(float*, const float*, const bf16*, int, int, hipStream_t);
 
 hipError_t gather_last(float* out, const float* x, const int* len, int n, int S, int d,
                        hipStream_t s) {

@@ -257,8 +257,10 @@ def init_params(cfg, seed: int, device="cuda") -> torch.Tensor:
     return params
 
 
-# Attention of a model (include/dadgpt/gpt2_generate.h DADGPT_GPT2_ATTN_*).
+# Attention of a model (include/dadgpt/gpt2_generate.h DADGPT_GPT2_ATTN_*), and the flag for
+# fp32 projections (DADGPT_GPT2_FP32_PROJECTIONS).
 ATTENTION = {"bf16": 0, "fp32": 1, "fp32_materialized": 2}
+FP32_PROJECTIONS = 0x100
 
 
 class GPT2:
@@ -266,9 +268,12 @@ class GPT2:
 
     attention: 'bf16' (flash prefill and decode kernels over bf16 caches), 'fp32' (the fp32
     flash kernels over fp32 caches) or 'fp32_materialized' (the reference's materialized path
-    on fp32 GEMMs, over fp32 caches); everything else is identical."""
+    on fp32 GEMMs, over fp32 caches); everything else is identical.
+    projections: 'bf16' (bf16 GEMM inputs, the default) or 'fp32' (with fp32 attention: the
+    reference's fp32 precision end to end)."""
 
-    def __init__(self, cfg, params: torch.Tensor, max_batch: int, attention: str = "bf16"):
+    def __init__(self, cfg, params: torch.Tensor, max_batch: int, attention: str = "bf16",
+                 projections: str = "bf16"):
         self.cfg = Config.of(cfg)
         if params.dtype != torch.bfloat16 or not params.is_cuda:
             raise ValueError("params must be a bfloat16 device tensor")
@@ -279,8 +284,10 @@ class GPT2:
         self._m = ctypes.c_void_p()
         torch.cuda.synchronize()  # the arena may still be being written on torch's stream
         _check(gen_lib().dadgpt_gpt2_create(ctypes.byref(self.cfg), params.data_ptr(), max_batch,
-                                            ATTENTION[attention], ctypes.byref(self._m)))
-        self.attention = attention
+                                            ATTENTION[attention] |
+                                            (FP32_PROJECTIONS if projections == "fp32" else 0),
+                                            ctypes.byref(self._m)))
+        self.attention, self.projections = attention, projections
 
     def close(self):
         if self._m:

@@ -97,3 +97,15 @@ def decode_inputs(n_seq: int, H: int, max_len: int, D: int, seed: int = BASE_SEE
     if bf16:
         q, kc, vc = bf16_round(q), bf16_round(kc), bf16_round(vc)
     return q, kc, vc, lens
+
+
+# GPT-2 124M generation, 16 prompts of U[16, 256] random tokens, 128 greedy
+# tokens each (the parameter arena is seeded with CFG5_SEED too).
+CFG5_N, CFG5_NEW, CFG5_SEED = 16, 128, 0x5EED
+
+
+def cfg5_prompts(vocab_size: int, n: int = CFG5_N, seed: int = CFG5_SEED):
+    """The config 5 prompts: lengths U[16, 256], token ids U[0, vocab_size - 1]."""
+    lens = uniform_int(16, 256, n, seed ^ 0x10)
+    return [list(uniform_int(0, vocab_size - 1, int(L), seed + 0x100 + i))
+            for i, L in enumerate(lens)]

@@ -70,6 +70,12 @@ enum {
   DADGPT_GPT2_ATTN_FP32 = 1,
   DADGPT_GPT2_ATTN_FP32_MATERIALIZED = 2
 };
+/* OR-ed into attn_mode with either fp32 attention: the projections run in fp32 too (fp32
+ * LayerNorm/GELU/attention outputs feed fp32 hipBLASLt GEMMs over fp32 widenings of the
+ * weights), i.e. the reference's default precision end to end (MatmulPrecision::FP32,
+ * cuda/gpu_ops.cu:61). The decode step then uses the same GEMMs instead of the skinny bf16
+ * kernels. */
+#define DADGPT_GPT2_FP32_PROJECTIONS 0x100
 
 /* A model over a caller-owned device parameter arena (kept by pointer: it must outlive the
  * model). Allocates the fused QKV weights, transposed copies of the projection weights, the
@@ -77,7 +83,7 @@ enum {
  * rows, a hipBLASLt handle, and in FP32_MATERIALIZED mode a [max_batch * H, ctx, ctx] fp32
  * probability buffer. d_head must be 32 or 64. attn_mode is one of the values above. */
 int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params, int max_batch,
-                       int attn_mode, dadgpt_gpt2** out);
+                       int attn_mode, dadgpt_gpt2** out);  /* attn_mode: see above */
 void dadgpt_gpt2_destroy(dadgpt_gpt2* model);
 
 /* Decode steps after the first replay one captured HIP graph per batch size (default on);

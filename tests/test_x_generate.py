@@ -324,3 +324,91 @@ def test_gpt2_124m_bf16_attention_matches_fp32_attention(gpu):
     m16.close()
     m32.close()
     torch.cuda.synchronize()
+
+
+TOL_FP32_PATHS = 1e-3  # logits, fp32 flash vs fp32 materialized, fp32 projections, same history
+GATE_MARGIN = 1e-4     # greedy gate: fp32 picks must agree wherever the margin exceeds this
+
+
+def _shared_history_check(a, b, tol, label):
+    """Rows of two runs of the same prompts: while a row's history is shared (up to and
+    including its first differing pick) the logits agree within tol, and a differing pick
+    falls where the reference run's top-1/top-2 margin is within twice the measured logit
+    difference. Returns (first divergence per row, max logit difference, margins there)."""
+    div = first_divergence(a["tokens"], b["tokens"])
+    n_new = a["tokens"].shape[1]
+    worst, at_div = 0.0, []
+    for r, t_div in enumerate(div):
+        for t in range(min(t_div + 1, n_new)):
+            dev_t = float(np.abs(a["logits"][t, r] - b["logits"][t, r]).max())
+            worst = max(worst, dev_t)
+            assert dev_t <= tol, (label, r, t, dev_t)
+        if t_div < n_new:
+            dev_d = float(np.abs(a["logits"][t_div, r] - b["logits"][t_div, r]).max())
+            margin = float(b["margins"][r, t_div])
+            at_div.append(margin)
+            assert margin <= 2 * dev_d, (label, r, t_div, margin, dev_d)
+    print(f"[cfg5] {label}: rows identical {sum(d == n_new for d in div)}/{len(div)}, first "
+          f"divergence {div}, max logit difference on shared history {worst:.3g}, reference "
+          f"margins at divergences {[round(m, 6) for m in at_div]}", flush=True)
+    return div, worst, at_div
+
+
+@pytest.mark.gpu
+def test_cfg5_generation_workload(gpu):
+    """BASELINE config 5 at its real workload: GPT-2 124M architecture, random init, the 16
+    prompts of U[16, 256] tokens, 128 greedy steps, max_batch 16 (with bf16 projections the
+    decode step runs the skinny M = 16 kernels and replays as a captured graph). Four models
+    over the same weights:
+      bf16        bf16 attention, bf16 projections (the product);
+      fp32        fp32 flash attention, bf16 projections (everything else as the product);
+      fp32/fp32   fp32 flash attention, fp32 projections (the reference's precision);
+      mat/fp32    fp32 materialized attention, fp32 projections (the reference's other
+                  attention path: the GPU's own fp32 reference).
+
+    - KV-cache invariant for every model (tests/test_model.cpp:216-252,375-414): decode-step
+      logits at steps 1, 64 and 127 equal the prefill of the prompt extended by the generated
+      tokens, for all 16 rows: within 2.5e-2 with bf16 projections, 1e-3 with fp32 ones. A bf16
+      projection input is an fp32 activation rounded once; prefill (hipBLASLt) and decode
+      (skinny kernels) compute those activations in different orders, and a one-ulp bf16 flip
+      (2^-8 relative) carries through 12 layers (measured 1.0-1.4e-2).
+    - bf16 vs fp32 attention (bf16 projections): logits within 5e-2 on shared history; a
+      token may differ only at a near-tie (fp32 margin within twice the logit difference).
+      The same bf16 rounding of projection inputs limits how closely any two attention
+      implementations can agree under bf16 projections (~1e-2).
+    - The greedy gate between the two fp32 attention paths with fp32 projections: logits within
+      1e-3 on shared history, tokens identical wherever the fp32 margin exceeds 1e-4 (and
+      twice the measured difference)."""
+    import torch
+
+    from dadgpt_amd import gpt2
+
+    params = gpt2.init_params(GPT2, synth.CFG5_SEED)
+    prompts = synth.cfg5_prompts(GPT2["vocab_size"])
+    n_new = synth.CFG5_NEW
+    runs = {}
+    for name, attention, projections, kv_tol in (
+            ("bf16", "bf16", "bf16", 2.5e-2), ("fp32", "fp32", "bf16", 2.5e-2),
+            ("fp32/fp32", "fp32", "fp32", 1e-3), ("mat/fp32", "fp32_materialized", "fp32", 1e-3)):
+        case(f"cfg5: 16 prompts x {n_new} greedy tokens, {attention} attention, {projections} "
+             f"projections")
+        m = gpt2.GPT2(GPT2, params, synth.CFG5_N, attention=attention, projections=projections)
+        out = m.generate(prompts, n_new, logits=True)
+        errs = []
+        for t in (1, 64, n_new - 1):
+            longer = [list(p) + list(out["tokens"][b, :t]) for b, p in enumerate(prompts)]
+            again = m.generate(longer, 1, logits=True)
+            errs.append(float(np.abs(again["logits"][0] - out["logits"][t]).max()))
+        print(f"[cfg5] {name}: decode vs prefill logits at steps 1, 64, 127: "
+              f"{[float(f'{e:.3g}') for e in errs]}", flush=True)
+        assert max(errs) <= kv_tol, (name, errs)
+        m.close()
+        runs[name] = out
+    _shared_history_check(runs["bf16"], runs["fp32"], TOL_ATTN_LOGIT, "bf16 vs fp32 attention")
+    _, _, at_div = _shared_history_check(runs["fp32/fp32"], runs["mat/fp32"], TOL_FP32_PATHS,
+                                         "fp32 flash vs fp32 materialized (fp32 projections)")
+    assert all(m <= GATE_MARGIN for m in at_div), at_div
+    for name, r in runs.items():
+        print(f"[cfg5] {name}: min margin {r['margins'].min():.3g}", flush=True)
+    del params
+    torch.cuda.synchronize()
