@@ -36,10 +36,13 @@ sys.path.insert(0, ROOT)
 import dadgpt_amd  # noqa: E402,F401
 
 PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 4096 flop/clk/CU x 2.4 GHz, dense
+PEAK_F32_TFLOPS = 157.3     # fp32 MFMA, dense
 PEAK_HBM_GBPS = 8000.0
+CPU_THREADS = 16            # the GPU box's CPU share for one GPU
 
 B, H, T, D = 16, 12, 1024, 64
 BH = B * H
+CFG2_BH = 8 * H                          # config 2: B8 H12 T1024 D64, forward only
 SCALE = 0.125
 UNIT = 2.0 * BH * T * T * D / 2          # one causal S x S x D product: 12.885 GFLOP
 FWD_FLOPS = 2 * UNIT                     # 25.770 GFLOP
@@ -64,7 +67,8 @@ def parse():
     p.add_argument("--reps", type=int, default=20, help="launches per kernel timing")
     p.add_argument("--decode-copies", type=int, default=8)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-slices", type=int, default=24)
+    p.add_argument("--cpu-slices", type=int, default=6,
+                   help="cfg3 (b,h) slices for the single-thread CPU run (x16 for all cores)")
     p.add_argument("--profile-sample", action="store_true")
     p.add_argument("--no-generate", action="store_true", help="skip the config 5 leg")
     p.add_argument("--generate-only", action="store_true",
@@ -102,33 +106,124 @@ def load_traffic():
     return out
 
 
+def decode_lens():
+    """Config 4's cache lengths: U[1, 1024] per sequence, seeded."""
+    import numpy as np
+    from dadgpt_amd import synth
+    return synth.uniform_int(1, DEC_L, DEC_N, synth.BASE_SEED ^ synth.TENSOR_ID["lens"]).astype(
+        np.int32)
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed(fn, reps=1):
+    """Median wall time of reps calls (after one untimed warm-up when reps > 1)."""
+    if reps > 1:
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
 def cpu_baseline(n_slices):
-    """The reference's CPU path (oracle/_ref: its own tensor_ops.cpp/backward.cpp) or, when
-    that is not built, the C restatement, on n_slices of the B16 H12 T1024 D64 problem."""
+    """The reference's CPU path on this host (oracle/_ref: its own tensor_ops.cpp and
+    backward.cpp composed in the materialized op order; the C restatement when that is not
+    built). Bounded samples, about 20 s in all:
+      - cfg3 forward+backward on n_slices (b,h) slices single-threaded, and on 16 * n_slices
+        slices over CPU_THREADS threads (slices are independent; ctypes releases the GIL);
+        value = the all-thread rate in algorithmic TFLOP/s;
+      - cfg1 (B1 H4 T64 D32) forward+backward in full, cfg4 decode (32 ragged caches) in full;
+      - cfg5: per-token cost of the reference's CPU GPT-2 forward (one sequence of 16 and of 32
+        tokens), extrapolated to 16 prompts + 128 greedy tokens each."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
     import oracle
     from dadgpt_amd import synth
 
-    q, k, v, g = synth.attn_inputs(n_slices, T, D, seed=synth.BASE_SEED + 3, with_dout=True,
-                                   bf16=True)
-    kind = "reference" if oracle.ref_available() else "port"
-    t0 = time.perf_counter()
-    if kind == "reference":
-        oracle.ref_attn_fwd(q, k, v, SCALE)
-        oracle.ref_attn_bwd(g, q, k, v, SCALE)
-    else:
-        oracle.attn_fwd_slices(q, k, v, SCALE, 0, n_slices)
-        oracle.attn_bwd_slices(g, q, k, v, SCALE, 0, n_slices)
-    dt = time.perf_counter() - t0
-    flops = (FWD_FLOPS + BWD_FLOPS) * n_slices / BH
+    ref = oracle.ref_available()
+    kind = "reference" if ref else "port"
+    fwd = oracle.ref_attn_fwd if ref else (lambda q, k, v, sc: oracle.attn_fwd_slices(
+        q, k, v, sc, 0, q.shape[0]))
+    bwd = oracle.ref_attn_bwd if ref else (lambda g, q, k, v, sc: oracle.attn_bwd_slices(
+        g, q, k, v, sc, 0, q.shape[0]))
+    per_slice = (FWD_FLOPS + BWD_FLOPS) / BH
+
+    def run(x):
+        q, k, v, g = x
+        fwd(q, k, v, SCALE)
+        bwd(g, q, k, v, SCALE)
+
+    one = synth.attn_inputs(n_slices, T, D, seed=synth.BASE_SEED + 3, with_dout=True, bf16=True)
+    dt1 = _timed(lambda: run(one))
+    chunks = [synth.attn_inputs(n_slices, T, D, seed=synth.BASE_SEED + 30 + i, with_dout=True,
+                                bf16=True) for i in range(CPU_THREADS)]
+    with ThreadPoolExecutor(CPU_THREADS) as pool:
+        t0 = time.perf_counter()
+        list(pool.map(run, chunks))
+        dtn = time.perf_counter() - t0
+    tf1 = per_slice * n_slices / dt1 / 1e12
+    tfn = per_slice * n_slices * CPU_THREADS / dtn / 1e12
+
+    q1, k1, v1, g1 = synth.attn_inputs(4, 64, 32, seed=synth.BASE_SEED, with_dout=True)
+    sc1 = float(np.float32(1 / np.sqrt(32)))
+    cfg1_s = _timed(lambda: (fwd(q1, k1, v1, sc1), bwd(g1, q1, k1, v1, sc1)), reps=3)
+    qd, kc, vc, _ = synth.decode_inputs(DEC_N, DEC_H, DEC_L, DEC_D, seed=synth.BASE_SEED + 4)
+    lens = decode_lens()  # the GPU decode measurement's lengths
+    dec = oracle.ref_decode if ref else oracle.decode
+    cfg4_s = _timed(lambda: dec(qd, kc, vc, lens, SCALE), reps=3)
+    cfg4_bytes = 2 * int(lens.sum()) * DEC_H * DEC_D * 2 + 2 * DEC_N * DEC_H * DEC_D * 2
+
+    cfg5 = None
+    if ref:
+        from dadgpt_amd import gpt2
+        cfg = gpt2.PRESETS["gpt2-124m"]
+        host = gpt2.init_params(cfg, synth.CFG5_SEED).float().cpu().numpy()
+        toks = synth.cfg5_prompts(cfg["vocab_size"])[0]
+        t16 = _timed(lambda: oracle.ref_gpt2_forward(host, cfg, toks[:16]))
+        t32 = _timed(lambda: oracle.ref_gpt2_forward(host, cfg, toks[:32]))
+        per_tok = (t32 - t16) / 16  # the marginal cost of one more token
+        prompts = synth.cfg5_prompts(cfg["vocab_size"])
+        work = sum(len(p) for p in prompts) + synth.CFG5_N * synth.CFG5_NEW
+        cfg5 = {"tokens_per_s_extrapolated": round(synth.CFG5_N * synth.CFG5_NEW /
+                                                   (work * per_tok), 3),
+                "seconds_per_token": round(per_tok, 4),
+                "sample": "one sequence through the reference's CPU GPT-2 forward at 16 and 32 "
+                          "tokens (fp32, single thread); the marginal per-token cost times "
+                          f"{work} token forwards (16 prompts + 16 x 128 generated tokens; the "
+                          "reference's CPU path has no KV cache), extrapolated"}
     return {
-        "value": float(f"{flops / dt / 1e12:.6g}"),
+        "value": float(f"{tfn:.6g}"),
         "unit": "TFLOP/s",
-        "cores": 1,
+        "cores": CPU_THREADS,
         "kind": kind,
-        "sample": (f"fp32 forward+backward of {n_slices} of {BH} (b,h) slices of B16 H12 T1024 "
-                   f"D64 (bf16-rounded inputs), single thread, {dt:.2f} s; algorithmic FLOPs "
-                   f"of those slices / wall time"),
-        "seconds": round(dt, 3),
+        "sample": (f"fp32 forward+backward of {n_slices * CPU_THREADS} of {BH} (b,h) slices of "
+                   f"B16 H12 T1024 D64 (bf16-rounded inputs), {n_slices} slices per thread on "
+                   f"{CPU_THREADS} threads, {dtn:.2f} s; algorithmic FLOPs of those slices / "
+                   f"wall time"),
+        "seconds": round(dtn, 3),
+        "host": {"cpu_model": _cpu_model(), "hardware_threads": os.cpu_count(),
+                 "threads_available": len(os.sched_getaffinity(0))},
+        "single_thread": {"value": float(f"{tf1:.6g}"), "unit": "TFLOP/s", "cores": 1,
+                          "sample": f"{n_slices} slices, one thread, {dt1:.2f} s"},
+        "cfg1_fwd_bwd_ms": round(cfg1_s * 1e3, 3),
+        "cfg4_decode": {"ms": round(cfg4_s * 1e3, 3),
+                        "gbps": round(cfg4_bytes / cfg4_s / 1e9, 3), "bytes": cfg4_bytes,
+                        "cores": 1},
+        "cfg5": cfg5,
     }
 
 
@@ -156,7 +251,7 @@ class Workload:
         self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
         self.delta = torch.empty(BH, T, device=dev)
 
-        lens_h = synth.uniform_int(1, DEC_L, DEC_N, synth.BASE_SEED ^ synth.TENSOR_ID["lens"])
+        lens_h = decode_lens()
         self.lens = torch.from_numpy(lens_h.astype(np.int32)).to(dev)
         # K and V rows actually read, plus q and out
         self.dec_bytes = int(2 * lens_h.sum() * DEC_H * DEC_D * 2 + 2 * DEC_N * DEC_H * DEC_D * 2)
@@ -170,6 +265,42 @@ class Workload:
     def fwd(self):
         self.A.flash_attention_forward_bf16(self.out, self.lse, self.q, self.k, self.v, BH, T, D,
                                             SCALE, None)
+
+    def fwd_cfg2(self):
+        """BASELINE config 2 (B8 H12 T1024 D64): the first 96 slices of the config 3 tensors."""
+        self.A.flash_attention_forward_bf16(self.out, self.lse, self.q, self.k, self.v, CFG2_BH,
+                                            T, D, SCALE, None)
+
+    def fp32_paths(self):
+        """The reference's precision at config 3: the fp32 flash kernels and the fp32
+        materialized path (hipBLASLt strided-batched GEMMs + fused row passes, [BH, T, T]
+        probabilities in HBM). Returns (flash fwd, flash bwd, materialized fwd, bwd)."""
+        import torch
+        from dadgpt_amd import gpt2
+        A = self.A
+        f = [t.float() for t in (self.q, self.k, self.v, self.g)]
+        q, k, v, g = f
+        out, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
+        lse, delta = torch.empty(BH, T, device="cuda"), torch.empty(BH, T, device="cuda")
+        probs = torch.empty(BH, T, T, device="cuda")
+        dsc = torch.empty(BH, T, T, device="cuda")
+        blas = gpt2.Blas()
+        self._fp32 = (f, out, dq, dk, dv, lse, delta, probs, dsc, blas)
+
+        def ffwd():
+            A.flash_attention_forward(out, lse, q, k, v, BH, T, D, SCALE)
+
+        def fbwd():
+            A.flash_attention_backward(dq, dk, dv, delta, g, out, lse, q, k, v, BH, T, D,
+                                             SCALE)
+
+        def mfwd():
+            blas.attention_materialized_forward(out, probs, q, k, v, BH, T, D, SCALE)
+
+        def mbwd():
+            blas.attention_materialized_backward(dq, dk, dv, dsc, g, probs, q, k, v, BH, T, D,
+                                                 SCALE)
+        return ffwd, fbwd, mfwd, mbwd
 
     def bwd(self):
         self.A.flash_attention_backward_bf16(self.dq, self.dk, self.dv, self.delta, self.g,
@@ -366,13 +497,14 @@ def main():
     # (a single pass timed the later variants up to 25% slower than interleaved rounds do)
     tok_fwd, tok_bwd = wl.tokens()
     drop_fwd, drop_bwd = wl.dropout()
-    for _ in range(5):
-        tok_fwd()
-        tok_bwd()
-        drop_fwd()
-        drop_bwd()
+    f32_fwd, f32_bwd, mat_fwd, mat_bwd = wl.fp32_paths()
+    for _ in range(5):  # also builds and tunes the hipBLASLt plans of the materialized path
+        for fn in (tok_fwd, tok_bwd, drop_fwd, drop_bwd, f32_fwd, f32_bwd, mat_fwd, mat_bwd):
+            fn()
     timed = {"fwd": wl.fwd, "bwd_dq": wl.phase(1), "bwd_dkdv": wl.phase(2), "bwd": wl.bwd,
-             "tok_fwd": tok_fwd, "tok_bwd": tok_bwd, "drop_fwd": drop_fwd, "drop_bwd": drop_bwd}
+             "fwd_cfg2": wl.fwd_cfg2, "tok_fwd": tok_fwd, "tok_bwd": tok_bwd,
+             "drop_fwd": drop_fwd, "drop_bwd": drop_bwd, "f32_fwd": f32_fwd, "f32_bwd": f32_bwd,
+             "mat_fwd": mat_fwd, "mat_bwd": mat_bwd}
     best = {}
     for _ in range(3):
         for name, fn in timed.items():
@@ -426,6 +558,26 @@ def main():
         "bwd_tflops": round(BWD_FLOPS / (tok_ms[1] * 1e-3) / 1e12, 2),
         "layout": "q,k,v in one token-major [B*T, 3*H*D] buffer, out/dout [B*T, H*D], "
                   "dq,dk,dv into one [B*T, 3*H*D] buffer"}
+    cfg2_tf = FWD_FLOPS * CFG2_BH / BH / (best["fwd_cfg2"] * 1e-3) / 1e12
+    comps["fwd_cfg2"] = {"ms": round(best["fwd_cfg2"], 5),
+                         "algorithmic_gflop": round(FWD_FLOPS * CFG2_BH / BH / 1e9, 3),
+                         "tflops": round(cfg2_tf, 2),
+                         "frac_mfma_peak": round(cfg2_tf / PEAK_BF16_TFLOPS, 4),
+                         "config": "BASELINE config 2: B8 H12 T1024 D64 bf16 causal forward"}
+    for key, (fk, bk), what in (
+            ("fp32_flash", ("f32_fwd", "f32_bwd"),
+             "fp32 flash kernels (fp32 MFMA), config 3 shape"),
+            ("fp32_materialized", ("mat_fwd", "mat_bwd"),
+             "fp32 materialized path (hipBLASLt fp32 strided-batched GEMMs over the full "
+             "T x T scores + fused row passes; executes twice the causal FLOPs), config 3 "
+             "shape")):
+        ftf = FWD_FLOPS / (best[fk] * 1e-3) / 1e12
+        btf = BWD_FLOPS / (best[bk] * 1e-3) / 1e12
+        comps[key] = {"fwd_ms": round(best[fk], 5), "bwd_ms": round(best[bk], 5),
+                      "fwd_tflops": round(ftf, 2), "bwd_tflops": round(btf, 2),
+                      "fwd_frac_fp32_mfma_peak": round(ftf / PEAK_F32_TFLOPS, 4),
+                      "bwd_frac_fp32_mfma_peak": round(btf / PEAK_F32_TFLOPS, 4),
+                      "peak_tflops": PEAK_F32_TFLOPS, "what": what}
     comps["dropout"] = {
         "p": 0.1, "fwd_ms": round(drop_ms[0], 5), "bwd_ms": round(drop_ms[1], 5),
         "fwd_tflops": round(FWD_FLOPS / (drop_ms[0] * 1e-3) / 1e12, 2),
