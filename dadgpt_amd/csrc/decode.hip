@@ -22,16 +22,29 @@
 // A cache that fits one chunk is written directly. A longer one merges inside the same kernel:
 // each chunk publishes an fp32 partial (max in log2 units, sum, unnormalised o) and counts
 // itself on a per-cache counter; the chunk that arrives last merges all partials, writes the
-// output and rearms the counter to zero. The partials and the counter move only through
-// agent-scope relaxed accesses (stores, loads and the atomic with the device-scope cache bit),
-// each coherent across the XCDs on its own, and the stores are complete (s_waitcnt vmcnt(0))
-// before the counter is incremented. No agent-scope fence is used: on this part a release
-// fence writes back the whole L2 (the L2s of the 8 XCDs are not coherent with each other),
-// which made the first fence-based version of this kernel 17x slower.
+// output and rearms the counter to zero.
+//
+// Ordering of that merge. The partials and the counter move only through agent-scope relaxed
+// atomic accesses, and the rules that make this correct are those of the AMDGPU memory model
+// for gfx942/gfx950 (LLVM AMDGPUUsage, "Memory Model GFX942"): a monotonic agent-scope atomic
+// store, load or read-modify-write is a global_store / global_load / global_atomic with sc1 = 1,
+// which is coherent across the 8 XCDs on its own (it bypasses the XCD-local L2), and
+// s_waitcnt vmcnt(0) after a store waits for the store to complete. The publish sequence
+// (sc1 stores, vmcnt(0), sc1 atomic increment; the last arriver reads with sc1 loads) is
+// the compiler's agent-scope release / acquire sequence without its L2 writeback and
+// invalidate, which only plain (non-sc1) accesses need. A release fence here writes back the
+// whole L2, which made the first fence-based version of this kernel 17x slower. Other targets
+// compile the standard release / acquire pair (DADGPT_DECODE_SC1_COHERENT below).
 #include <mutex>
 
 #include "common.hpp"
 #include "kernels.hpp"
+
+#if defined(__gfx942__) || defined(__gfx950__) || !defined(__HIP_DEVICE_COMPILE__)
+#define DADGPT_DECODE_SC1_COHERENT 1
+#else
+#define DADGPT_DECODE_SC1_COHERENT 0
+#endif
 
 namespace dadgpt {
 namespace {
@@ -226,6 +239,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
       st_agent(my + 1, wl);
     }
   }
+#if DADGPT_DECODE_SC1_COHERENT
   // This thread's stores are complete at the device coherence point (the asm is also a
   // compiler barrier for them); the barrier then covers the whole workgroup's.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -235,6 +249,14 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
                                                    __HIP_MEMORY_SCOPE_AGENT);
     sm_last = before == (unsigned)(nch - 1);
   }
+#else
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned before = __hip_atomic_fetch_add(counter + hrow, 1u, __ATOMIC_ACQ_REL,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    sm_last = before == (unsigned)(nch - 1);
+  }
+#endif
   __syncthreads();
   if (!sm_last) return;
 
