@@ -16,8 +16,8 @@
 // MFMA as B operands from registers; the operands that must be read along the score dimension
 // (Q^T and dO^T in the dK/dV kernel, K^T in the dQ kernel) are read across the rows of the
 // row-major LDS tiles with ds_read_b64_tr_b16, so every tile is staged once, row-major.
-// Masking is compiled only into the blocks that straddle the diagonal (template DIAG), so the
-// other blocks run branch-free. The streamed tiles (Q and dO for dK/dV, K and V for dQ) are
+// Masking runs only in the blocks that straddle the diagonal, behind a uniform branch around
+// the instructions that zero P. The streamed tiles (Q and dO for dK/dV, K and V for dQ) are
 // double-buffered in LDS through direct global->LDS loads, one tile ahead of the compute.
 // STRIDED and DROP instantiations as in the forward: per-tensor strides, and dropout with
 // the keep bits regenerated (dV from P keep/(1-p), dS = P (dP keep/(1-p) - delta)).
@@ -94,14 +94,17 @@ constexpr int kKW = 32;  // keys per wave
 //   s  = -lse/scale + Q K^T         so P = exp2(c s) with c = scale log2(e)
 //   dp = -delta + dO V^T            so P dp = P (dP - delta) = dS
 // which leaves two multiplies and an exp2 per score on the VALU. slc holds the tile's
-// -lse/scale, sdl its -delta. MASK zeroes P for keys after the query and for tile rows past S
-// (rows_left = S - r0; those rows hold copies of row S-1).
+// -lse/scale, sdl its -delta. `mask` zeroes P for keys after the query and for tile rows past
+// S (rows_left = S - r0; those rows hold copies of row S-1). It is a runtime flag, not a
+// template parameter, and guards only the few instructions that zero P: with two inlined copies
+// of the block the compiler gave their MFMAs different accumulator registers and copied all 64
+// accumulator values back after every block.
 //
 // With dropout (DROP; f = keep/(1-p) from bit 8j+e of `keep`): dV accumulates (P f)^T dO and
 // dS = P (dP f - delta), so dp starts from zero and -delta is read separately.
-template <int D, bool MASK, bool DROP>
-__device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dvacc)[D / 32],
-                                           const bf16x8 (&kop)[D / 16],
+template <int D, bool DROP>
+__device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
+                                           f32x16 (&dvacc)[D / 32], const bf16x8 (&kop)[D / 16],
                                            const bf16x8 (&vop)[D / 16], const bf16* sq,
                                            const bf16* sdo, const float* slc, const float* sdl,
                                            int qb, int key_minus_r0, int rows_left, int lane,
@@ -149,9 +152,20 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
   bf16x8 pb[2], dsb[2];
   f32x16 nd;  // -delta of the block's queries (dropout only)
   if constexpr (DROP) stats(sdl, nd);
+  float pr[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) pr[i] = fast_exp2(s[i] * c);
+  if (mask) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int qt0 = 32 * qb + 16 * j + 8 * hi;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        pr[8 * j + e] = (key_minus_r0 > qt0 + e || qt0 + e >= rows_left) ? 0.f : pr[8 * j + e];
+    }
+  }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int qt0 = 32 * qb + 16 * j + 8 * hi;
     u32x4 wp, wd;
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2) {
@@ -159,9 +173,7 @@ __device__ __forceinline__ void dkdv_block(f32x16 (&dkacc)[D / 32], f32x16 (&dva
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int e = 2 * e2 + h;
-        float pe = fast_exp2(s[8 * j + e] * c);
-        // key > query (key - r0 > tile query index), or a row past S
-        if (MASK) pe = (key_minus_r0 > qt0 + e || qt0 + e >= rows_left) ? 0.f : pe;
+        const float pe = pr[8 * j + e];
         if constexpr (DROP) {
           const float f = keep_factor(keep, 8 * j + e, dscale);
           p[h] = pe * f;
@@ -292,12 +304,9 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
         uint32_t keep = 0;
         if constexpr (DROP) keep = keep_col16(dr, (uint64_t)bh * S + qlo, kw0, lane);
         // some key after some query, or rows past S: mask
-        if (edge || qlo < kw0 + kKW - 1)
-          dkdv_block<D, true, DROP>(dkacc, dvacc, kop, vop, cq, cdo, st[cb][0], st[cb][1], qb,
-                                    key - r0, S - r0, lane, c, keep, dr.scale);
-        else
-          dkdv_block<D, false, DROP>(dkacc, dvacc, kop, vop, cq, cdo, st[cb][0], st[cb][1], qb,
-                                     key - r0, S - r0, lane, c, keep, dr.scale);
+        dkdv_block<D, DROP>(edge || qlo < kw0 + kKW - 1, dkacc, dvacc, kop, vop, cq, cdo,
+                            st[cb][0], st[cb][1], qb, key - r0, S - r0, lane, c, keep,
+                            dr.scale);
       }
     }
     wait_vm_lds<0>();
@@ -324,8 +333,9 @@ constexpr int kQW = 32;  // queries per wave
 // One 32-key chunk (tile keys 32*kb ..) against the wave's 32 queries. Register 8j+e of lane
 // half hi holds tile key 32kb + 16j + 8hi + e. With dropout (DROP), dS = P (dP * f - delta)
 // with f = keep/(1-p) from bit 8j+e of `keep`.
-template <int D, bool DIAG, bool DROP>
-__device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (&qop)[D / 16],
+template <int D, bool DROP>
+__device__ __forceinline__ void dq_chunk(bool diag, f32x16 (&dqacc)[D / 32],
+                                         const bf16x8 (&qop)[D / 16],
                                          const bf16x8 (&doop)[D / 16], const bf16* sk,
                                          const bf16* sv, int kb, int qrow_minus_k0, float lse2,
                                          float dlt, int lane, float scale_log2, uint32_t keep,
@@ -339,6 +349,14 @@ __device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (
     s = mfma32(lds_op(sk, rm_off<D>(krow, 2 * ds + hi)), qop[ds], s);
     dp = mfma32(lds_op(sv, rm_off<D>(krow, 2 * ds + hi)), doop[ds], dp);
   }
+  float pr[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) pr[i] = fast_exp2(fmaf(s[i], scale_log2, -lse2));
+  if (diag) {  // runtime flag around the zeroing only (see dkdv_block)
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      pr[i] = 32 * kb + 16 * (i / 8) + 8 * hi + i % 8 > qrow_minus_k0 ? 0.f : pr[i];
+  }
   bf16x8 dsb[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -349,8 +367,7 @@ __device__ __forceinline__ void dq_chunk(f32x16 (&dqacc)[D / 32], const bf16x8 (
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int e = 2 * e2 + h;
-        float p = fast_exp2(fmaf(s[8 * j + e], scale_log2, -lse2));
-        if (DIAG) p = 32 * kb + 16 * j + 8 * hi + e > qrow_minus_k0 ? 0.f : p;
+        const float p = pr[8 * j + e];
         if constexpr (DROP)
           d[h] = p * fmaf(dp[8 * j + e], keep_factor(keep, 8 * j + e, dscale), -dlt);
         else
@@ -416,7 +433,7 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
 #pragma unroll
   for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
 
-  // Keys past S read row S-1; every chunk holding such keys is a DIAG chunk (the key is after
+  // Keys past S read row S-1; every chunk holding such keys is a diagonal chunk (the key is after
   // every valid query), so they are masked. The first tile loads alongside the operands
   // above, under one wait (see the dK/dV kernel).
   using Dma = DmaTile<D, kWaves>;
@@ -456,12 +473,9 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
         if (klo > q0 + kQW - 1) continue;    // every key after every query of the wave
         uint32_t keep = 0;
         if constexpr (DROP) keep = keep_row16(dr, (uint64_t)bh * S + qrow, klo, hi);
-        if (klo + 31 > q0)                   // some key after some query: mask
-          dq_chunk<D, true, DROP>(dqacc, qop, doop, ck, cv, kb, qrow - k0, lse2, dlt, lane,
-                                  scale_log2, keep, dr.scale);
-        else
-          dq_chunk<D, false, DROP>(dqacc, qop, doop, ck, cv, kb, qrow - k0, lse2, dlt, lane,
-                                   scale_log2, keep, dr.scale);
+        // some key after some query: mask
+        dq_chunk<D, DROP>(klo + 31 > q0, dqacc, qop, doop, ck, cv, kb, qrow - k0, lse2, dlt,
+                          lane, scale_log2, keep, dr.scale);
       }
     }
     wait_vm_lds<0>();
