@@ -4,12 +4,13 @@ The keep bits are a fixed function of (seed, bh*S + query, key) (Philox4x32-10; 
 oracle implements the same definition and is pinned by the generator's published
 known-answer vectors), so for a given seed the GPU kernels and the oracle drop the same
 probabilities, and the results are compared at the bf16 tolerances: O <= 2e-2, lse <= 1e-3,
-dQ/dK/dV <= 5e-2 (max-abs, against the fp32 oracle on the same bf16-rounded inputs). Kept
-probabilities are scaled by 1/(1-p), and so are O, dP's kept terms, dS and the gradients
-built from them, together with every bf16 rounding of those values on the way (P f as the
-P V operand, dS as the dQ and dK operands, the stored outputs): at p = 0.9, |O| reaches 16,
-where storing it in bf16 alone moves it by up to 0.03. O and the gradients are therefore held
-to the tolerance times 1/(1-p), the factor their values carry; lse carries no factor.
+dQ/dK/dV <= 5e-2 (max-abs, against the fp32 oracle on the same bf16-rounded inputs), for every
+drop rate up to 0.5. Kept probabilities are scaled by 1/(1-p), and so are O, dP's kept terms,
+dS and the gradients built from them, together with every bf16 rounding of those values on the
+way (P f as the P V operand, dS as the dQ and dK operands, the stored outputs): at p = 0.9,
+|O| reaches 16, where storing it in bf16 alone moves it by up to 0.03. Above p = 0.5, O and the
+gradients are therefore held to the tolerance times 1/(1-p), the factor their values carry;
+lse carries no factor.
 """
 import math
 
@@ -33,9 +34,12 @@ def case(msg):
 
 
 def within_scaled(got, ref, tol, p, what):
-    """max |got - ref| <= tol / (1 - p): the bf16 tolerance at the magnitude dropout scales to."""
+    """max |got - ref| <= tol for p <= 0.5; above, tol / (1 - p): the bf16 tolerance at the
+    magnitude dropout scales the values to."""
+    bound = tol if p <= 0.5 else tol / (1.0 - p)
     err = max_abs(got, ref)
-    assert err <= tol / (1.0 - p), f"{what}: max-abs {err:.3e} > {tol / (1.0 - p):.3e}"
+    print(f"  {what}: max-abs {err:.3e} (p={p}, bound {bound:.3e})", flush=True)
+    assert err <= bound, f"{what}: max-abs {err:.3e} > {bound:.3e}"
 
 
 def dev(x):
