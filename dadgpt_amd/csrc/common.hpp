@@ -79,12 +79,6 @@ __device__ __forceinline__ float sum_halves(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// acc + lo + hi of a packed bf16 pair, in fp32 (v_dot2_f32_bf16 against (1, 1)).
-__device__ __forceinline__ float dot2_bf16_ones(uint32_t w, float acc) {
-  const bf16x2 one = {static_cast<bf16>(1.0f), static_cast<bf16>(1.0f)};
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
-}
-
 // Flips the sign of the 8 bf16 values (exact).
 __device__ __forceinline__ bf16x8 neg_bf16x8(bf16x8 x) {
   return as_bf16x8(as_u32x4(x) ^ 0x80008000u);
