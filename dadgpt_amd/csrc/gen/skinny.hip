@@ -6,12 +6,14 @@
 // many CUs; the work around each projection is folded into it, because at this size every
 // dependent kernel costs its launch plus a memory round trip.
 //
-// Workgroup = 16 output columns x W waves: wave w takes the K range [w K/W, (w+1) K/W)
-// (W = 4, or 16 for K >= 2048) and issues all its weight loads up front; the partial products
-// are summed through LDS and the epilogue runs in the same workgroup, so no result crosses
-// workgroups. The grid is N/16 workgroups (144 for the QKV projection of GPT-2 124M, 192 for
-// fc1, 48 for Wo and fc2). The epilogue's own inputs (bias, residual, cache row) are loaded
-// first, so their latency hides under the weight stream.
+// Workgroup = 16 output columns (4 or 8 for narrow projections, below) x W waves: wave w takes
+// the K range [w K/W, (w+1) K/W) (W = 4, or 16 for K >= 2048) and issues all its weight loads
+// up front; the partial products are summed through LDS and the epilogue runs in the same
+// workgroup, so no result crosses workgroups. The grid is N/16 workgroups for the LayerNorm
+// projections (144 for the QKV projection of GPT-2 124M, 192 for fc1) and N/4 for Wo and fc2
+// (192 instead of 48, which spreads their weight streams over most CUs). The epilogue's own
+// inputs (bias, residual, cache row) are loaded first, so their latency hides under the
+// weight stream.
 // v_mfma_f32_16x16x32_bf16: lane l supplies A[l%16][8(l/16)+e] and B[8(l/16)+e][l%16] and
 // holds D[4(l/16)+r][l%16]. Here A = W^T (rows = output columns n) and B = the activations
 // transposed (columns = rows m of the batch), so D = out^T.
@@ -68,8 +70,10 @@ struct Epi {  // the epilogue's per-lane inputs, loaded (not yet converted) befo
   int pos = 0;
 };
 
-// WAVES waves, each over a K range of KW (K = WAVES * KW).
-template <int PRO, int EPI, int KW, int WAVES>
+// WAVES waves, each over a K range of KW (K = WAVES * KW); COLS (16, 8 or 4) output columns
+// per workgroup, so that a projection with few columns still spreads its weight stream over
+// most CUs (the MFMA's other rows are zero and never stored).
+template <int PRO, int EPI, int KW, int WAVES, int COLS>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
   constexpr int K = WAVES * KW, NT = KW / 32;  // MFMA k-steps per wave
   constexpr int LDS_K = PRO == kProLn ? K : 1;
@@ -77,14 +81,16 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 act[kRows][LDS_K + kPad];
   __shared__ f32x4 red[WAVES - 1][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int n0 = blockIdx.x * 16, kw0 = wave * KW;
+  static_assert(COLS == 16 || COLS == 8 || COLS == 4, "column tile");
+  const int n0 = blockIdx.x * COLS, kw0 = wave * KW;
   const int M = a.M, N = a.N;
   const int m = lane & 15, nl = n0 + 4 * (lane >> 4);  // this lane's row and first column
+  const bool mine = 4 * (lane >> 4) < COLS;            // its columns belong to this workgroup
   const bool full4 = nl + 3 < N;                       // its 4 columns all exist
 
   // 0. the epilogue's inputs (wave 0 finishes the outputs), first in the load queue
   Epi<EPI> ep;
-  if (wave == 0 && m < M && nl < N) {
+  if (wave == 0 && mine && m < M && nl < N) {
     if constexpr (EPI == kEpiQkv) {
       ep.pos = a.pos[m];
       ep.bias_f = *reinterpret_cast<const f32x4*>(a.bias_f + nl);  // 3d is a multiple of 16
@@ -123,10 +129,13 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
   // 1. this wave's weight operands: row n of W^T (clamped to N-1 past the edge; those columns
   //    are not stored), 8 k per lane and step; all issued before anything waits
   bf16x8 w[NT];
-  {
+  if (COLS == 16 || (lane & 15) < COLS) {
     const bf16* wp = a.wt + (size_t)min(n0 + (lane & 15), N - 1) * K + kw0 + 8 * (lane >> 4);
 #pragma unroll
     for (int t = 0; t < NT; ++t) w[t] = *reinterpret_cast<const bf16x8*>(wp + 32 * t);
+  } else {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) w[t] = bf16x8{};
   }
   // (nothing that consumes a load moves above here: every load is in flight before the first
   // wait)
@@ -179,7 +188,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
   if (wave > 0) return;
 #pragma unroll
   for (int i = 0; i < WAVES - 1; ++i) acc += red[i][lane];
-  if (m >= M || nl >= N) return;
+  if (!mine || m >= M || nl >= N) return;
   if constexpr (EPI == kEpiStore) {
     float* o = a.out + (size_t)m * N + nl;
     if (full4 && (((size_t)m * N + nl) & 3) == 0)
@@ -240,7 +249,17 @@ hipError_t launch_kw(const SkinnyArgs& a, hipStream_t s) {
   if constexpr (PRO == kProLn && (WAVES != 4 || 4 * KW > kMaxLnK)) {
     return hipErrorInvalidValue;
   } else {
-    skinny_kernel<PRO, EPI, KW, WAVES><<<dim3((a.N + 15) / 16), 64 * WAVES, 0, s>>>(a);
+    // Narrower column tiles for the row-prologue projections while 16-column tiles would
+    // leave most of the 256 CUs idle (Wo and fc2 of GPT-2: 48 workgroups). The LayerNorm
+    // prologue stays at 16 columns: every workgroup recomputes the rows' statistics, and
+    // more workgroups made QKV slower (8.4 against 6.7 us at 8 columns).
+    if (PRO == kProLn || a.N >= 16 * 160) {
+      skinny_kernel<PRO, EPI, KW, WAVES, 16><<<dim3((a.N + 15) / 16), 64 * WAVES, 0, s>>>(a);
+    } else if (a.N >= 8 * 160) {
+      skinny_kernel<PRO, EPI, KW, WAVES, 8><<<dim3((a.N + 7) / 8), 64 * WAVES, 0, s>>>(a);
+    } else {
+      skinny_kernel<PRO, EPI, KW, WAVES, 4><<<dim3((a.N + 3) / 4), 64 * WAVES, 0, s>>>(a);
+    }
     return hipGetLastError();
   }
 }
