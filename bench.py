@@ -358,10 +358,10 @@ class Workload:
                                                    3 * HD, B, H, T, D, SCALE)
         return fwd, bwd
 
-    def decode(self, i):
+    def decode(self, i, lens=None, n_seq=DEC_N):
         self.A.decode_attention(self.od, self.qd, self.kcs[i % self.ncopy],
-                                self.vcs[i % self.ncopy], self.lens, DEC_N, DEC_H, DEC_L, DEC_D,
-                                SCALE, self.ws, None)
+                                self.vcs[i % self.ncopy], self.lens if lens is None else lens,
+                                n_seq, DEC_H, DEC_L, DEC_D, SCALE, self.ws, None)
 
 
 def profile_sample(wl, reps):
@@ -530,6 +530,28 @@ def main():
     torch.cuda.synchronize()
     dec_ms = event_time_ms(graph.replay, 5, torch.cuda.current_stream()) / per_graph
     dec_gbps = wl.dec_bytes / (dec_ms * 1e-3) / 1e9
+
+    # the same kernel and cache buffers on uniform lengths, to split cfg4's time: every cache
+    # one 512-key chunk (no split, no raggedness), and every cache 1024 keys (two chunks,
+    # merged by the last-arriving chunk), each over ~50 MB
+    def decode_case(n_seq, length):
+        lens = torch.full((n_seq,), length, dtype=torch.int32, device="cuda")
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(per_graph):
+                wl.decode(i, lens, n_seq)
+        g.replay()
+        torch.cuda.synchronize()
+        ms = event_time_ms(g.replay, 5, torch.cuda.current_stream()) / per_graph
+        nbytes = 2 * n_seq * length * DEC_H * DEC_D * 2 + 2 * n_seq * DEC_H * DEC_D * 2
+        return {"us_per_launch": round(ms * 1e3, 3), "bytes": nbytes,
+                "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    dec_cases = {"one_chunk_per_cache": dict(decode_case(DEC_N, 512),
+                                             config="32 seqs x 12 heads x 512 keys"),
+                 "two_chunks_per_cache": dict(decode_case(DEC_N // 2, 1024),
+                                              config="16 seqs x 12 heads x 1024 keys")}
+    print(f"[bench] decode on uniform lengths: {json.dumps(dec_cases)}", file=sys.stderr,
+          flush=True)
     # eager launches over the rotating copies (launch gaps included)
     eager_dec_ms = event_time_ms(lambda it=iter(range(10 ** 9)): wl.decode(next(it)),
                                  args.reps, stream)
@@ -605,6 +627,7 @@ def main():
                            "what": "torch copy_ of a buffer of the decode's byte count (rotating "
                                    "sources, eager): the rate a vendor streaming kernel reaches "
                                    "on this box, to set gbps against"},
+                       "uniform_lengths": dec_cases,
                        "cache_copies": wl.ncopy, "hbm_bytes_per_launch": traffic.get("decode"),
                        "config": "32 seqs, H12, D64, bf16 cache [32,12,1024,64], lens U[1,1024]"}
 
