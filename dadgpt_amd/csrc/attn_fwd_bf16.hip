@@ -46,7 +46,8 @@ namespace {
 // Geometry: NQB 32-query blocks per wave, WAVES waves per workgroup, MINB workgroups per CU
 // (the register budget: 512 / (MINB * WAVES / 4) per lane). 4 waves of one query block and 3
 // workgroups per CU (3 waves per SIMD) measured fastest; 4 per SIMD (the kernel fits 128
-// registers), 8- and 16-wave workgroups and two query blocks per wave were no faster.
+// registers), 8- and 16-wave workgroups and two query blocks per wave were no faster, and
+// 2-wave workgroups (twice as many, for small batches) were slower at both B16 and B8.
 #ifndef DADGPT_FWD_NQB
 #define DADGPT_FWD_NQB 1
 #endif
