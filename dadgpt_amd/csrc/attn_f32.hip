@@ -30,6 +30,10 @@ namespace dadgpt {
 namespace {
 
 constexpr int kWaves = 4;             // waves per workgroup
+// Two workgroups per CU, i.e. at most 256 registers a lane: dK/dV would otherwise take 320 and
+// run one wave per SIMD. With the cap nothing spills at D = 64 except 4 registers of the
+// dropout dK/dV, and the backward runs 15% faster (the forward 3%).
+constexpr int kMinBlocks = 2;
 constexpr int kRows = 32 * kWaves;    // rows (queries or keys) a workgroup owns
 constexpr int kTile = 64;             // rows per staged tile (two 32-row chunks)
 
@@ -161,7 +165,7 @@ __device__ __forceinline__ float* stage_slot(float* first, float* second, int wa
 // ------------------------------------------------------------------------------ forward
 
 template <int D, bool DROP>
-__global__ __launch_bounds__(64 * kWaves) void fwd_f32_kernel(
+__global__ __launch_bounds__(64 * kWaves, kMinBlocks) void fwd_f32_kernel(
     float* __restrict__ out, float* __restrict__ lse, const float* __restrict__ q,
     const float* __restrict__ k, const float* __restrict__ v, int S, float scale,
     const DropParams dr) {
@@ -257,7 +261,7 @@ __global__ __launch_bounds__(256) void delta_f32_kernel(float* __restrict__ delt
 }
 
 template <int D, bool DROP>
-__global__ __launch_bounds__(64 * kWaves) void dkdv_f32_kernel(
+__global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
     float* __restrict__ dk, float* __restrict__ dv, const float* __restrict__ q,
     const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, float scale,
@@ -337,7 +341,7 @@ __global__ __launch_bounds__(64 * kWaves) void dkdv_f32_kernel(
 }
 
 template <int D, bool DROP>
-__global__ __launch_bounds__(64 * kWaves) void dq_f32_kernel(
+__global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
     float* __restrict__ dq, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta, int S, float scale, const DropParams dr) {
