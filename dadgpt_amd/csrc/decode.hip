@@ -10,7 +10,8 @@
 // workgroup per chunk; wave w owns keys [chunk*C + w*KW, chunk*C + (w+1)*KW). Every 16-byte
 // load instruction of a wave covers whole key rows (bf16 D=64: 8 lanes x 16 B per row, 8 rows
 // per instruction, a contiguous 1 KiB), all K and V loads of a wave are issued before any
-// arithmetic, and they carry the non-temporal hint (the cache is streamed once). The 8 waves
+// arithmetic, and they carry the non-temporal hint (the cache is streamed once). bf16 scores
+// are v_dot2_f32_bf16 on the packed q and K words, so neither side is unpacked. The 8 waves
 // merge (max, sum, o) in LDS with the logsumexp rule. Chunks are small enough that the work
 // of a long cache spreads over several CUs: one CU streaming a whole 1024-key cache alone was
 // the tail of the launch.
@@ -64,6 +65,18 @@ struct Elem<bf16> {
       f[2 * i + 1] = bf16_hi(w[i]);
     }
   }
+  // q . k over the 8 bf16 pairs of two 16-byte words: four v_dot2_f32_bf16 on the packed
+  // operands (bf16 products are exact in fp32), with no unpacking of either side.
+  static __device__ __forceinline__ float dot(const u32x4& q, const u32x4& k) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t qi = q[i], ki = k[i];
+      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, qi),
+                                            __builtin_bit_cast(bf16x2, ki), acc, false);
+    }
+    return acc;
+  }
   static __device__ __forceinline__ bf16 from(float x) { return static_cast<bf16>(x); }
 };
 template <>
@@ -72,6 +85,12 @@ struct Elem<float> {
   static __device__ __forceinline__ void unpack(const u32x4& w, float* f) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(w[i]);
+  }
+  static __device__ __forceinline__ float dot(const u32x4& q, const u32x4& k) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = fmaf(__uint_as_float(q[i]), __uint_as_float(k[i]), acc);
+    return acc;
   }
   static __device__ __forceinline__ float from(float x) { return x; }
 };
@@ -150,6 +169,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
   for (int e = 0; e < EPL; ++e) o[e] = 0.f;
 
   if (key0 < L) {  // wave-uniform: waves past the length skip their loads
+    // q first (it is small and read by every chunk of the cache), kept packed.
+    const u32x4 qw = ld_g128u(q + hrow * D + sub * EPL);
     // Rows past the length load row L-1 instead (valid, since key0 < L) and are masked out
     // below: the loads stay unconditional, so the compiler issues all of them back to back.
     u32x4 kr[NLD], vr[NLD];
@@ -163,8 +184,6 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
       const int key = min(key0 + i * KPL + grp, L - 1);
       vr[i] = ld_stream(vh + (size_t)key * D);
     }
-    float qf[EPL];
-    Elem<T>::unpack(ld_g128u(q + hrow * D + sub * EPL), qf);
     // Keep the scheduler from sinking loads towards their uses: all of them stay in flight.
     __builtin_amdgcn_sched_barrier(0);
 
@@ -172,11 +191,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
     float s[NLD];
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      float kf[EPL];
-      Elem<T>::unpack(kr[i], kf);
-      float acc = 0.f;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc = fmaf(qf[e], kf[e], acc);
+      float acc = Elem<T>::dot(qw, kr[i]);
 #pragma unroll
       for (int off = 1; off < LPR; off <<= 1) acc += __shfl_xor(acc, off, 64);
       const int key = key0 + i * KPL + grp;
