@@ -155,11 +155,13 @@ class Blas:
 
     def __init__(self):
         self._h = ctypes.c_void_p()
+        # bound now: at interpreter exit __del__ may run after this module's globals are gone
+        self._destroy = gen_lib().dadgpt_blas_destroy
         _check(gen_lib().dadgpt_blas_create(ctypes.byref(self._h)))
 
     def close(self):
-        if self._h:
-            gen_lib().dadgpt_blas_destroy(self._h)
+        if getattr(self, "_h", None):
+            self._destroy(self._h)
             self._h = ctypes.c_void_p()
 
     __del__ = close
@@ -282,6 +284,7 @@ class GPT2:
         self.params = params
         self.max_batch = max_batch
         self._m = ctypes.c_void_p()
+        self._destroy = gen_lib().dadgpt_gpt2_destroy  # bound now, as in Blas
         torch.cuda.synchronize()  # the arena may still be being written on torch's stream
         _check(gen_lib().dadgpt_gpt2_create(ctypes.byref(self.cfg), params.data_ptr(), max_batch,
                                             ATTENTION[attention] |
@@ -290,8 +293,8 @@ class GPT2:
         self.attention, self.projections = attention, projections
 
     def close(self):
-        if self._m:
-            gen_lib().dadgpt_gpt2_destroy(self._m)
+        if getattr(self, "_m", None):
+            self._destroy(self._m)
             self._m = ctypes.c_void_p()
 
     __del__ = close
