@@ -97,20 +97,21 @@ hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* 
 
 // ---- skinny projections of the decode step (skinny.hip) ----
 
-enum SkinnyPrologue { kProRows = 0, kProLn = 1 };
+enum SkinnyPrologue { kProRows = 0, kProLn = 1, kProRowsBlocked = 2 };
+constexpr int kSkinnyRows = 16;  // rows of the skinny path; kEpiGelu's g holds this many
 enum SkinnyEpilogue { kEpiStore = 0, kEpiQkv = 1, kEpiGelu = 2, kEpiResidual = 3 };
 
 struct SkinnyArgs {
   const bf16* wt;        // W^T [N][K]
   int M, N, K;           // rows (<= 16), columns, reduction length
-  const bf16* act;       // kProRows: A [M][K]
+  const bf16* act;       // kProRows: A [M][K]; kProRowsBlocked: A [K/32][16][32]
   const float* x;        // kProLn: A = LayerNorm(x [M][K]) * ln_w + ln_b
   const bf16* ln_w;
   const bf16* ln_b;
   float* out;            // kEpiStore: [M][N]
   const float* bias_f;   // kEpiQkv: fp32 bias [N]
   const bf16* bias;      // kEpiGelu, kEpiResidual: bias [N]
-  bf16* g;               // kEpiGelu: gelu(A W + bias) [M][N]
+  bf16* g;               // kEpiGelu: gelu(A W + bias), K-blocked [N/32][16][32]
   float* x_out;          // kEpiResidual: residual stream [M][N], += A W + bias in place
   void* q;               // kEpiQkv: q [M, H, dh] and k, v into the caches
   void* kcache;          //   [.., H, max_len, dh] at row pos[m]; bf16, or fp32 if qkv_fp32

@@ -411,9 +411,9 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
     SkinnyArgs f2{};
     f2.wt = m->w2_t[l];
     f2.M = n, f2.N = d, f2.K = c.d_ff;
-    f2.act = m->g;
+    f2.act = m->g;  // K-blocked by fc1's epilogue
     f2.bias = m->P(L.fc2_b), f2.x_out = m->x;
-    TRY_HIP(skinny_gemm(kProRows, kEpiResidual, f2, s), "skinny fc2");
+    TRY_HIP(skinny_gemm(kProRowsBlocked, kEpiResidual, f2, s), "skinny fc2");
   }
   // final LayerNorm, then the tied logits
   TRY_HIP(residual_layernorm<bf16>(m->x, nullptr, nullptr, m->h, m->P(m->off.lnf_w),
@@ -605,7 +605,9 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       (st = m->alloc_n(&m->lse, rows * c.n_heads, "lse")) ||
       (!proj32 && (st = m->alloc_n(&m->h, rows * d, "ln out"))) ||
       (!proj32 && (st = m->alloc_n(&m->a, rows * d, "attn in"))) ||
-      (!proj32 && (st = m->alloc_n(&m->g, rows * c.d_ff, "gelu out"))) ||
+      // (the skinny fc1 writes 16 K-blocked rows, whatever max_batch is)
+      (!proj32 && (st = m->alloc_n(&m->g, std::max(rows, (size_t)kSkinnyRows) * c.d_ff,
+                                   "gelu out"))) ||
       (proj32 && (st = m->alloc_n(&m->h32, rows * d, "ln out"))) ||
       (proj32 && (st = m->alloc_n(&m->a32, rows * d, "attn in"))) ||
       (proj32 && (st = m->alloc_n(&m->g32, rows * c.d_ff, "gelu out"))) ||

@@ -7,9 +7,9 @@
 // dependent kernel costs its launch plus a memory round trip.
 //
 // Workgroup = 16 output columns (4 or 8 for narrow projections, below) x W waves: wave w takes
-// the K range [w K/W, (w+1) K/W) (W = 4, or 16 for K >= 2048) and issues all its weight loads
-// up front; the partial products are summed through LDS and the epilogue runs in the same
-// workgroup, so no result crosses workgroups. The grid is N/16 workgroups for the LayerNorm
+// the K range [w K/W, (w+1) K/W) (W = 4, 8 for the LayerNorm prologue at K a multiple of 256,
+// 16 for K >= 2048) and issues all its weight loads up front; the partial products are summed
+// through LDS and the epilogue runs in the same workgroup, so no result crosses workgroups. The grid is N/16 workgroups for the LayerNorm
 // projections (144 for the QKV projection of GPT-2 124M, 192 for fc1) and N/4 for Wo and fc2
 // (192 instead of 48, which spreads their weight streams over most CUs). The epilogue's own
 // inputs (bias, residual, cache row) are loaded first, so their latency hides under the
@@ -21,12 +21,17 @@
 // Prologues (where the B operands come from):
 //   kProRows  bf16 activations act [M][K], read straight from global memory (L2-resident)
 //   kProLn    A = bf16(LayerNorm(x) w + b) of the fp32 residual stream x [M][K], computed by
-//             every workgroup into LDS (two-pass mean and variance, eps 1e-5); the weight
-//             loads are issued before it, so the stream runs under it
+//             every workgroup into LDS (two-pass mean and variance, eps 1e-5) with 16 or 32
+//             threads per row; the weight loads are issued right after its inputs, so the
+//             stream runs under it
+//   kProRowsBlocked  bf16 activations stored K-blocked, [K/32][16][32] (the kEpiGelu layout):
+//             each operand load of a wave is 1 KiB contiguous instead of 64 bytes of 16 rows,
+//             which halves the cache lines every workgroup pulls through its CU for fc2
 // Epilogues (per output element, after the bias):
 //   kEpiStore     out [M][N] fp32                                       (logits)
 //   kEpiQkv       q -> q [M, H, dh]; k, v -> the caches [.., H, max_len, dh] at row pos[m]
-//   kEpiGelu      g [M][N] = bf16(gelu(.))                              (fc1)
+//   kEpiGelu      g = bf16(gelu(.)), K-blocked for the next projection: element (m, n) at
+//                 ((n/32)*16 + m)*32 + n%32 (the buffer holds 16 rows)       (fc1)
 //   kEpiResidual  x [M][N] += .  (the residual stream, in place)        (Wo, fc2)
 #include <hip/hip_runtime.h>
 
@@ -40,7 +45,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kRows = 16;      // batch rows of the skinny path
+constexpr int kRows = kSkinnyRows;  // batch rows of the skinny path
 constexpr int kPad = 8;        // LDS row padding (16 bytes): conflict-free operand reads
 constexpr int kMaxLnK = 1024;  // kProLn: the prologue holds a row's values in registers
 
@@ -56,9 +61,10 @@ __device__ __forceinline__ f32x4 ld_bf16x4(const bf16* p) {
   return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
 }
 
-__device__ __forceinline__ float sum16(float v) {  // over the 16 lanes of a row group
+template <int TPR>
+__device__ __forceinline__ float sum_row(float v) {  // over the TPR lanes of a row group
 #pragma unroll
-  for (int off = 1; off < 16; off <<= 1) v += __shfl_xor(v, off, 64);
+  for (int off = 1; off < TPR; off <<= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
 
@@ -77,7 +83,7 @@ template <int PRO, int EPI, int KW, int WAVES, int COLS>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
   constexpr int K = WAVES * KW, NT = KW / 32;  // MFMA k-steps per wave
   constexpr int LDS_K = PRO == kProLn ? K : 1;
-  static_assert(PRO != kProLn || WAVES == 4, "the LayerNorm prologue uses 16 threads per row");
+  constexpr int TPR = 64 * WAVES / kRows;  // LayerNorm threads per row (16 or 32)
   __shared__ __attribute__((aligned(16))) bf16 act[kRows][LDS_K + kPad];
   __shared__ f32x4 red[WAVES - 1][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -108,21 +114,22 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
     }
   }
 
-  // 0b. the LayerNorm prologue's rows and parameters (16 threads per row, K/16 values each),
-  //     also ahead of the weights
-  constexpr int NV = PRO == kProLn ? K / 64 : 1;  // float4 pieces per thread
-  const int lr = tid >> 4, lj = tid & 15;
-  f32x4 xv[NV];
-  bf16x4 lw[NV], lb[NV];
+  // 0b. the LayerNorm prologue's rows and parameters (TPR threads per row, pieces of 8
+  //     columns: one 16-byte load of each parameter per piece), also ahead of the weights
+  constexpr int NV = PRO == kProLn ? K / (8 * TPR) : 1;  // 8-column pieces per thread
+  const int lr = tid / TPR, lj = tid % TPR;
+  f32x4 xv[NV][2];
+  bf16x8 lw[NV], lb[NV];
   if constexpr (PRO == kProLn) {
-    static_assert(K % 64 == 0 && K <= kMaxLnK, "row fits the registers");
+    static_assert(K % (8 * TPR) == 0 && K <= kMaxLnK, "row fits the registers");
     const int rr = min(lr, M - 1);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int c = 4 * (lj + 16 * i);
-      xv[i] = *reinterpret_cast<const f32x4*>(a.x + (size_t)rr * K + c);
-      lw[i] = *reinterpret_cast<const bf16x4*>(a.ln_w + c);
-      lb[i] = *reinterpret_cast<const bf16x4*>(a.ln_b + c);
+      const int c = 8 * (lj + TPR * i);
+      xv[i][0] = *reinterpret_cast<const f32x4*>(a.x + (size_t)rr * K + c);
+      xv[i][1] = *reinterpret_cast<const f32x4*>(a.x + (size_t)rr * K + c + 4);
+      lw[i] = *reinterpret_cast<const bf16x8*>(a.ln_w + c);
+      lb[i] = *reinterpret_cast<const bf16x8*>(a.ln_b + c);
     }
   }
 
@@ -143,11 +150,17 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
 
   // 2. B operands: lane holds batch row m = lane%16 (rows m >= M are zero), k = 8(lane/16) ..
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (PRO == kProRows) {
-    const bf16* ap = a.act + (size_t)min(m, M - 1) * K + kw0 + 8 * (lane >> 4);
+  if constexpr (PRO != kProLn) {
     bf16x8 b[NT];
+    if constexpr (PRO == kProRowsBlocked) {  // 16 rows x 32 k per 1 KiB block
+      const bf16* ap = a.act + ((size_t)(kw0 / 32) * kRows + m) * 32 + 8 * (lane >> 4);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) b[t] = *reinterpret_cast<const bf16x8*>(ap + 32 * t);
+      for (int t = 0; t < NT; ++t) b[t] = *reinterpret_cast<const bf16x8*>(ap + 32 * kRows * t);
+    } else {
+      const bf16* ap = a.act + (size_t)min(m, M - 1) * K + kw0 + 8 * (lane >> 4);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) b[t] = *reinterpret_cast<const bf16x8*>(ap + 32 * t);
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t)
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[t], m < M ? b[t] : bf16x8{}, acc, 0, 0,
@@ -156,23 +169,29 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
     // LayerNorm of the 16 rows into LDS (two-pass mean and variance in fp32, eps 1e-5)
     float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) sum += xv[i][0] + xv[i][1] + xv[i][2] + xv[i][3];
-    const float mean = sum16(sum) / (float)K;
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += xv[i][e >> 2][e & 3];
+    const float mean = sum_row<TPR>(sum) / (float)K;
     float sq = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sq += (xv[i][e] - mean) * (xv[i][e] - mean);
-    const float inv_std = 1.0f / sqrtf(sum16(sq) / (float)K + 1e-5f);
+      for (int e = 0; e < 8; ++e) {
+        const float dv = xv[i][e >> 2][e & 3] - mean;
+        sq += dv * dv;
+      }
+    const float inv_std = 1.0f / sqrtf(sum_row<TPR>(sq) / (float)K + 1e-5f);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      bf16x4 o;
+      bf16x8 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[e] = static_cast<bf16>(lr < M ? (xv[i][e] - mean) * inv_std * (float)lw[i][e] +
+      for (int e = 0; e < 8; ++e)
+        o[e] = static_cast<bf16>(lr < M ? (xv[i][e >> 2][e & 3] - mean) * inv_std *
+                                                  (float)lw[i][e] +
                                               (float)lb[i][e]
                                         : 0.0f);
-      *reinterpret_cast<bf16x4*>(&act[lr][4 * (lj + 16 * i)]) = o;
+      *reinterpret_cast<bf16x8*>(&act[lr][8 * (lj + TPR * i)]) = o;
     }
     __syncthreads();
     const bf16* ap = &act[m][kw0 + 8 * (lane >> 4)];
@@ -200,7 +219,8 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       o[r] = static_cast<bf16>(gelu_tanh(acc[r] + (float)ep.bias[r]));
-    bf16* g = a.g + (size_t)m * N + nl;
+    // K-blocked for kProRowsBlocked: the 4 columns lie in one 32-column block
+    bf16* g = a.g + ((size_t)(nl / 32) * kRows + m) * 32 + nl % 32;
     if (full4)
       *reinterpret_cast<bf16x4*>(g) = o;
     else
@@ -246,7 +266,8 @@ __global__ void transpose_kernel(bf16* out, const bf16* in, int rows, int cols) 
 
 template <int PRO, int EPI, int KW, int WAVES>
 hipError_t launch_kw(const SkinnyArgs& a, hipStream_t s) {
-  if constexpr (PRO == kProLn && (WAVES != 4 || 4 * KW > kMaxLnK)) {
+  constexpr int K = WAVES * KW;
+  if constexpr (PRO == kProLn && (K > kMaxLnK || K % (8 * 64 * WAVES / kRows) != 0)) {
     return hipErrorInvalidValue;
   } else {
     // Narrower column tiles for the row-prologue projections while 16-column tiles would
@@ -264,15 +285,19 @@ hipError_t launch_kw(const SkinnyArgs& a, hipStream_t s) {
   }
 }
 
-// The LayerNorm prologue splits K over 4 waves; the row prologue keeps each wave's range at
-// 128-256 (so all of a wave's loads fit in registers at once) with up to 16 waves.
+// The row prologues keep each wave's range at 128-256 (so all of a wave's loads fit in
+// registers at once) with up to 16 waves. The LayerNorm prologue runs on 8 waves (32 threads
+// per row) where K is a multiple of 256: its per-thread share of the row statistics is half
+// that of 4 waves, which took the GPT-2 QKV and fc1 LayerNorm from ~1.9 to ~1.1 us past the
+// arrival of x (with the 16-byte parameter loads).
 template <int PRO, int EPI>
 hipError_t launch_k(const SkinnyArgs& a, hipStream_t s) {
+  constexpr bool ln = PRO == kProLn;
   switch (a.K) {  // the reduction lengths of the supported configurations
     case 128: return launch_kw<PRO, EPI, 32, 4>(a, s);
-    case 512: return launch_kw<PRO, EPI, 128, 4>(a, s);
-    case 768: return launch_kw<PRO, EPI, 192, 4>(a, s);
-    case 1024: return launch_kw<PRO, EPI, 256, 4>(a, s);
+    case 512: return ln ? launch_kw<PRO, EPI, 64, 8>(a, s) : launch_kw<PRO, EPI, 128, 4>(a, s);
+    case 768: return ln ? launch_kw<PRO, EPI, 96, 8>(a, s) : launch_kw<PRO, EPI, 192, 4>(a, s);
+    case 1024: return ln ? launch_kw<PRO, EPI, 128, 8>(a, s) : launch_kw<PRO, EPI, 256, 4>(a, s);
     case 2048: return launch_kw<PRO, EPI, 128, 16>(a, s);
     case 3072: return launch_kw<PRO, EPI, 192, 16>(a, s);
     default: return hipErrorInvalidValue;
@@ -290,6 +315,7 @@ hipError_t skinny_gemm(int pro, int epi, const SkinnyArgs& a, hipStream_t s) {
   if (!skinny_supported(a.M, a.K) || a.N < 1) return hipErrorInvalidValue;
   if (pro == kProLn && a.K > kMaxLnK) return hipErrorInvalidValue;
   if (epi == kEpiQkv && (a.N % 3 || (a.N / 3) % a.dh)) return hipErrorInvalidValue;
+  if (epi == kEpiGelu && a.N % 32) return hipErrorInvalidValue;  // whole K-blocks
   if (pro == kProRows) {
     switch (epi) {
       case kEpiStore: return launch_k<kProRows, kEpiStore>(a, s);
@@ -297,6 +323,9 @@ hipError_t skinny_gemm(int pro, int epi, const SkinnyArgs& a, hipStream_t s) {
       default: return hipErrorInvalidValue;
     }
   }
+  if (pro == kProRowsBlocked)
+    return epi == kEpiResidual ? launch_k<kProRowsBlocked, kEpiResidual>(a, s)
+                               : hipErrorInvalidValue;
   switch (epi) {
     case kEpiQkv: return launch_k<kProLn, kEpiQkv>(a, s);
     case kEpiGelu: return launch_k<kProLn, kEpiGelu>(a, s);
