@@ -87,13 +87,15 @@ hipError_t gather_last(float* out, const float* x, const int* len, int n, int S,
 // Greedy pick per row of logits [n, V]: the first maximum (as std::max_element) and its
 // margin over the runner-up, stored at step = pos[b] - (prompt_len[b] - 1) in tokens
 // [step*n + b] and margins; then the decode state advances: tok[b] = pick, pos[b] += 1,
-// cache_len[b] = pos[b] + 1.
+// cache_len[b] = pos[b] + 1, and the next decode step's input row is embedded:
+// x[b] = wte[tok[b]] + wpe[pos[b]] (d floats; skipped where pos[b] >= ctx, past the last step).
 // Two launches: 32 blocks per row reduce slices into candidates (scratch of
-// pick_scratch_floats(n) floats), then one wave per row merges them.
+// pick_scratch_floats(n) floats), then one wave per row merges them and embeds.
 size_t pick_scratch_floats(int n);
 hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
                           const int* prompt_len, const float* logits, float* scratch, int n,
-                          int V, hipStream_t s);
+                          int V, float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
+                          hipStream_t s);
 
 // ---- skinny projections of the decode step (skinny.hip) ----
 

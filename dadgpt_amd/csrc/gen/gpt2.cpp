@@ -333,29 +333,28 @@ int first_layernorm(dadgpt_gpt2* m, int rows) {
 }
 
 // Weight-tied logits of the n final-LayerNorm rows in m->h, greedy pick (stored at the step
-// the device state implies).
+// the device state implies), and the embedding of each picked token at its position into
+// x[0, n), the next decode step's input.
 int head(dadgpt_gpt2* m, int n) {
   const auto& c = m->c;
   hipStream_t s = m->stream;
   TRY(proj(m, m->logits, in_h(m), m->P(m->off.tok_emb), m->emb32, n, c.d_model, c.vocab_size,
            true));
   TRY_HIP(argmax_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
-                         m->lens, m->logits, m->pick, n, c.vocab_size, s),
+                         m->lens, m->logits, m->pick, n, c.vocab_size, m->x,
+                         m->P(m->off.tok_emb), m->P(m->off.pos_emb), c.d_model, c.ctx_len, s),
           "argmax_advance");
   return DADGPT_OK;
 }
 
-// One decode step for n sequences: embed each sequence's last token at its position, the
-// blocks, the head. Everything it reads and advances is device state, so a captured copy
-// replays for every step.
+// One decode step for n sequences: the blocks over x (each sequence's last token embedded at
+// its position by the previous head), then the head. Everything it reads and advances is
+// device state, so a captured copy replays for every step.
 int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev);
 
 int decode_step(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   if (m->skinny && n <= 16) return decode_step_skinny(m, n, attn_ev);
   const auto& c = m->c;
-  TRY_HIP(embed(m->x, m->cur_tok, m->cur_pos, m->P(m->off.tok_emb), m->P(m->off.pos_emb), n, 1,
-                c.d_model, m->stream),
-          "embed");
   TRY(first_layernorm(m, n));
   for (int l = 0; l < c.n_layers; ++l)
     TRY(block(m, l, n, 1, false, attn_ev ? attn_ev + 2 * l : nullptr));
@@ -372,9 +371,6 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   const int d = c.d_model, H = c.n_heads, dh = m->dh;
   const float scale = 1.0f / std::sqrt(static_cast<float>(dh));  // src/model.cpp:389
   hipStream_t s = m->stream;
-  TRY_HIP(embed(m->x, m->cur_tok, m->cur_pos, m->P(m->off.tok_emb), m->P(m->off.pos_emb), n, 1,
-                d, s),
-          "embed");
   for (int l = 0; l < c.n_layers; ++l) {
     const auto& L = m->off.layers[l];
     SkinnyArgs q{};
@@ -426,7 +422,8 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   lg.out = m->logits;
   TRY_HIP(skinny_gemm(kProRows, kEpiStore, lg, s), "skinny logits");
   TRY_HIP(argmax_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
-                         m->lens, m->logits, m->pick, n, c.vocab_size, s),
+                         m->lens, m->logits, m->pick, n, c.vocab_size, m->x,
+                         m->P(m->off.tok_emb), m->P(m->off.pos_emb), d, c.ctx_len, s),
           "argmax_advance");
   return DADGPT_OK;
 }

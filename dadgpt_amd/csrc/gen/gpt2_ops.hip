@@ -230,12 +230,15 @@ __global__ __launch_bounds__(256) void pick_partial_kernel(float* pv1, int* pi1,
   }
 }
 
-// Stage 2: one wave per row merges the row's candidates, stores the pick and advances.
+// Stage 2: one wave per row merges the row's candidates, stores the pick, advances, and
+// embeds the picked token at its new position as the next decode step's input row (the
+// step's first launch would otherwise be that embedding).
 __global__ __launch_bounds__(64) void pick_final_kernel(int* tokens, float* margins, int* tok,
                                                         int* pos, int* cache_len,
                                                         const int* prompt_len, const float* pv1,
                                                         const int* pi1, const float* pv2,
-                                                        int n) {
+                                                        int n, float* x, const bf16* wte,
+                                                        const bf16* wpe, int d, int ctx) {
   const int b = blockIdx.x, t = threadIdx.x;
   Pick p{-__builtin_inff(), 0x7fffffff, -__builtin_inff()};
   if (t < kPickParts) {
@@ -248,16 +251,24 @@ __global__ __launch_bounds__(64) void pick_final_kernel(int* tokens, float* marg
                  __shfl_xor(p.v2, off, 64)};
     p = combine(p, q);
   }
+  // every lane holds the merged pick; pos[b] is read by all lanes before lane 0 advances it
+  const int pos_old = pos[b];
   if (t == 0) {
     // pos[b] is the position of the last token fed: prompt_len-1 for the pick after the
     // prompt (step 0), prompt_len-1+t for step t. The state lives on the device, so one
     // captured decode step replays for every t.
-    const int step = pos[b] - (prompt_len[b] - 1);
+    const int step = pos_old - (prompt_len[b] - 1);
     tokens[(size_t)step * n + b] = p.i1;
     margins[(size_t)step * n + b] = p.v1 - p.v2;
     tok[b] = p.i1;
-    pos[b] += 1;
-    cache_len[b] = pos[b] + 1;
+    pos[b] = pos_old + 1;
+    cache_len[b] = pos_old + 2;
+  }
+  const int np = pos_old + 1;
+  if (np < ctx) {  // the input row of the step that feeds this pick
+    const bf16* te = wte + (size_t)p.i1 * d;
+    const bf16* pe = wpe + (size_t)np * d;
+    for (int c = t; c < d; c += 64) x[(size_t)b * d + c] = (float)te[c] + (float)pe[c];
   }
 }
 
@@ -362,14 +373,15 @@ size_t pick_scratch_floats(int n) { return (size_t)3 * n * kPickParts; }
 
 hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
                           const int* prompt_len, const float* logits, float* scratch, int n,
-                          int V, hipStream_t s) {
+                          int V, float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
+                          hipStream_t s) {
   float* pv1 = scratch;
   int* pi1 = reinterpret_cast<int*>(scratch + (size_t)n * kPickParts);
   float* pv2 = scratch + (size_t)2 * n * kPickParts;
   pick_partial_kernel<<<dim3(n, kPickParts), 256, 0, s>>>(pv1, pi1, pv2, logits, V);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   pick_final_kernel<<<n, 64, 0, s>>>(tokens, margins, tok, pos, cache_len, prompt_len, pv1, pi1,
-                                     pv2, n);
+                                     pv2, n, x, wte, wpe, d, ctx);
   return hipGetLastError();
 }
 
