@@ -90,12 +90,19 @@ hipError_t gather_last(float* out, const float* x, const int* len, int n, int S,
 // cache_len[b] = pos[b] + 1, and the next decode step's input row is embedded:
 // x[b] = wte[tok[b]] + wpe[pos[b]] (d floats; skipped where pos[b] >= ctx, past the last step).
 // Two launches: 32 blocks per row reduce slices into candidates (scratch of
-// pick_scratch_floats(n) floats), then one wave per row merges them and embeds.
-size_t pick_scratch_floats(int n);
+// pick_scratch_floats(n, 0) floats), then one block per row merges them and embeds.
+size_t pick_scratch_floats(int n, int parts);
 hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
                           const int* prompt_len, const float* logits, float* scratch, int n,
                           int V, float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
                           hipStream_t s);
+// The same pick from candidates already reduced per workgroup by the logits projection
+// (kEpiStore with SkinnyArgs::cand): `parts` candidates per row in three planes of `rows`
+// rows (values, columns, runner-up values). One launch.
+hipError_t pick_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
+                        const int* prompt_len, const float* cand, int parts, int rows, int n,
+                        float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
+                        hipStream_t s);
 
 // ---- skinny projections of the decode step (skinny.hip) ----
 
@@ -111,6 +118,8 @@ struct SkinnyArgs {
   const bf16* ln_w;
   const bf16* ln_b;
   float* out;            // kEpiStore: [M][N]
+  float* cand;           // kEpiStore, optional: each workgroup's greedy candidate per row,
+                         //   planes [3][16][skinny_store_parts(N)] (value, column, runner-up)
   const float* bias_f;   // kEpiQkv: fp32 bias [N]
   const bf16* bias;      // kEpiGelu, kEpiResidual: bias [N]
   bf16* g;               // kEpiGelu: gelu(A W + bias), K-blocked [N/32][16][32]
@@ -123,6 +132,7 @@ struct SkinnyArgs {
 };
 
 bool skinny_supported(int M, int K);  // M <= 16 and a K the kernels are built for
+int skinny_store_parts(int N);        // workgroups of a kProRows/kEpiStore launch over N columns
 hipError_t skinny_gemm(int prologue, int epilogue, const SkinnyArgs& args, hipStream_t s);
 // out [cols][rows] = in [rows][cols]^T (bf16)
 hipError_t transpose(bf16* out, const bf16* in, int rows, int cols, hipStream_t s);

@@ -420,11 +420,12 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   lg.M = n, lg.N = c.vocab_size, lg.K = d;
   lg.act = m->h;
   lg.out = m->logits;
+  lg.cand = m->pick;  // each workgroup's greedy candidate per row
   TRY_HIP(skinny_gemm(kProRows, kEpiStore, lg, s), "skinny logits");
-  TRY_HIP(argmax_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
-                         m->lens, m->logits, m->pick, n, c.vocab_size, m->x,
-                         m->P(m->off.tok_emb), m->P(m->off.pos_emb), d, c.ctx_len, s),
-          "argmax_advance");
+  TRY_HIP(pick_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
+                       m->lens, m->pick, skinny_store_parts(c.vocab_size), kSkinnyRows, n, m->x,
+                       m->P(m->off.tok_emb), m->P(m->off.pos_emb), d, c.ctx_len, s),
+          "pick_advance");
   return DADGPT_OK;
 }
 
@@ -598,7 +599,11 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       (st = m->alloc_n(&m->f, rows * c.d_ff, "fc1 out")) ||
       (st = m->alloc_n(&m->xl, (size_t)max_batch * d, "last rows")) ||
       (st = m->alloc_n(&m->logits, (size_t)max_batch * c.vocab_size, "logits")) ||
-      (st = m->alloc_n(&m->pick, pick_scratch_floats(max_batch), "pick scratch")) ||
+      // the two-stage pick's candidates, or the skinny logits' per-workgroup ones (16 rows)
+      (st = m->alloc_n(&m->pick,
+                       pick_scratch_floats(std::max(max_batch, kSkinnyRows),
+                                           skinny_store_parts(c.vocab_size)),
+                       "pick scratch")) ||
       (st = m->alloc_n(&m->lse, rows * c.n_heads, "lse")) ||
       (!proj32 && (st = m->alloc_n(&m->h, rows * d, "ln out"))) ||
       (!proj32 && (st = m->alloc_n(&m->a, rows * d, "attn in"))) ||

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include "gen_internal.hpp"
+#include "pick.hpp"
 
 namespace dadgpt::gen {
 
@@ -180,21 +181,6 @@ __global__ void gather_last_kernel(float* out, const float* x, const int* len, i
   for (int c = threadIdx.x; c < d; c += blockDim.x) out[(size_t)b * d + c] = src[c];
 }
 
-struct Pick {
-  float v1;
-  int i1;
-  float v2;
-};
-
-// The better of two candidates (higher value, then lower index) keeps its index; the runner-up
-// value is the larger of the loser's best and the winner's runner-up.
-__device__ __forceinline__ Pick combine(Pick a, Pick b) {
-  const bool b_wins = b.v1 > a.v1 || (b.v1 == a.v1 && b.i1 < a.i1);
-  const Pick& w = b_wins ? b : a;
-  const Pick& l = b_wins ? a : b;
-  return Pick{w.v1, w.i1, fmaxf(l.v1, w.v2)};
-}
-
 constexpr int kPickParts = 32;  // blocks per row in the first stage of the greedy pick
 
 // Stage 1: block (b, part) reduces a contiguous slice of row b to one candidate.
@@ -206,16 +192,16 @@ __global__ __launch_bounds__(256) void pick_partial_kernel(float* pv1, int* pi1,
   const int span = (V + kPickParts - 1) / kPickParts;
   const int lo = part * span, hi = min(V, lo + span);
   const float* row = logits + (size_t)b * V;
-  Pick p{-__builtin_inff(), 0x7fffffff, -__builtin_inff()};
-  for (int v = lo + t; v < hi; v += 256) p = combine(p, Pick{row[v], v, -__builtin_inff()});
+  Pick p = pick_none();
+  for (int v = lo + t; v < hi; v += 256) p = pick_combine(p, Pick{row[v], v, -__builtin_inff()});
   s_v1[t] = p.v1;
   s_i1[t] = p.i1;
   s_v2[t] = p.v2;
   __syncthreads();
   for (int w = 128; w > 0; w >>= 1) {
     if (t < w) {
-      const Pick q = combine(Pick{s_v1[t], s_i1[t], s_v2[t]},
-                             Pick{s_v1[t + w], s_i1[t + w], s_v2[t + w]});
+      const Pick q = pick_combine(Pick{s_v1[t], s_i1[t], s_v2[t]},
+                                  Pick{s_v1[t + w], s_i1[t + w], s_v2[t + w]});
       s_v1[t] = q.v1;
       s_i1[t] = q.i1;
       s_v2[t] = q.v2;
@@ -230,29 +216,32 @@ __global__ __launch_bounds__(256) void pick_partial_kernel(float* pv1, int* pi1,
   }
 }
 
-// Stage 2: one wave per row merges the row's candidates, stores the pick, advances, and
-// embeds the picked token at its new position as the next decode step's input row (the
-// step's first launch would otherwise be that embedding).
-__global__ __launch_bounds__(64) void pick_final_kernel(int* tokens, float* margins, int* tok,
-                                                        int* pos, int* cache_len,
-                                                        const int* prompt_len, const float* pv1,
-                                                        const int* pi1, const float* pv2,
-                                                        int n, float* x, const bf16* wte,
-                                                        const bf16* wpe, int d, int ctx) {
+// Stage 2: one 256-thread block per row merges the row's `parts` candidates (stage 1's, or
+// those of the logits projection's epilogue), stores the pick, advances, and embeds the
+// picked token at its new position as the next decode step's input row (the step's first
+// launch would otherwise be that embedding).
+__global__ __launch_bounds__(256) void pick_final_kernel(int* tokens, float* margins, int* tok,
+                                                         int* pos, int* cache_len,
+                                                         const int* prompt_len, const float* pv1,
+                                                         const int* pi1, const float* pv2,
+                                                         int parts, int n, float* x,
+                                                         const bf16* wte, const bf16* wpe, int d,
+                                                         int ctx) {
+  __shared__ Pick s_wave[4];
   const int b = blockIdx.x, t = threadIdx.x;
-  Pick p{-__builtin_inff(), 0x7fffffff, -__builtin_inff()};
-  if (t < kPickParts) {
-    const int k = b * kPickParts + t;
-    p = Pick{pv1[k], pi1[k], pv2[k]};
+  Pick p = pick_none();
+  for (int k = t; k < parts; k += 256) {
+    const size_t i = (size_t)b * parts + k;
+    p = pick_combine(p, Pick{pv1[i], pi1[i], pv2[i]});
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const Pick q{__shfl_xor(p.v1, off, 64), __shfl_xor(p.i1, off, 64),
-                 __shfl_xor(p.v2, off, 64)};
-    p = combine(p, q);
-  }
-  // every lane holds the merged pick; pos[b] is read by all lanes before lane 0 advances it
+  for (int off = 32; off > 0; off >>= 1) p = pick_combine(p, pick_shfl_xor(p, off));
+  if ((t & 63) == 0) s_wave[t >> 6] = p;
+  __syncthreads();
+  p = pick_combine(pick_combine(s_wave[0], s_wave[1]), pick_combine(s_wave[2], s_wave[3]));
+  // pos[b] is read by every thread before thread 0 advances it (after the barrier below)
   const int pos_old = pos[b];
+  __syncthreads();
   if (t == 0) {
     // pos[b] is the position of the last token fed: prompt_len-1 for the pick after the
     // prompt (step 0), prompt_len-1+t for step t. The state lives on the device, so one
@@ -268,7 +257,7 @@ __global__ __launch_bounds__(64) void pick_final_kernel(int* tokens, float* marg
   if (np < ctx) {  // the input row of the step that feeds this pick
     const bf16* te = wte + (size_t)p.i1 * d;
     const bf16* pe = wpe + (size_t)np * d;
-    for (int c = t; c < d; c += 64) x[(size_t)b * d + c] = (float)te[c] + (float)pe[c];
+    for (int c = t; c < d; c += 256) x[(size_t)b * d + c] = (float)te[c] + (float)pe[c];
   }
 }
 
@@ -369,7 +358,9 @@ hipError_t gather_last(float* out, const float* x, const int* len, int n, int S,
   return hipGetLastError();
 }
 
-size_t pick_scratch_floats(int n) { return (size_t)3 * n * kPickParts; }
+size_t pick_scratch_floats(int n, int parts) {
+  return (size_t)3 * n * (parts > kPickParts ? parts : kPickParts);
+}
 
 hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
                           const int* prompt_len, const float* logits, float* scratch, int n,
@@ -380,8 +371,20 @@ hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* 
   float* pv2 = scratch + (size_t)2 * n * kPickParts;
   pick_partial_kernel<<<dim3(n, kPickParts), 256, 0, s>>>(pv1, pi1, pv2, logits, V);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-  pick_final_kernel<<<n, 64, 0, s>>>(tokens, margins, tok, pos, cache_len, prompt_len, pv1, pi1,
-                                     pv2, n, x, wte, wpe, d, ctx);
+  pick_final_kernel<<<n, 256, 0, s>>>(tokens, margins, tok, pos, cache_len, prompt_len, pv1,
+                                      pi1, pv2, kPickParts, n, x, wte, wpe, d, ctx);
+  return hipGetLastError();
+}
+
+hipError_t pick_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
+                        const int* prompt_len, const float* cand, int parts, int rows, int n,
+                        float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
+                        hipStream_t s) {
+  const float* pv1 = cand;
+  const int* pi1 = reinterpret_cast<const int*>(cand + (size_t)rows * parts);
+  const float* pv2 = cand + (size_t)2 * rows * parts;
+  pick_final_kernel<<<n, 256, 0, s>>>(tokens, margins, tok, pos, cache_len, prompt_len, pv1,
+                                      pi1, pv2, parts, n, x, wte, wpe, d, ctx);
   return hipGetLastError();
 }
 

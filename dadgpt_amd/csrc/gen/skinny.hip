@@ -29,6 +29,9 @@
 //             which halves the cache lines every workgroup pulls through its CU for fc2
 // Epilogues (per output element, after the bias):
 //   kEpiStore     out [M][N] fp32                                       (logits)
+//                 and, if cand is set, the workgroup's greedy candidate of each row (best
+//                 column, its value, the runner-up value), so the pick reads 1/16 of the
+//                 logits' columns instead of re-reading all of them
 //   kEpiQkv       q -> q [M, H, dh]; k, v -> the caches [.., H, max_len, dh] at row pos[m]
 //   kEpiGelu      g = bf16(gelu(.)), K-blocked for the next projection: element (m, n) at
 //                 ((n/32)*16 + m)*32 + n%32 (the buffer holds 16 rows)       (fc1)
@@ -36,6 +39,7 @@
 #include <hip/hip_runtime.h>
 
 #include "gen_internal.hpp"
+#include "pick.hpp"
 
 namespace dadgpt::gen {
 
@@ -207,6 +211,24 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
   if (wave > 0) return;
 #pragma unroll
   for (int i = 0; i < WAVES - 1; ++i) acc += red[i][lane];
+  if constexpr (EPI == kEpiStore) {
+    if (a.cand != nullptr) {  // all 64 lanes take part: the 4 lanes of row m are 16 apart
+      Pick p = pick_none();
+      if (mine && m < M) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (nl + r < N) p = pick_combine(p, Pick{acc[r], nl + r, -__builtin_inff()});
+      }
+      p = pick_combine(p, pick_shfl_xor(p, 16));
+      p = pick_combine(p, pick_shfl_xor(p, 32));
+      if (lane < 16 && m < M) {
+        const size_t plane = (size_t)kRows * gridDim.x, i = (size_t)m * gridDim.x + blockIdx.x;
+        a.cand[i] = p.v1;
+        reinterpret_cast<int*>(a.cand)[plane + i] = p.i1;
+        a.cand[2 * plane + i] = p.v2;
+      }
+    }
+  }
   if (!mine || m >= M || nl >= N) return;
   if constexpr (EPI == kEpiStore) {
     float* o = a.out + (size_t)m * N + nl;
@@ -264,19 +286,26 @@ __global__ void transpose_kernel(bf16* out, const bf16* in, int rows, int cols) 
   }
 }
 
+// Column tile of a launch: 16 columns per workgroup, or 8 / 4 for the row-prologue
+// projections while 16-column tiles would leave most of the 256 CUs idle (Wo and fc2 of
+// GPT-2: 48 workgroups). The LayerNorm prologue stays at 16 columns: every workgroup
+// recomputes the rows' statistics, and more workgroups made QKV slower (8.4 against 6.7 us at
+// 8 columns).
+int col_tile(int pro, int N) {
+  if (pro == kProLn || N >= 16 * 160) return 16;
+  return N >= 8 * 160 ? 8 : 4;
+}
+
 template <int PRO, int EPI, int KW, int WAVES>
 hipError_t launch_kw(const SkinnyArgs& a, hipStream_t s) {
   constexpr int K = WAVES * KW;
   if constexpr (PRO == kProLn && (K > kMaxLnK || K % (8 * 64 * WAVES / kRows) != 0)) {
     return hipErrorInvalidValue;
   } else {
-    // Narrower column tiles for the row-prologue projections while 16-column tiles would
-    // leave most of the 256 CUs idle (Wo and fc2 of GPT-2: 48 workgroups). The LayerNorm
-    // prologue stays at 16 columns: every workgroup recomputes the rows' statistics, and
-    // more workgroups made QKV slower (8.4 against 6.7 us at 8 columns).
-    if (PRO == kProLn || a.N >= 16 * 160) {
+    const int cols = col_tile(PRO, a.N);
+    if (cols == 16) {
       skinny_kernel<PRO, EPI, KW, WAVES, 16><<<dim3((a.N + 15) / 16), 64 * WAVES, 0, s>>>(a);
-    } else if (a.N >= 8 * 160) {
+    } else if (cols == 8) {
       skinny_kernel<PRO, EPI, KW, WAVES, 8><<<dim3((a.N + 7) / 8), 64 * WAVES, 0, s>>>(a);
     } else {
       skinny_kernel<PRO, EPI, KW, WAVES, 4><<<dim3((a.N + 3) / 4), 64 * WAVES, 0, s>>>(a);
@@ -305,6 +334,11 @@ hipError_t launch_k(const SkinnyArgs& a, hipStream_t s) {
 }
 
 }  // namespace
+
+int skinny_store_parts(int N) {
+  const int cols = col_tile(kProRows, N);
+  return (N + cols - 1) / cols;
+}
 
 bool skinny_supported(int M, int K) {
   return M >= 1 && M <= kRows &&
