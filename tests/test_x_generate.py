@@ -35,6 +35,10 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 TINY = dict(d_model=128, n_layers=2, n_heads=4, d_ff=512, ctx_len=64, vocab_size=512)
 TINY64 = dict(d_model=256, n_layers=2, n_heads=4, d_ff=512, ctx_len=96, vocab_size=384)
 GPT2 = dict(d_model=768, n_layers=12, n_heads=12, d_ff=3072, ctx_len=1024, vocab_size=50257)
+# GPT-2's layer shapes (d 768, d_ff 3072: the skinny decode kernels' 8-wave LayerNorm prologue,
+# 16-wave K-blocked fc2, 4-column Wo tiles) on two layers, with a vocabulary whose logits
+# projection ends in a partial 16-column tile and leaves 626 candidates per row for the pick
+MID = dict(d_model=768, n_layers=2, n_heads=12, d_ff=3072, ctx_len=128, vocab_size=10007)
 TOL_LOGIT = 2e-2
 
 
@@ -195,7 +199,8 @@ def _prompts(cfg, lens, seed):
 @pytest.mark.gpu
 @pytest.mark.parametrize("cfg,attention", [(TINY, "bf16"), (TINY, "fp32"),
                                            (TINY, "fp32_materialized"), (TINY64, "bf16"),
-                                           (TINY64, "fp32"), (TINY64, "fp32_materialized")])
+                                           (TINY64, "fp32"), (TINY64, "fp32_materialized"),
+                                           (MID, "bf16"), (MID, "fp32")])
 def test_generate_matches_oracle(gpu, cfg, attention):
     case(f"generate vs oracle d={cfg['d_model']} H={cfg['n_heads']} attention={attention}")
     model, params = _gpu_model(cfg, seed=21, max_batch=4, attention=attention)
@@ -217,18 +222,25 @@ def test_generate_matches_oracle(gpu, cfg, attention):
 
 
 @pytest.mark.gpu
-def test_decode_step_equals_prefill_of_longer_prompt(gpu):
+@pytest.mark.parametrize("cfg", [TINY64, MID])
+def test_decode_step_equals_prefill_of_longer_prompt(gpu, cfg):
     """KV cache invariant: the logits of decode step t equal the prefill logits of the prompt
-    extended by the first t generated tokens (tests/test_model.cpp:216-252, 375-414)."""
-    cfg = TINY64
-    case("decode step == prefill of the longer prompt")
+    extended by the first t generated tokens (tests/test_model.cpp:216-252, 375-414). On MID
+    the decode steps run the skinny kernels and the prefill hipBLASLt, two independent
+    implementations of every projection. Bound: 1e-2 at d 256; at d 768 the two paths' bf16
+    activations (the same rounding points, different summation orders) flip in more elements
+    (measured 1.09e-2), so the bound is the oracle tolerance, which each path meets alone."""
+    case(f"decode step == prefill of the longer prompt d={cfg['d_model']}")
+    tol = 1e-2 if cfg is TINY64 else TOL_LOGIT
     model, _ = _gpu_model(cfg, seed=22, max_batch=3)
     prompts = _prompts(cfg, [9, 40, 2], 400)
     out = model.generate(prompts, 6, logits=True)
     for t in (1, 3, 5):
         longer = [list(p) + list(out["tokens"][b, :t]) for b, p in enumerate(prompts)]
         again = model.generate(longer, 1, logits=True)
-        assert np.abs(again["logits"][0] - out["logits"][t]).max() <= 1e-2, t
+        err = float(np.abs(again["logits"][0] - out["logits"][t]).max())
+        print(f"step {t}: max |decode - prefill| = {err:.3g}", flush=True)
+        assert err <= tol, t
     model.close()
 
 
