@@ -11,7 +11,8 @@
 // load instruction of a wave covers whole key rows (bf16 D=64: 8 lanes x 16 B per row, 8 rows
 // per instruction, a contiguous 1 KiB), all K and V loads of a wave are issued before any
 // arithmetic, and they carry the non-temporal hint (the cache is streamed once). bf16 scores
-// are v_dot2_f32_bf16 on the packed q and K words, so neither side is unpacked. The 8 waves
+// are v_dot2_f32_bf16 on the packed q and K words, so neither side is unpacked; the
+// reductions across lanes use DPP and v_permlane16/32_swap (lanes.hpp), not LDS round trips. The 8 waves
 // merge (max, sum, o) in LDS with the logsumexp rule. Chunks are small enough that the work
 // of a long cache spreads over several CUs: one CU streaming a whole 1024-key cache alone was
 // the tail of the launch.
@@ -40,6 +41,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "lanes.hpp"
 
 #if defined(__gfx942__) || defined(__gfx950__) || !defined(__HIP_DEVICE_COMPILE__)
 #define DADGPT_DECODE_SC1_COHERENT 1
@@ -191,15 +193,12 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
     float s[NLD];
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      float acc = Elem<T>::dot(qw, kr[i]);
-#pragma unroll
-      for (int off = 1; off < LPR; off <<= 1) acc += __shfl_xor(acc, off, 64);
+      const float acc = lanes::group_sum<LPR>(Elem<T>::dot(qw, kr[i]));
       const int key = key0 + i * KPL + grp;
       s[i] = key < L ? acc * scale_log2 : neg_inf();
       mx = fmaxf(mx, s[i]);
     }
-#pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    mx = lanes::wave_max_of_groups<LPR>(mx);  // uniform within each row group already
     // key0 < L, so key key0 is valid and mx is finite
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
@@ -210,12 +209,16 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
 #pragma unroll
       for (int e = 0; e < EPL; ++e) o[e] = fmaf(p, vf[e], o[e]);
     }
+    // sum over the row groups: lanes with the same column slice (lane % LPR) are partners
+    if constexpr (LPR < 8) {
+      lsum += __shfl_xor(lsum, LPR, 64);
 #pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) {
-      lsum += __shfl_xor(lsum, off, 64);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) o[e] += __shfl_xor(o[e], off, 64);
+      for (int e = 0; e < EPL; ++e) o[e] += __shfl_xor(o[e], LPR, 64);
     }
+    constexpr int K0 = LPR < 8 ? 8 : LPR;
+    lsum = lanes::sum_across<K0>(lsum);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) o[e] = lanes::sum_across<K0>(o[e]);
   }
   if (grp == 0) {
 #pragma unroll

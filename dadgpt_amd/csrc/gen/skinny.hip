@@ -40,6 +40,7 @@
 
 #include "gen_internal.hpp"
 #include "pick.hpp"
+#include "lanes.hpp"
 
 namespace dadgpt::gen {
 
@@ -67,9 +68,7 @@ __device__ __forceinline__ f32x4 ld_bf16x4(const bf16* p) {
 
 template <int TPR>
 __device__ __forceinline__ float sum_row(float v) {  // over the TPR lanes of a row group
-#pragma unroll
-  for (int off = 1; off < TPR; off <<= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  return lanes::group_sum<TPR>(v);                   // DPP and permlane swaps, no LDS trips
 }
 
 template <int EPI>
