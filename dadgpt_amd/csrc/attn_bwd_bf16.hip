@@ -24,6 +24,7 @@
 #include "common.hpp"
 #include "dropout.hpp"
 #include "kernels.hpp"
+#include "lanes.hpp"
 #include "tiles.hpp"
 
 namespace dadgpt {
@@ -79,9 +80,7 @@ __global__ __launch_bounds__(256) void delta_bf16_kernel(float* __restrict__ del
         acc += bf16_lo(a[w]) * bf16_lo(b[w]) + bf16_hi(a[w]) * bf16_hi(b[w]);
     }
   }
-  acc += __shfl_xor(acc, 1, 64);
-  acc += __shfl_xor(acc, 2, 64);
-  acc += __shfl_xor(acc, 4, 64);
+  acc = lanes::group_sum<LPR>(acc);
   if (valid && part == 0) delta[drow] = acc;
 }
 

@@ -25,6 +25,7 @@
 #include "common.hpp"
 #include "dropout.hpp"
 #include "kernels.hpp"
+#include "lanes.hpp"
 
 namespace dadgpt {
 namespace {
@@ -254,8 +255,7 @@ __global__ __launch_bounds__(256) void delta_f32_kernel(float* __restrict__ delt
     const f32x4 a = *reinterpret_cast<const f32x4*>(dout + row * D + 4 * c);
     const f32x4 b = *reinterpret_cast<const f32x4*>(out + row * D + 4 * c);
     float acc = a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
-#pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    acc = lanes::group_sum<LPR>(acc);
     if (c == 0) delta[row] = acc;
   }
 }

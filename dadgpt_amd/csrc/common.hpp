@@ -58,11 +58,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Value held by lane (l ^ 32): the same query/key index in the other lane half.
-__device__ __forceinline__ float other_half(float x) {
-  return __shfl_xor(x, 32, 64);
-}
-
 // Reductions over lanes l and l ^ 32 with v_permlane32_swap (no LDS round trip). With both
 // operands x, the swap returns {x[l % 32], x[32 + l % 32]} in every lane, so both lanes of a
 // pair compute the same value in the same order.

@@ -15,6 +15,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "lanes.hpp"
 
 namespace dadgpt {
 
@@ -89,7 +90,14 @@ template <int S>
 __device__ __forceinline__ uint32_t transpose8_step(uint32_t x, int t) {
   constexpr uint32_t hi_cols = S == 4 ? 0xF0F0u : S == 2 ? 0xCCCCu : 0xAAAAu;  // column bit S set
   constexpr uint32_t lo_cols = hi_cols ^ 0xFFFFu;
-  const uint32_t y = (uint32_t)__shfl_xor((int)x, S, 64);
+  // partner l ^ S: quad_perm gives it exactly for S = 1, 2 (a VALU op); S = 4 crosses quads
+  uint32_t y;
+  if constexpr (S == 1)
+    y = lanes::dpp_u32<lanes::kQuadXor1>(x);
+  else if constexpr (S == 2)
+    y = lanes::dpp_u32<lanes::kQuadXor2>(x);
+  else
+    y = (uint32_t)__shfl_xor((int)x, S, 64);
   return (t & S) ? (x & hi_cols) | ((y & hi_cols) >> S) : (x & lo_cols) | ((y & lo_cols) << S);
 }
 __device__ __forceinline__ uint32_t transpose8_bits(uint32_t x, int t) {

@@ -6,6 +6,7 @@
 
 #include "gen_internal.hpp"
 #include "pick.hpp"
+#include "lanes.hpp"
 
 namespace dadgpt::gen {
 
@@ -50,11 +51,7 @@ __global__ void embed_kernel(float* x, const int* tok, const int* pos0, const bf
     x[(size_t)r * d + c] = (float)te[c] + (float)pe[c];
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return lanes::group_sum<64>(v); }
 
 // Sum over the 256 threads of a block (4 waves): wave shuffles, then the 4 partials via LDS.
 __device__ __forceinline__ float block_sum(float v, float* sm) {

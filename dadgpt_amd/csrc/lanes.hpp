@@ -23,6 +23,10 @@ template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
 }
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
 
 // The value of lane l ^ 16 and of lane l ^ 32 (v_permlane16_swap / v_permlane32_swap with the
 // same register on both sides: each lane keeps its own value in one result and receives its
@@ -61,6 +65,19 @@ __device__ __forceinline__ float group_sum(float x) {
   if constexpr (N >= 16) x += dpp<kMirror>(x);
   if constexpr (N >= 32) x = sum_xor16(x);
   if constexpr (N >= 64) x = sum_xor32(x);
+  return x;
+}
+
+// Maximum over each aligned group of N lanes, as group_sum.
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+  static_assert(N >= 2 && N <= 64 && (N & (N - 1)) == 0, "power-of-two group");
+  x = fmaxf(x, dpp<kQuadXor1>(x));
+  if constexpr (N >= 4) x = fmaxf(x, dpp<kQuadXor2>(x));
+  if constexpr (N >= 8) x = fmaxf(x, dpp<kHalfMirror>(x));
+  if constexpr (N >= 16) x = fmaxf(x, dpp<kMirror>(x));
+  if constexpr (N >= 32) x = max_xor16(x);
+  if constexpr (N >= 64) x = max_xor32(x);
   return x;
 }
 

@@ -15,6 +15,7 @@
 // (cuda/gpu_ops.cu:542-563), masked, then scaled (src/model.cpp:601-607). Only the order of
 // the row sums differs (a wave tree instead of a block tree).
 #include "common.hpp"
+#include "lanes.hpp"
 #include "kernels.hpp"
 
 namespace dadgpt {
@@ -23,16 +24,8 @@ namespace {
 constexpr int kRowsPerBlock = 4;
 constexpr float kMaskValue = -1e9f;  // cuda/gpu_ops.cu:482
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
-  return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
-}
+__device__ __forceinline__ float wave_max(float x) { return lanes::group_max<64>(x); }
+__device__ __forceinline__ float wave_sum(float x) { return lanes::group_sum<64>(x); }
 
 template <int V, typename F>
 __device__ __forceinline__ void read_row(const float* row, int cols, int lane, F f) {
