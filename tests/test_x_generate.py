@@ -39,6 +39,10 @@ GPT2 = dict(d_model=768, n_layers=12, n_heads=12, d_ff=3072, ctx_len=1024, vocab
 # 16-wave K-blocked fc2, 4-column Wo tiles) on two layers, with a vocabulary whose logits
 # projection ends in a partial 16-column tile and leaves 626 candidates per row for the pick
 MID = dict(d_model=768, n_layers=2, n_heads=12, d_ff=3072, ctx_len=128, vocab_size=10007)
+# the other reduction lengths of the 8-wave LayerNorm prologue (K = 512 with a 2048-deep fc2,
+# K = 1024 with d_head 64 over 16 heads)
+W512 = dict(d_model=512, n_layers=2, n_heads=8, d_ff=2048, ctx_len=64, vocab_size=3001)
+W1024 = dict(d_model=1024, n_layers=1, n_heads=16, d_ff=3072, ctx_len=64, vocab_size=2053)
 TOL_LOGIT = 2e-2
 
 
@@ -200,7 +204,8 @@ def _prompts(cfg, lens, seed):
 @pytest.mark.parametrize("cfg,attention", [(TINY, "bf16"), (TINY, "fp32"),
                                            (TINY, "fp32_materialized"), (TINY64, "bf16"),
                                            (TINY64, "fp32"), (TINY64, "fp32_materialized"),
-                                           (MID, "bf16"), (MID, "fp32")])
+                                           (MID, "bf16"), (MID, "fp32"), (W512, "bf16"),
+                                           (W1024, "bf16")])
 def test_generate_matches_oracle(gpu, cfg, attention):
     case(f"generate vs oracle d={cfg['d_model']} H={cfg['n_heads']} attention={attention}")
     model, params = _gpu_model(cfg, seed=21, max_batch=4, attention=attention)
