@@ -46,9 +46,11 @@ int materialized_decode(dadgpt_blas* h, float* out, float* probs, const float* q
 hipError_t init_normal(bf16* p, size_t n, uint64_t seed, float stddev, hipStream_t s);
 hipError_t fill(bf16* p, size_t n, float value, hipStream_t s);
 
-// Rows r = b*S + s of x [n*S, d] fp32 = wte[tok[r]] + wpe[pos0[b] + s].
+// Prompt rows: row r of x [rows, d] fp32 = wte[tok[p]] + wpe[pos0[b] + s] for the padded
+// position p = b*S + s = rowmap[r] (the prompts packed without padding), or p = r when rowmap
+// is null (tok holds the padded [n, S] prompts).
 hipError_t embed(float* x, const int* tok, const int* pos0, const bf16* wte, const bf16* wpe,
-                 int n, int S, int d, hipStream_t s);
+                 const int* rowmap, int rows, int S, int d, hipStream_t s);
 
 // Per row (d <= 2048): if y, x[r] += sum_{s < splits} y[s][r] + bias (the residual add of a
 // projection, y holding `splits` partial sums [splits][rows][d]); then, if w,
@@ -59,17 +61,20 @@ hipError_t residual_layernorm(float* x, const float* y, const bf16* bias, O* out
                               const bf16* w, const bf16* b, int rows, int d, hipStream_t s,
                               int splits = 1);
 
-// qkv [n*S, 3d] fp32 (+ bias bqkv [3d] fp32): q -> qh [n*H, S, dh]; k, v -> kh, vh
-// [n*H, S, dh] when kh is not null; k, v of the rows s < nvalid[b] -> caches
-// [n_cap, H, max_len, dh] at position pos0[b] + s. T is bf16 or float.
+// qkv [rows, 3d] fp32 (+ bias bqkv [3d] fp32), row r at padded position b*S + s = rowmap[r]
+// (r itself when rowmap is null): q -> qh [n*H, S, dh]; k, v -> kh, vh [n*H, S, dh] when kh
+// is not null; k, v of the rows s < nvalid[b] -> caches [n_cap, H, max_len, dh] at position
+// pos0[b] + s. T is bf16 or float.
 template <typename T>
 hipError_t qkv_split(T* qh, T* kh, T* vh, T* kcache, T* vcache, const float* qkv,
-                     const float* bqkv, const int* pos0, const int* nvalid, int n, int S, int H,
-                     int dh, int max_len, hipStream_t s);
+                     const float* bqkv, const int* pos0, const int* nvalid, const int* rowmap,
+                     int rows, int S, int H, int dh, int max_len, hipStream_t s);
 
-// out [n*S, d] (O: bf16 or float) <- heads [n*H, S, dh] (T).
+// out [rows, d] (O: bf16 or float) <- heads [n*H, S, dh] (T), row r from padded position
+// rowmap[r] (r when rowmap is null).
 template <typename T, typename O>
-hipError_t merge_heads(O* out, const T* heads, int n, int S, int H, int dh, hipStream_t s);
+hipError_t merge_heads(O* out, const T* heads, const int* rowmap, int rows, int S, int H, int dh,
+                       hipStream_t s);
 
 // out[i] = bf16(in[i]); out[i] = float(in[i]).
 hipError_t to_bf16(bf16* out, const float* in, size_t count, hipStream_t s);
@@ -80,9 +85,9 @@ template <typename O>
 hipError_t bias_gelu(O* out, const float* y, const bf16* bias, int rows, int cols,
                      hipStream_t s);
 
-// out[b] = x[b*S + len[b] - 1] (rows of d floats).
-hipError_t gather_last(float* out, const float* x, const int* len, int n, int S, int d,
-                       hipStream_t s);
+// out[r] = in[idx[r]] (rows of d elements; T float or bf16).
+template <typename T>
+hipError_t gather_rows(T* out, const T* in, const int* idx, int rows, int d, hipStream_t s);
 
 // Greedy pick per row of logits [n, V]: the first maximum (as std::max_element) and its
 // margin over the runner-up, stored at step = pos[b] - (prompt_len[b] - 1) in tokens

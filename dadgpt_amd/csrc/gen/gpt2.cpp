@@ -147,6 +147,9 @@ struct dadgpt_gpt2 {
   void* ws = nullptr;
   size_t ws_bytes = 0;
   int *tok_in = nullptr, *pos0 = nullptr, *nvalid = nullptr, *ones = nullptr, *lens = nullptr;
+  // prefill rows packed without padding: padded position b*S + s of each packed row, and the
+  // packed row of each prompt's last token
+  int *rowmap = nullptr, *lastrow = nullptr;
   int *cur_tok = nullptr, *cur_pos = nullptr, *cache_len = nullptr;
   int* out_tok = nullptr;       // [ctx_len, max_batch]: every step any call can take
   float* out_margin = nullptr;
@@ -172,9 +175,10 @@ struct dadgpt_gpt2 {
 namespace {
 
 // Prefill attention over n padded prompts of S rows. fp32: split heads [n*H, S, dh] in
-// m->qh/kh/vh -> m->ao (merged afterwards). bf16: Q heads from m->qh, K and V read in place
-// from the layer's cache (rows 0..S-1 of [max_batch, H, ctx, dh]), and the output written
-// token-major into m->a, the Wo GEMM's input: no split K/V copies and no merge pass.
+// m->qh/kh/vh -> m->ao (merged into the packed rows afterwards). bf16: Q heads from m->qh, K
+// and V read in place from the layer's cache (rows 0..S-1 of [max_batch, H, ctx, dh]), and
+// the output written token-major into m->ao (padded rows), gathered into the packed rows of
+// the Wo GEMM's input afterwards: no split K/V copies.
 int attention_prefill(dadgpt_gpt2* m, int layer, int n, int S, float scale) {
   const int H = m->c.n_heads, dh = m->dh;
   if (m->materialized) {
@@ -192,7 +196,7 @@ int attention_prefill(dadgpt_gpt2* m, int layer, int n, int S, float scale) {
       tokens{d * S, dh, d};
   const dadgpt_head_strides st[4] = {heads, cache, cache, tokens};
   return dadgpt_flash_attention_forward_bf16_strided(
-      (uint16_t*)m->a, m->lse, (const uint16_t*)m->qh, (const uint16_t*)m->kc[layer],
+      (uint16_t*)m->ao, m->lse, (const uint16_t*)m->qh, (const uint16_t*)m->kc[layer],
       (const uint16_t*)m->vc[layer], n, H, S, dh, scale, st, m->stream);
 }
 
@@ -248,13 +252,14 @@ int layernorm_h(dadgpt_gpt2* m, float* x, const float* y, const bf16* bias, cons
   return check_hip(e, "residual_layernorm");
 }
 
-// One transformer block over `rows` rows (n sequences of S rows each). prefill: the rows are
-// prompt positions 0..S-1 (K/V appended for s < len); otherwise one token per sequence at
-// cur_pos. attn_ev: optional pair of events around the attention launch.
-int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev) {
+// One transformer block over `rows` rows. prefill: the prompts' positions packed without
+// padding (m->rowmap gives each row's place b*S + s in the padded [n, S] batch the attention
+// runs on; K/V appended for s < len); otherwise one token per sequence at cur_pos (rows = n,
+// S = 1). attn_ev: optional pair of events around the attention launch.
+int block(dadgpt_gpt2* m, int l, int n, int S, int rows, bool prefill, hipEvent_t* attn_ev) {
   const auto& c = m->c;
   const auto& L = m->off.layers[l];
-  const int d = c.d_model, H = c.n_heads, dh = m->dh, rows = n * S;
+  const int d = c.d_model, H = c.n_heads, dh = m->dh;
   const float scale = 1.0f / std::sqrt(static_cast<float>(dh));  // src/model.cpp:389
   hipStream_t s = m->stream;
 
@@ -265,32 +270,36 @@ int block(dadgpt_gpt2* m, int l, int n, int S, bool prefill, hipEvent_t* attn_ev
   if (prefill) {
     if (m->fp32)
       TRY_HIP(qkv_split<float>((float*)m->qh, (float*)m->kh, (float*)m->vh, (float*)m->kc[l],
-                               (float*)m->vc[l], m->qkv, m->bqkv[l], m->pos0, m->nvalid, n, S, H,
-                               dh, c.ctx_len, s),
+                               (float*)m->vc[l], m->qkv, m->bqkv[l], m->pos0, m->nvalid,
+                               m->rowmap, rows, S, H, dh, c.ctx_len, s),
               "qkv_split");
     else  // Q heads and the cache append only
       TRY_HIP(qkv_split<bf16>((bf16*)m->qh, nullptr, nullptr, (bf16*)m->kc[l], (bf16*)m->vc[l],
-                              m->qkv, m->bqkv[l], m->pos0, m->nvalid, n, S, H, dh, c.ctx_len,
-                              s),
+                              m->qkv, m->bqkv[l], m->pos0, m->nvalid, m->rowmap, rows, S, H,
+                              dh, c.ctx_len, s),
               "qkv_split");
     if (int st = attention_prefill(m, l, n, S, scale))
       return attn_fail(m, st, "prefill attention");
     if (m->proj32)
-      TRY_HIP((merge_heads<float, float>(m->a32, (const float*)m->ao, n, S, H, dh, s)),
+      TRY_HIP((merge_heads<float, float>(m->a32, (const float*)m->ao, m->rowmap, rows, S, H, dh,
+                                         s)),
               "merge_heads");
     else if (m->fp32)
-      TRY_HIP((merge_heads<float, bf16>(m->a, (const float*)m->ao, n, S, H, dh, s)),
+      TRY_HIP((merge_heads<float, bf16>(m->a, (const float*)m->ao, m->rowmap, rows, S, H, dh, s)),
               "merge_heads");
+    else
+      TRY_HIP(gather_rows<bf16>(m->a, (const bf16*)m->ao, m->rowmap, rows, d, s),
+              "gather_rows(attention)");
   } else {
     if (m->fp32)
       TRY_HIP(qkv_split<float>((float*)m->qh, nullptr, nullptr, (float*)m->kc[l],
-                               (float*)m->vc[l], m->qkv, m->bqkv[l], m->cur_pos, m->ones, n, 1,
-                               H, dh, c.ctx_len, s),
+                               (float*)m->vc[l], m->qkv, m->bqkv[l], m->cur_pos, m->ones,
+                               nullptr, n, 1, H, dh, c.ctx_len, s),
               "qkv_split");
     else
       TRY_HIP(qkv_split<bf16>((bf16*)m->qh, nullptr, nullptr, (bf16*)m->kc[l], (bf16*)m->vc[l],
-                              m->qkv, m->bqkv[l], m->cur_pos, m->ones, n, 1, H, dh, c.ctx_len,
-                              s),
+                              m->qkv, m->bqkv[l], m->cur_pos, m->ones, nullptr, n, 1, H, dh,
+                              c.ctx_len, s),
               "qkv_split");
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[0], s), "hipEventRecord");
     if (int st = attention_decode(m, l, n, scale)) return attn_fail(m, st, "decode attention");
@@ -357,7 +366,7 @@ int decode_step(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   const auto& c = m->c;
   TRY(first_layernorm(m, n));
   for (int l = 0; l < c.n_layers; ++l)
-    TRY(block(m, l, n, 1, false, attn_ev ? attn_ev + 2 * l : nullptr));
+    TRY(block(m, l, n, 1, n, false, attn_ev ? attn_ev + 2 * l : nullptr));
   return head(m, n);
 }
 
@@ -619,6 +628,8 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       (m->fp32 && (st = m->alloc(&m->vh, rows * d * ab, "v heads"))) ||
       (st = m->alloc(&m->ao, rows * d * ab, "attn out")) ||
       (st = m->alloc_n(&m->tok_in, rows, "tokens")) ||
+      (st = m->alloc_n(&m->rowmap, rows, "prefill row map")) ||
+      (st = m->alloc_n(&m->lastrow, max_batch, "prefill last rows")) ||
       (st = m->alloc_n(&m->pos0, max_batch, "pos0")) ||
       (st = m->alloc_n(&m->nvalid, max_batch, "nvalid")) ||
       (st = m->alloc_n(&m->ones, max_batch, "ones")) ||
@@ -732,14 +743,27 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
   hipStream_t s = m->stream;
   const size_t outs = (size_t)new_tokens * n;  // <= ctx_len * max_batch, the buffers' size
 
-  // padded prompt rows, lengths, and the position before the first generated token
-  std::vector<int> tok((size_t)n * S, 0), len(prompt_lens, prompt_lens + n), pos(n);
+  // padded prompt rows, lengths, the position before the first generated token, and the
+  // packed prefill rows (every prompt position once, no padding): their padded positions and
+  // each prompt's last one
+  std::vector<int> tok((size_t)n * S, 0), len(prompt_lens, prompt_lens + n), pos(n), rowmap,
+      lastrow(n);
+  rowmap.reserve((size_t)n * S);
   for (int b = 0; b < n; ++b) {
-    for (int t = 0; t < len[b]; ++t) tok[(size_t)b * S + t] = prompts[(size_t)b * prompt_stride + t];
+    for (int t = 0; t < len[b]; ++t) {
+      tok[(size_t)b * S + t] = prompts[(size_t)b * prompt_stride + t];
+      rowmap.push_back(b * S + t);
+    }
+    lastrow[b] = (int)rowmap.size() - 1;
     pos[b] = len[b] - 1;
   }
+  const int rows = (int)rowmap.size();
   TRY_HIP(hipMemcpyAsync(m->tok_in, tok.data(), tok.size() * sizeof(int), hipMemcpyHostToDevice, s),
           "hipMemcpyAsync(tokens)");
+  TRY_HIP(hipMemcpyAsync(m->rowmap, rowmap.data(), rows * sizeof(int), hipMemcpyHostToDevice, s),
+          "hipMemcpyAsync(row map)");
+  TRY_HIP(hipMemcpyAsync(m->lastrow, lastrow.data(), n * sizeof(int), hipMemcpyHostToDevice, s),
+          "hipMemcpyAsync(last rows)");
   TRY_HIP(hipMemcpyAsync(m->nvalid, len.data(), n * sizeof(int), hipMemcpyHostToDevice, s),
           "hipMemcpyAsync(lens)");
   TRY_HIP(hipMemcpyAsync(m->lens, len.data(), n * sizeof(int), hipMemcpyHostToDevice, s),
@@ -753,13 +777,14 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
   hipEvent_t* ev = m->events.data();
   if (timed) TRY_HIP(hipEventRecord(ev[0], s), "hipEventRecord");
 
-  // ---- prefill: the padded batch [n, S], then the pick after each prompt ----
-  TRY_HIP(embed(m->x, m->tok_in, m->pos0, m->P(m->off.tok_emb), m->P(m->off.pos_emb), n, S,
-                c.d_model, s),
+  // ---- prefill: the packed prompt rows (attention over the padded batch [n, S]), then the
+  //      pick after each prompt ----
+  TRY_HIP(embed(m->x, m->tok_in, m->pos0, m->P(m->off.tok_emb), m->P(m->off.pos_emb), m->rowmap,
+                rows, S, c.d_model, s),
           "embed");
-  TRY(first_layernorm(m, n * S));
-  for (int l = 0; l < c.n_layers; ++l) TRY(block(m, l, n, S, true, nullptr));
-  TRY_HIP(gather_last(m->xl, m->x, m->lens, n, S, c.d_model, s), "gather_last");
+  TRY(first_layernorm(m, rows));
+  for (int l = 0; l < c.n_layers; ++l) TRY(block(m, l, n, S, rows, true, nullptr));
+  TRY_HIP(gather_rows<float>(m->xl, m->x, m->lastrow, n, c.d_model, s), "gather_rows(last)");
   TRY(layernorm_h(m, m->xl, nullptr, nullptr, m->P(m->off.lnf_w), m->P(m->off.lnf_b), n));
   TRY(head(m, n));
   if (timed) TRY_HIP(hipEventRecord(ev[1], s), "hipEventRecord");

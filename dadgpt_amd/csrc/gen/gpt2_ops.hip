@@ -43,9 +43,10 @@ __global__ void fill_kernel(bf16* p, size_t n, float value) {
 }
 
 __global__ void embed_kernel(float* x, const int* tok, const int* pos0, const bf16* wte,
-                             const bf16* wpe, int S, int d) {
-  const int r = blockIdx.x, b = r / S, s = r % S;
-  const bf16* te = wte + (size_t)tok[r] * d;
+                             const bf16* wpe, const int* rowmap, int S, int d) {
+  // packed row r holds padded position p = b*S + s (rowmap), or r = p without a map
+  const int r = blockIdx.x, p = rowmap ? rowmap[r] : r, b = p / S, s = p % S;
+  const bf16* te = wte + (size_t)tok[p] * d;
   const bf16* pe = wpe + (size_t)(pos0[b] + s) * d;
   for (int c = threadIdx.x; c < d; c += blockDim.x)
     x[(size_t)r * d + c] = (float)te[c] + (float)pe[c];
@@ -112,9 +113,10 @@ __global__ __launch_bounds__(256) void residual_layernorm_kernel(float* x, const
 
 template <typename T>
 __global__ void qkv_split_kernel(T* qh, T* kh, T* vh, T* kcache, T* vcache, const float* qkv,
-                                 const float* bqkv, const int* pos0, const int* nvalid, int S,
-                                 int H, int dh, int max_len) {
-  const int r = blockIdx.x, b = r / S, s = r % S;
+                                 const float* bqkv, const int* pos0, const int* nvalid,
+                                 const int* rowmap, int S, int H, int dh, int max_len) {
+  // qkv row r is padded position p = b*S + s (rowmap), or r = p without a map
+  const int r = blockIdx.x, pr = rowmap ? rowmap[r] : r, b = pr / S, s = pr % S;
   const int d = H * dh;
   const float* row = qkv + (size_t)r * 3 * d;
   const bool append = s < nvalid[b];
@@ -137,8 +139,10 @@ __global__ void qkv_split_kernel(T* qh, T* kh, T* vh, T* kcache, T* vcache, cons
 }
 
 template <typename T, typename O>
-__global__ void merge_heads_kernel(O* out, const T* heads, int S, int H, int dh) {
-  const int r = blockIdx.x, b = r / S, s = r % S;
+__global__ void merge_heads_kernel(O* out, const T* heads, const int* rowmap, int S, int H,
+                                   int dh) {
+  // output row r is padded position p = b*S + s (rowmap), or r = p without a map
+  const int r = blockIdx.x, p = rowmap ? rowmap[r] : r, b = p / S, s = p % S;
   const int d = H * dh;
   for (int c = threadIdx.x; c < d; c += blockDim.x) {
     const int h = c / dh, e = c % dh;
@@ -172,10 +176,11 @@ __global__ void bias_gelu_kernel(O* out, const float* y, const bf16* bias, int r
     out[i] = static_cast<O>(gelu_tanh(y[i] + (float)bias[i % cols]));
 }
 
-__global__ void gather_last_kernel(float* out, const float* x, const int* len, int S, int d) {
-  const int b = blockIdx.x;
-  const float* src = x + ((size_t)b * S + len[b] - 1) * d;
-  for (int c = threadIdx.x; c < d; c += blockDim.x) out[(size_t)b * d + c] = src[c];
+template <typename T>
+__global__ void gather_rows_kernel(T* out, const T* in, const int* idx, int d) {
+  const int r = blockIdx.x;
+  const T* src = in + (size_t)idx[r] * d;
+  for (int c = threadIdx.x; c < d; c += blockDim.x) out[(size_t)r * d + c] = src[c];
 }
 
 constexpr int kPickParts = 32;  // blocks per row in the first stage of the greedy pick
@@ -285,8 +290,8 @@ hipError_t fill(bf16* p, size_t n, float value, hipStream_t s) {
 }
 
 hipError_t embed(float* x, const int* tok, const int* pos0, const bf16* wte, const bf16* wpe,
-                 int n, int S, int d, hipStream_t s) {
-  embed_kernel<<<n * S, 256, 0, s>>>(x, tok, pos0, wte, wpe, S, d);
+                 const int* rowmap, int rows, int S, int d, hipStream_t s) {
+  embed_kernel<<<rows, 256, 0, s>>>(x, tok, pos0, wte, wpe, rowmap, S, d);
   return hipGetLastError();
 }
 
@@ -307,28 +312,29 @@ template hipError_t residual_layernorm<float>(float*, const float*, const bf16*,
 
 template <typename T>
 hipError_t qkv_split(T* qh, T* kh, T* vh, T* kcache, T* vcache, const float* qkv,
-                     const float* bqkv, const int* pos0, const int* nvalid, int n, int S, int H,
-                     int dh, int max_len, hipStream_t s) {
-  qkv_split_kernel<T><<<n * S, 256, 0, s>>>(qh, kh, vh, kcache, vcache, qkv, bqkv, pos0, nvalid,
-                                            S, H, dh, max_len);
+                     const float* bqkv, const int* pos0, const int* nvalid, const int* rowmap,
+                     int rows, int S, int H, int dh, int max_len, hipStream_t s) {
+  qkv_split_kernel<T><<<rows, 256, 0, s>>>(qh, kh, vh, kcache, vcache, qkv, bqkv, pos0, nvalid,
+                                           rowmap, S, H, dh, max_len);
   return hipGetLastError();
 }
 template hipError_t qkv_split<bf16>(bf16*, bf16*, bf16*, bf16*, bf16*, const float*,
-                                    const float*, const int*, const int*, int, int, int, int,
-                                    int, hipStream_t);
+                                    const float*, const int*, const int*, const int*, int, int,
+                                    int, int, int, hipStream_t);
 template hipError_t qkv_split<float>(float*, float*, float*, float*, float*, const float*,
-                                     const float*, const int*, const int*, int, int, int, int,
-                                     int, hipStream_t);
+                                     const float*, const int*, const int*, const int*, int, int,
+                                     int, int, int, hipStream_t);
 
 template <typename T, typename O>
-hipError_t merge_heads(O* out, const T* heads, int n, int S, int H, int dh, hipStream_t s) {
-  merge_heads_kernel<T, O><<<n * S, 256, 0, s>>>(out, heads, S, H, dh);
+hipError_t merge_heads(O* out, const T* heads, const int* rowmap, int rows, int S, int H, int dh,
+                       hipStream_t s) {
+  merge_heads_kernel<T, O><<<rows, 256, 0, s>>>(out, heads, rowmap, S, H, dh);
   return hipGetLastError();
 }
-template hipError_t merge_heads<float, bf16>(bf16*, const float*, int, int, int, int,
-                                             hipStream_t);
-template hipError_t merge_heads<float, float>(float*, const float*, int, int, int, int,
-                                              hipStream_t);
+template hipError_t merge_heads<float, bf16>(bf16*, const float*, const int*, int, int, int,
+                                             int, hipStream_t);
+template hipError_t merge_heads<float, float>(float*, const float*, const int*, int, int, int,
+                                              int, hipStream_t);
 
 hipError_t to_f32(float* out, const bf16* in, size_t count, hipStream_t s) {
   to_f32_kernel<<<grid_for(count), 256, 0, s>>>(out, in, count);
@@ -349,11 +355,13 @@ hipError_t bias_gelu(O* out, const float* y, const bf16* bias, int rows, int col
 template hipError_t bias_gelu<bf16>(bf16*, const float*, const bf16*, int, int, hipStream_t);
 template hipError_t bias_gelu<float>(float*, const float*, const bf16*, int, int, hipStream_t);
 
-hipError_t gather_last(float* out, const float* x, const int* len, int n, int S, int d,
-                       hipStream_t s) {
-  gather_last_kernel<<<n, 256, 0, s>>>(out, x, len, S, d);
+template <typename T>
+hipError_t gather_rows(T* out, const T* in, const int* idx, int rows, int d, hipStream_t s) {
+  gather_rows_kernel<T><<<rows, 256, 0, s>>>(out, in, idx, d);
   return hipGetLastError();
 }
+template hipError_t gather_rows<float>(float*, const float*, const int*, int, int, hipStream_t);
+template hipError_t gather_rows<bf16>(bf16*, const bf16*, const int*, int, int, hipStream_t);
 
 size_t pick_scratch_floats(int n, int parts) {
   return (size_t)3 * n * (parts > kPickParts ? parts : kPickParts);
