@@ -279,14 +279,36 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
   if (!sm_last) return;
 
   if (tid < D) {
-    float gm = neg_inf();
-    for (int c = 0; c < nch; ++c) gm = fmaxf(gm, ld_agent(ph + c * (D + 2)));
-    float gl = 0.f, go = 0.f;
-    for (int c = 0; c < nch; ++c) {  // every chunk < nch holds a valid key: finite max
-      const float* pc = ph + c * (D + 2);
-      const float f = fast_exp2(ld_agent(pc) - gm);
-      gl += ld_agent(pc + 1) * f;
-      go += ld_agent(pc + 2 + tid) * f;
+    // The partials of kMergeBatch chunks are all loaded before any is used (one memory round
+    // trip per batch: this merge ends the kernel for the caches that finish last), and the
+    // batches merge online. Every chunk < nch holds a valid key: finite maxima. For
+    // nch <= kMergeBatch this is sum_c l_c 2^(m_c - max) in chunk order, as a two-pass merge.
+    constexpr int kMergeBatch = 4;
+    float gm = neg_inf(), gl = 0.f, go = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += kMergeBatch) {
+      float mv[kMergeBatch], lv[kMergeBatch], ov[kMergeBatch];
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) {
+        const float* pc = ph + min(c0 + j, nch - 1) * (D + 2);  // past nch: unused
+        mv[j] = ld_agent(pc);
+        lv[j] = ld_agent(pc + 1);
+        ov[j] = ld_agent(pc + 2 + tid);
+      }
+      float bm = gm;
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j)
+        if (c0 + j < nch) bm = fmaxf(bm, mv[j]);
+      const float fo = fast_exp2(gm - bm);  // 0 before the first batch (gl = go = 0 then)
+      gl *= fo;
+      go *= fo;
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j)
+        if (c0 + j < nch) {
+          const float f = fast_exp2(mv[j] - bm);
+          gl += lv[j] * f;
+          go += ov[j] * f;
+        }
+      gm = bm;
     }
     out[hrow * D + tid] = Elem<T>::from(go / gl);
   }
