@@ -9,9 +9,10 @@
 // Workgroup = 16 output columns (4 or 8 for narrow projections, below) x W waves: wave w takes
 // the K range [w K/W, (w+1) K/W) (W = 4, 8 for the LayerNorm prologue at K a multiple of 256,
 // 16 for K >= 2048) and issues all its weight loads up front; the partial products are summed
-// through LDS and the epilogue runs in the same workgroup, so no result crosses workgroups. The grid is N/16 workgroups for the LayerNorm
-// projections (144 for the QKV projection of GPT-2 124M, 192 for fc1) and N/4 for Wo and fc2
-// (192 instead of 48, which spreads their weight streams over most CUs). The epilogue's own
+// through LDS and the epilogue runs in the same workgroup, so no result crosses workgroups.
+// The grid is N/16 workgroups for the LayerNorm projections (144 for the QKV projection of
+// GPT-2 124M, 192 for fc1) and N/4 for Wo and fc2 (192 instead of 48, which spreads their
+// weight streams over most CUs). The epilogue's own
 // inputs (bias, residual, cache row) are loaded first, so their latency hides under the
 // weight stream.
 // v_mfma_f32_16x16x32_bf16: lane l supplies A[l%16][8(l/16)+e] and B[8(l/16)+e][l%16] and
@@ -22,8 +23,8 @@
 //   kProRows  bf16 activations act [M][K], read straight from global memory (L2-resident)
 //   kProLn    A = bf16(LayerNorm(x) w + b) of the fp32 residual stream x [M][K], computed by
 //             every workgroup into LDS (two-pass mean and variance, eps 1e-5) with 16 or 32
-//             threads per row; the weight loads are issued right after its inputs, so the
-//             stream runs under it
+//             threads per row, row sums on DPP and permlane swaps; the weight loads are
+//             issued right after its inputs, so the stream runs under it
 //   kProRowsBlocked  bf16 activations stored K-blocked, [K/32][16][32] (the kEpiGelu layout):
 //             each operand load of a wave is 1 KiB contiguous instead of 64 bytes of 16 rows,
 //             which halves the cache lines every workgroup pulls through its CU for fc2
