@@ -250,6 +250,29 @@ def test_decode_step_equals_prefill_of_longer_prompt(gpu, cfg):
 
 
 @pytest.mark.gpu
+def test_generate_beyond_the_skinny_batch_matches_oracle(gpu):
+    """More than 16 sequences: the decode step runs on the hipBLASLt projections and the
+    two-stage greedy pick (whose last stage also embeds the next step's input rows), instead
+    of the skinny kernels; teacher-forced against the oracle as test_generate_matches_oracle."""
+    cfg = TINY
+    n = 20
+    case(f"generate vs oracle, {n} sequences (non-skinny decode step)")
+    model, params = _gpu_model(cfg, seed=24, max_batch=n)
+    prompts = _prompts(cfg, [1 + (7 * i) % 23 for i in range(n)], 600)
+    new = 6
+    out = model.generate(prompts, new, logits=True)
+    for b, p in enumerate(prompts):
+        seq = list(p)
+        for t in range(new):
+            ref = G.forward(params, cfg, seq, round_bf16=True)[-1]
+            got = out["logits"][t, b]
+            assert np.abs(got - ref).max() <= TOL_LOGIT, (b, t, np.abs(got - ref).max())
+            assert out["tokens"][b, t] == int(np.argmax(got)), "pick is the first maximum"
+            seq.append(int(out["tokens"][b, t]))
+    model.close()
+
+
+@pytest.mark.gpu
 def test_generate_is_deterministic_and_batch_independent(gpu):
     """Same tokens run to run, and a sequence's tokens do not depend on its batch mates."""
     cfg = TINY
