@@ -111,7 +111,7 @@ hipError_t pick_advance(int* tokens, float* margins, int* tok, int* pos, int* ca
 
 // ---- skinny projections of the decode step (skinny.hip) ----
 
-enum SkinnyPrologue { kProRows = 0, kProLn = 1, kProRowsBlocked = 2 };
+enum SkinnyPrologue { kProRows = 0, kProLn = 1, kProRowsBlocked = 2, kProRowsF32 = 3 };
 constexpr int kSkinnyRows = 16;  // rows of the skinny path; kEpiGelu's g holds this many
 enum SkinnyEpilogue { kEpiStore = 0, kEpiQkv = 1, kEpiGelu = 2, kEpiResidual = 3 };
 
@@ -119,6 +119,7 @@ struct SkinnyArgs {
   const bf16* wt;        // W^T [N][K]
   int M, N, K;           // rows (<= 16), columns, reduction length
   const bf16* act;       // kProRows: A [M][K]; kProRowsBlocked: A [K/32][16][32]
+  const float* act32;    // kProRowsF32: A [M][K] fp32, rounded to bf16 as it is loaded
   const float* x;        // kProLn: A = LayerNorm(x [M][K]) * ln_w + ln_b
   const bf16* ln_w;
   const bf16* ln_b;

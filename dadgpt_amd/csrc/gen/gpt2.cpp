@@ -393,18 +393,17 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[2 * l], s), "hipEventRecord");
     if (int st = attention_decode(m, l, n, scale)) return attn_fail(m, st, "decode attention");
     if (attn_ev) TRY_HIP(hipEventRecord(attn_ev[2 * l + 1], s), "hipEventRecord");
-    const bf16* attn_in = m->a;  // the skinny path runs with bf16 projections only
-    if (m->fp32)
-      TRY_HIP(to_bf16(m->a, (const float*)m->ao, (size_t)n * d, s), "to_bf16");
-    else
-      attn_in = (const bf16*)m->ao;
-
+    // the attention output [n, H, dh] is the [n, d] row layout; fp32 attention's is rounded to
+    // bf16 inside the Wo kernel (the skinny path runs with bf16 projections only)
     SkinnyArgs o{};
     o.wt = m->wo_t[l];
     o.M = n, o.N = d, o.K = d;
-    o.act = attn_in;
+    if (m->fp32)
+      o.act32 = (const float*)m->ao;
+    else
+      o.act = (const bf16*)m->ao;
     o.bias = m->P(L.bo), o.x_out = m->x;
-    TRY_HIP(skinny_gemm(kProRows, kEpiResidual, o, s), "skinny Wo");
+    TRY_HIP(skinny_gemm(m->fp32 ? kProRowsF32 : kProRows, kEpiResidual, o, s), "skinny Wo");
 
     SkinnyArgs f1{};
     f1.wt = m->w1_t[l];

@@ -25,6 +25,8 @@
 //             every workgroup into LDS (two-pass mean and variance, eps 1e-5) with 16 or 32
 //             threads per row, row sums on DPP and permlane swaps; the weight loads are
 //             issued right after its inputs, so the stream runs under it
+//   kProRowsF32  fp32 activations act32 [M][K] (the fp32 attention output), rounded to bf16
+//             in registers as the operands are loaded: no separate conversion launch
 //   kProRowsBlocked  bf16 activations stored K-blocked, [K/32][16][32] (the kEpiGelu layout):
 //             each operand load of a wave is 1 KiB contiguous instead of 64 bytes of 16 rows,
 //             which halves the cache lines every workgroup pulls through its CU for fc2
@@ -160,6 +162,21 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
       const bf16* ap = a.act + ((size_t)(kw0 / 32) * kRows + m) * 32 + 8 * (lane >> 4);
 #pragma unroll
       for (int t = 0; t < NT; ++t) b[t] = *reinterpret_cast<const bf16x8*>(ap + 32 * kRows * t);
+    } else if constexpr (PRO == kProRowsF32) {
+      const float* ap = a.act32 + (size_t)min(m, M - 1) * K + kw0 + 8 * (lane >> 4);
+      f32x4 lo[NT], hi[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        lo[t] = *reinterpret_cast<const f32x4*>(ap + 32 * t);
+        hi[t] = *reinterpret_cast<const f32x4*>(ap + 32 * t + 4);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          b[t][e] = static_cast<bf16>(lo[t][e]);
+          b[t][4 + e] = static_cast<bf16>(hi[t][e]);
+        }
     } else {
       const bf16* ap = a.act + (size_t)min(m, M - 1) * K + kw0 + 8 * (lane >> 4);
 #pragma unroll
@@ -359,6 +376,9 @@ hipError_t skinny_gemm(int pro, int epi, const SkinnyArgs& a, hipStream_t s) {
   }
   if (pro == kProRowsBlocked)
     return epi == kEpiResidual ? launch_k<kProRowsBlocked, kEpiResidual>(a, s)
+                               : hipErrorInvalidValue;
+  if (pro == kProRowsF32)
+    return epi == kEpiResidual ? launch_k<kProRowsF32, kEpiResidual>(a, s)
                                : hipErrorInvalidValue;
   switch (epi) {
     case kEpiQkv: return launch_k<kProLn, kEpiQkv>(a, s);
