@@ -55,11 +55,13 @@ hipError_t embed(float* x, const int* tok, const int* pos0, const bf16* wte, con
 // Per row (d <= 2048): if y, x[r] += sum_{s < splits} y[s][r] + bias (the residual add of a
 // projection, y holding `splits` partial sums [splits][rows][d]); then, if w,
 // out[r] = O(LayerNorm(x[r]) * w + b) with eps 1e-5 (two-pass mean and variance, fp32); O is
-// bf16 or float (the precision of the projection that reads it).
+// bf16 or float (the precision of the projection that reads it). blocked (rows <= 16, d a
+// multiple of 32): out in the skinny projections' K-blocked layout, element (r, c) at
+// ((c/32)*16 + r)*32 + c%32.
 template <typename O>
 hipError_t residual_layernorm(float* x, const float* y, const bf16* bias, O* out,
                               const bf16* w, const bf16* b, int rows, int d, hipStream_t s,
-                              int splits = 1);
+                              int splits = 1, bool blocked = false);
 
 // qkv [rows, 3d] fp32 (+ bias bqkv [3d] fp32), row r at padded position b*S + s = rowmap[r]
 // (r itself when rowmap is null): q -> qh [n*H, S, dh]; k, v -> kh, vh [n*H, S, dh] when kh

@@ -421,7 +421,7 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   }
   // final LayerNorm, then the tied logits
   TRY_HIP(residual_layernorm<bf16>(m->x, nullptr, nullptr, m->h, m->P(m->off.lnf_w),
-                                   m->P(m->off.lnf_b), n, d, s),
+                                   m->P(m->off.lnf_b), n, d, s, 1, /*blocked=*/true),
           "residual_layernorm");
   SkinnyArgs lg{};
   lg.wt = m->P(m->off.tok_emb);  // [V, d]: already W^T of the tied projection
@@ -429,7 +429,7 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   lg.act = m->h;
   lg.out = m->logits;
   lg.cand = m->pick;  // each workgroup's greedy candidate per row
-  TRY_HIP(skinny_gemm(kProRows, kEpiStore, lg, s), "skinny logits");
+  TRY_HIP(skinny_gemm(kProRowsBlocked, kEpiStore, lg, s), "skinny logits");
   TRY_HIP(pick_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
                        m->lens, m->pick, skinny_store_parts(c.vocab_size), kSkinnyRows, n, m->x,
                        m->P(m->off.tok_emb), m->P(m->off.pos_emb), d, c.ctx_len, s),

@@ -74,7 +74,8 @@ template <typename O>
 __global__ __launch_bounds__(256) void residual_layernorm_kernel(float* x, const float* y,
                                                                  const bf16* bias, O* out,
                                                                  const bf16* w, const bf16* b,
-                                                                 int d, int splits) {
+                                                                 int d, int splits,
+                                                                 int blocked) {
   __shared__ float sm[4];
   float* xr = x + (size_t)blockIdx.x * d;
   float v[kLnMaxPerThread];
@@ -103,11 +104,14 @@ __global__ __launch_bounds__(256) void residual_layernorm_kernel(float* x, const
     if (c < d) sq += (v[i] - mean) * (v[i] - mean);
   }
   const float inv_std = 1.0f / sqrtf(block_sum(sq, sm) / (float)d + 1e-5f);
-  O* orow = out + (size_t)blockIdx.x * d;
+  O* orow = out + (size_t)blockIdx.x * (blocked ? 32 : d);
 #pragma unroll
   for (int i = 0; i < kLnMaxPerThread; ++i) {
     const int c = threadIdx.x + 256 * i;
-    if (c < d) orow[c] = static_cast<O>((v[i] - mean) * inv_std * (float)w[c] + (float)b[c]);
+    // blocked: element (r, c) at ((c/32)*16 + r)*32 + c%32 (the skinny K-blocked layout)
+    if (c < d)
+      orow[blocked ? (c / 32) * 32 * kSkinnyRows + c % 32 : c] =
+          static_cast<O>((v[i] - mean) * inv_std * (float)w[c] + (float)b[c]);
   }
 }
 
@@ -298,17 +302,18 @@ hipError_t embed(float* x, const int* tok, const int* pos0, const bf16* wte, con
 template <typename O>
 hipError_t residual_layernorm(float* x, const float* y, const bf16* bias, O* out,
                               const bf16* w, const bf16* b, int rows, int d, hipStream_t s,
-                              int splits) {
+                              int splits, bool blocked) {
   if (d > 256 * kLnMaxPerThread) return hipErrorInvalidValue;
-  residual_layernorm_kernel<O><<<rows, 256, 0, s>>>(x, y, bias, out, w, b, d, splits);
+  if (blocked && (rows > kSkinnyRows || d % 32 != 0)) return hipErrorInvalidValue;
+  residual_layernorm_kernel<O><<<rows, 256, 0, s>>>(x, y, bias, out, w, b, d, splits, blocked);
   return hipGetLastError();
 }
 template hipError_t residual_layernorm<bf16>(float*, const float*, const bf16*, bf16*,
                                              const bf16*, const bf16*, int, int, hipStream_t,
-                                             int);
+                                             int, bool);
 template hipError_t residual_layernorm<float>(float*, const float*, const bf16*, float*,
                                               const bf16*, const bf16*, int, int, hipStream_t,
-                                              int);
+                                              int, bool);
 
 template <typename T>
 hipError_t qkv_split(T* qh, T* kh, T* vh, T* kcache, T* vcache, const float* qkv,

@@ -353,7 +353,7 @@ hipError_t launch_k(const SkinnyArgs& a, hipStream_t s) {
 }  // namespace
 
 int skinny_store_parts(int N) {
-  const int cols = col_tile(kProRows, N);
+  const int cols = col_tile(kProRows, N);  // the same tile for kProRowsBlocked
   return (N + cols - 1) / cols;
 }
 
@@ -374,9 +374,13 @@ hipError_t skinny_gemm(int pro, int epi, const SkinnyArgs& a, hipStream_t s) {
       default: return hipErrorInvalidValue;
     }
   }
-  if (pro == kProRowsBlocked)
-    return epi == kEpiResidual ? launch_k<kProRowsBlocked, kEpiResidual>(a, s)
-                               : hipErrorInvalidValue;
+  if (pro == kProRowsBlocked) {
+    switch (epi) {
+      case kEpiStore: return launch_k<kProRowsBlocked, kEpiStore>(a, s);
+      case kEpiResidual: return launch_k<kProRowsBlocked, kEpiResidual>(a, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (pro == kProRowsF32)
     return epi == kEpiResidual ? launch_k<kProRowsF32, kEpiResidual>(a, s)
                                : hipErrorInvalidValue;
