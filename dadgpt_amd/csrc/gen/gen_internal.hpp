@@ -96,6 +96,7 @@ hipError_t gather_rows(T* out, const T* in, const int* idx, int rows, int d, hip
 // [step*n + b] and margins; then the decode state advances: tok[b] = pick, pos[b] += 1,
 // cache_len[b] = pos[b] + 1, and the next decode step's input row is embedded:
 // x[b] = wte[tok[b]] + wpe[pos[b]] (d floats; skipped where pos[b] >= ctx, past the last step).
+// A row with no comparable logit (all NaN) picks column 0, as std::max_element does.
 // Two launches: 32 blocks per row reduce slices into candidates (scratch of
 // pick_scratch_floats(n, 0) floats), then one block per row merges them and embeds.
 size_t pick_scratch_floats(int n, int parts);
@@ -108,7 +109,7 @@ hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* 
 // rows (values, columns, runner-up values). One launch.
 hipError_t pick_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
                         const int* prompt_len, const float* cand, int parts, int rows, int n,
-                        float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
+                        int V, float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
                         hipStream_t s);
 
 // ---- skinny projections of the decode step (skinny.hip) ----

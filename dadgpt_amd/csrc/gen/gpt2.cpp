@@ -431,8 +431,9 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   lg.cand = m->pick;  // each workgroup's greedy candidate per row
   TRY_HIP(skinny_gemm(kProRowsBlocked, kEpiStore, lg, s), "skinny logits");
   TRY_HIP(pick_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
-                       m->lens, m->pick, skinny_store_parts(c.vocab_size), kSkinnyRows, n, m->x,
-                       m->P(m->off.tok_emb), m->P(m->off.pos_emb), d, c.ctx_len, s),
+                       m->lens, m->pick, skinny_store_parts(c.vocab_size), kSkinnyRows, n,
+                       c.vocab_size, m->x, m->P(m->off.tok_emb), m->P(m->off.pos_emb), d,
+                       c.ctx_len, s),
           "pick_advance");
   return DADGPT_OK;
 }
@@ -772,7 +773,13 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
 
   const int steps = new_tokens - 1;
   const bool timed = timing != nullptr;
-  if (timed) TRY(ensure_events(m, 3 + (m->use_graphs ? 0 : 2 * (size_t)steps * c.n_layers)));
+  // Only a decode step made of this library's own kernels is captured and replayed (the
+  // skinny step of up to 16 sequences with bf16 projections and flash decode attention). A
+  // step with hipBLASLt calls (more than 16 sequences, shapes the skinny kernels are not
+  // built for, fp32 projections, materialized attention) runs eagerly: the library may record
+  // memory-set nodes of its own into a capture, which are not safe to replay.
+  const bool graphs = m->use_graphs && m->skinny && n <= kSkinnyRows && !m->materialized;
+  if (timed) TRY(ensure_events(m, 3 + (graphs ? 0 : 2 * (size_t)steps * c.n_layers)));
   hipEvent_t* ev = m->events.data();
   if (timed) TRY_HIP(hipEventRecord(ev[0], s), "hipEventRecord");
 
@@ -792,9 +799,9 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
   // ---- decode: feed token t-1 at its position, pick token t ----
   // With graphs, step 1 runs eagerly (it builds any missing hipBLASLt plan) and every later
   // step replays the captured step. Without graphs, timing brackets each attention launch.
-  const bool attn_events = timed && !m->use_graphs;
+  const bool attn_events = timed && !graphs;
   for (int t = 1; t <= steps; ++t) {
-    if (m->use_graphs && t > 1) {
+    if (graphs && t > 1) {
       hipGraphExec_t g = nullptr;
       TRY(step_graph(m, n, &g));
       TRY_HIP(hipGraphLaunch(g, s), "hipGraphLaunch");

@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) void pick_final_kernel(int* tokens, float* mar
                                                          int* pos, int* cache_len,
                                                          const int* prompt_len, const float* pv1,
                                                          const int* pi1, const float* pv2,
-                                                         int parts, int n, float* x,
+                                                         int parts, int n, int V, float* x,
                                                          const bf16* wte, const bf16* wpe, int d,
                                                          int ctx) {
   __shared__ Pick s_wave[4];
@@ -245,23 +245,29 @@ __global__ __launch_bounds__(256) void pick_final_kernel(int* tokens, float* mar
   if ((t & 63) == 0) s_wave[t >> 6] = p;
   __syncthreads();
   p = pick_combine(pick_combine(s_wave[0], s_wave[1]), pick_combine(s_wave[2], s_wave[3]));
+  // A row with no comparable logit (all NaN) leaves no candidate's column: it picks column 0,
+  // as std::max_element does, so the token and the embedding row below stay in range.
+  const int pick = p.i1 >= 0 && p.i1 < V ? p.i1 : 0;
   // pos[b] is read by every thread before thread 0 advances it (after the barrier below)
   const int pos_old = pos[b];
   __syncthreads();
   if (t == 0) {
     // pos[b] is the position of the last token fed: prompt_len-1 for the pick after the
     // prompt (step 0), prompt_len-1+t for step t. The state lives on the device, so one
-    // captured decode step replays for every t.
+    // captured decode step replays for every t. (0 <= step < ctx while the host keeps
+    // prompt + new tokens within the context; the token buffers hold ctx rows of n.)
     const int step = pos_old - (prompt_len[b] - 1);
-    tokens[(size_t)step * n + b] = p.i1;
-    margins[(size_t)step * n + b] = p.v1 - p.v2;
-    tok[b] = p.i1;
+    if (step >= 0 && step < ctx) {
+      tokens[(size_t)step * n + b] = pick;
+      margins[(size_t)step * n + b] = p.v1 - p.v2;
+    }
+    tok[b] = pick;
     pos[b] = pos_old + 1;
     cache_len[b] = pos_old + 2;
   }
   const int np = pos_old + 1;
-  if (np < ctx) {  // the input row of the step that feeds this pick
-    const bf16* te = wte + (size_t)p.i1 * d;
+  if (np >= 0 && np < ctx) {  // the input row of the step that feeds this pick
+    const bf16* te = wte + (size_t)pick * d;
     const bf16* pe = wpe + (size_t)np * d;
     for (int c = t; c < d; c += 256) x[(size_t)b * d + c] = (float)te[c] + (float)pe[c];
   }
@@ -382,19 +388,19 @@ hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* 
   pick_partial_kernel<<<dim3(n, kPickParts), 256, 0, s>>>(pv1, pi1, pv2, logits, V);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   pick_final_kernel<<<n, 256, 0, s>>>(tokens, margins, tok, pos, cache_len, prompt_len, pv1,
-                                      pi1, pv2, kPickParts, n, x, wte, wpe, d, ctx);
+                                      pi1, pv2, kPickParts, n, V, x, wte, wpe, d, ctx);
   return hipGetLastError();
 }
 
 hipError_t pick_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
                         const int* prompt_len, const float* cand, int parts, int rows, int n,
-                        float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
+                        int V, float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
                         hipStream_t s) {
   const float* pv1 = cand;
   const int* pi1 = reinterpret_cast<const int*>(cand + (size_t)rows * parts);
   const float* pv2 = cand + (size_t)2 * rows * parts;
   pick_final_kernel<<<n, 256, 0, s>>>(tokens, margins, tok, pos, cache_len, prompt_len, pv1,
-                                      pi1, pv2, parts, n, x, wte, wpe, d, ctx);
+                                      pi1, pv2, parts, n, V, x, wte, wpe, d, ctx);
   return hipGetLastError();
 }
 

@@ -89,7 +89,11 @@ void dadgpt_gpt2_destroy(dadgpt_gpt2* model);
 /* Decode steps after the first replay one captured HIP graph per batch size (default on);
  * off, every step is launched kernel by kernel (and timing brackets each attention launch).
  * The replayed step reads all per-step state (tokens, positions, cache lengths) from device
- * memory, so it is the same work as the eager step. */
+ * memory, so it is the same work as the eager step. Only steps made of this library's own
+ * kernels are captured: up to 16 sequences on the skinny projections, with flash decode
+ * attention. Steps that call hipBLASLt (more batch rows, other shapes, fp32 projections,
+ * materialized attention) always run eagerly, since the library may record memory-set nodes
+ * into a capture that are not safe to replay. */
 int dadgpt_gpt2_set_graphs(dadgpt_gpt2* model, int enable);
 
 /* Greedy generation for n <= max_batch prompts (host arrays):

@@ -288,12 +288,14 @@ def test_generate_is_deterministic_and_batch_independent(gpu):
 
 
 @pytest.mark.gpu
-def test_graph_replayed_steps_equal_eager_steps(gpu):
+@pytest.mark.parametrize("cfg", [TINY, MID], ids=["tiny", "mid"])
+def test_graph_replayed_steps_equal_eager_steps(gpu, cfg):
     """The captured decode step, replayed for every step after the first, gives the same
     tokens and logits as launching each step eagerly; checked over two calls in a row (the
-    second with a smaller batch, so a second graph is captured) with eager work between."""
-    cfg = TINY64
-    case("graph replay vs eager decode steps")
+    second with a smaller batch, so a second graph is captured) with eager work between.
+    Both configs run the skinny decode step, the one that is captured (steps with hipBLASLt
+    calls run eagerly whatever set_graphs says)."""
+    case(f"graph replay vs eager decode steps d_model={cfg['d_model']}")
     model, _ = _gpu_model(cfg, seed=25, max_batch=4)
     for prompts in (_prompts(cfg, [7, 30, 2, 15], 700), _prompts(cfg, [11, 4], 800)):
         g = model.generate(prompts, 9, logits=True)
@@ -302,6 +304,29 @@ def test_graph_replayed_steps_equal_eager_steps(gpu):
         model.set_graphs(True)
         np.testing.assert_array_equal(g["tokens"], e["tokens"])
         np.testing.assert_array_equal(g["logits"], e["logits"])
+    model.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cfg", [TINY, TINY64], ids=["skinny_graph", "hipblaslt_eager"])
+def test_nan_logits_pick_column_zero(gpu, cfg):
+    """Rows whose logits are all NaN (a NaN parameter arena) have no first maximum to find:
+    the pick takes column 0, as std::max_element does (src/generate.cpp:34-37), and the
+    next step's input row is that token's embedding, so every index stays inside the
+    vocabulary. Both pick paths: the skinny logits' candidates (TINY, replayed graph) and
+    the two-stage pick after hipBLASLt logits (TINY64)."""
+    import torch
+
+    from dadgpt_amd import gpt2
+
+    case(f"NaN logits pick column 0, d_model={cfg['d_model']}")
+    params = gpt2.init_params(cfg, 26)
+    params.fill_(float("nan"))
+    torch.cuda.synchronize()
+    model = gpt2.GPT2(cfg, params, 2)
+    out = model.generate(_prompts(cfg, [5, 9], 900), 4, logits=True)
+    assert np.isnan(out["logits"]).all()
+    np.testing.assert_array_equal(out["tokens"], np.zeros((2, 4), np.int32))
     model.close()
 
 
