@@ -236,9 +236,19 @@ __global__ __launch_bounds__(256) void pick_final_kernel(int* tokens, float* mar
   __shared__ Pick s_wave[4];
   const int b = blockIdx.x, t = threadIdx.x;
   Pick p = pick_none();
-  for (int k = t; k < parts; k += 256) {
-    const size_t i = (size_t)b * parts + k;
-    p = pick_combine(p, Pick{pv1[i], pi1[i], pv2[i]});
+  // kPer candidates per thread are loaded before any is merged: one memory round trip per
+  // batch instead of one per candidate (the merge order does not change the result)
+  constexpr int kPer = 16;
+  for (int k0 = 0; k0 < parts; k0 += 256 * kPer) {
+    Pick c[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int k = k0 + 256 * j + t;
+      const size_t i = (size_t)b * parts + k;
+      c[j] = k < parts ? Pick{pv1[i], pi1[i], pv2[i]} : pick_none();
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) p = pick_combine(p, c[j]);
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) p = pick_combine(p, pick_shfl_xor(p, off));
