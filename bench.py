@@ -413,12 +413,27 @@ def generate_cfg5():
     m32 = gpt2.GPT2(cfg, params, GEN_N, attention="fp32")
     ref = m32.generate(prompts, GEN_NEW, timing=True)
     m32.close()
+    # the greedy gate at the reference's precision: fp32 flash attention against the GPU's own
+    # fp32 materialized attention, both over fp32 projections, logits kept for the comparison
+    gate = {}
+    for name, attention in (("flash", "fp32"), ("materialized", "fp32_materialized")):
+        mg = gpt2.GPT2(cfg, params, GEN_N, attention=attention, projections="fp32")
+        gate[name] = mg.generate(prompts, GEN_NEW, logits=True)
+        mg.close()
     del params
     torch.cuda.synchronize()
+
+    def first_divergence(a, b):
+        return [int(np.nonzero(ra != rb)[0][0]) if (ra != rb).any() else GEN_NEW
+                for ra, rb in zip(a, b)]
     a, b = best["tokens"], ref["tokens"]
-    div = [int(np.nonzero(ra != rb)[0][0]) if (ra != rb).any() else GEN_NEW
-           for ra, rb in zip(a, b)]
+    div = first_divergence(a, b)
     div_margins = [float(ref["margins"][r, d]) for r, d in enumerate(div) if d < GEN_NEW]
+    gf, gm = gate["flash"], gate["materialized"]
+    gdiv = first_divergence(gf["tokens"], gm["tokens"])
+    gate_dev = max(float(np.abs(gf["logits"][:min(d + 1, GEN_NEW), r] -
+                                gm["logits"][:min(d + 1, GEN_NEW), r]).max())
+                   for r, d in enumerate(gdiv))
     total_ms = t["prefill_ms"] + t["decode_ms"]
     out = {
         "config": "GPT-2 124M arch (d768 L12 H12 ff3072 ctx1024 V50257), random init, 16 "
@@ -443,6 +458,15 @@ def generate_cfg5():
             "fp32_margin_at_divergence_max": max(div_margins) if div_margins else None,
             "min_margin_fp32": float(ref["margins"].min()),
             "min_margin_bf16": float(best["margins"].min()),
+        },
+        "greedy_gate_fp32": {
+            "what": "fp32 flash attention vs the GPU's own fp32 materialized attention, both "
+                    "with fp32 projections (the reference's precision), same weights and prompts",
+            "rows_identical": int(sum(d == GEN_NEW for d in gdiv)),
+            "identical_tokens": float((gf["tokens"] == gm["tokens"]).mean()),
+            "first_divergence_per_row": gdiv,
+            "max_logit_difference_shared_history": gate_dev,
+            "min_margin": float(gm["margins"].min()),
         },
     }
     print(f"[bench] generate cfg5 {json.dumps(out)}", file=sys.stderr, flush=True)
