@@ -127,6 +127,44 @@ SMALL_BF16 = [(1, 1, 64), (2, 70, 64), (3, 129, 64), (1, 64, 64), (2, 300, 32), 
               (4, 256, 64), (1, 1000, 64)]
 
 
+def _sweep_shapes(n=10, seed=2026):
+    """Seeded random shapes: BH in [1, 6], S in [2, 600] with a bias to tile edges (multiples
+    of 32 and 64, plus or minus one), D in {32, 64}, scale in [0.05, 1/sqrt(D)] (at most the
+    model's scale, so gradient magnitudes stay those the tolerances are stated for)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        S = int(rng.integers(2, 601))
+        if rng.random() < 0.5:
+            S = max(1, int(rng.choice([32, 64])) * int(rng.integers(1, 10)) +
+                    int(rng.integers(-1, 2)))
+        D = int(rng.choice([32, 64]))
+        out.append((int(rng.integers(1, 7)), S, D,
+                    float(np.float32(rng.uniform(0.05, 1.0 / math.sqrt(D))))))
+    return out
+
+
+@pytest.mark.parametrize("BH,S,D,scale", _sweep_shapes())
+def test_bf16_and_fp32_random_shapes(gpu, BH, S, D, scale):
+    """bf16 and fp32 kernels, forward and backward, on seeded random shapes and scales against
+    the oracle at the path's tolerances (the fixed shapes above cover the named edge cases)."""
+    case(f"random shape BH={BH} S={S} D={D} scale={scale:.4f}")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=900 + S + 7 * BH + D, with_dout=True,
+                                       bf16=True)
+    o_ref, l_ref = oracle.attn_fwd(qn, kn, vn, scale, threads=8)
+    ref = oracle.attn_bwd(gn, qn, kn, vn, scale, threads=8)[:3]
+    for dtype, tol_o, tol_l, tol_g in ((torch.bfloat16, TOL_O, TOL_LSE, TOL_GRAD),
+                                       (torch.float32, TOL_F32, TOL_F32, TOL_F32)):
+        q, k, v, g = (dev(x, dtype) for x in (qn, kn, vn, gn))
+        out, lse = A.attention_forward(q, k, v, scale)
+        dq, dk, dv, _ = A.attention_backward(g, out, lse, q, k, v, scale)
+        torch.cuda.synchronize()
+        assert max_abs(host(out), o_ref) <= tol_o, dtype
+        assert max_abs(host(lse), l_ref) <= tol_l, dtype
+        for a, b, nm in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+            assert max_abs(host(a), b) <= tol_g, (dtype, nm)
+
+
 @pytest.mark.parametrize("BH,S,D", SMALL_BF16)
 def test_bf16_forward_backward_small(gpu, BH, S, D):
     case(f"bf16 small BH={BH} S={S} D={D}")
