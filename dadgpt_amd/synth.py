@@ -89,7 +89,8 @@ def attn_inputs(BH: int, S: int, D: int, seed: int = BASE_SEED, with_dout: bool 
 
 def decode_inputs(n_seq: int, H: int, max_len: int, D: int, seed: int = BASE_SEED,
                   bf16: bool = True, min_len: int = 1):
-    """q [n,H,D], k/v caches [n,H,max_len,D] (rows >= len zeroed), lens ~ U[min_len,max_len]."""
+    """q [n,H,D], k/v caches [n,H,max_len,D] (every row filled; a kernel reads only the first
+    lens[s] rows of sequence s), lens ~ U[min_len,max_len]."""
     lens = uniform_int(min_len, max_len, n_seq, seed ^ TENSOR_ID["lens"]).astype(np.int32)
     q = normal((n_seq, H, D), seed ^ TENSOR_ID["q"])
     kc = normal((n_seq, H, max_len, D), seed ^ TENSOR_ID["kcache"])

@@ -411,6 +411,36 @@ def test_decode_length_clamping(gpu):
     assert max_abs(o[1:], ref) <= TOL_DEC, "lengths beyond max_len clamp to max_len"
 
 
+def _decode_sweep(n=8, seed=77):
+    """Seeded random decode shapes: 1-24 sequences, 1-12 heads, max_len 1-2600 (so 1 to 6
+    chunks of a bf16 cache and up to 11 of an fp32 one), d_head 32 or 64, bf16 and fp32 caches
+    alternately; at most 400k cache rows (about 100 MB per fp32 cache)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        n_seq, H = int(rng.integers(1, 25)), int(rng.integers(1, 13))
+        L = int(rng.integers(1, 2601))
+        L = max(1, min(L, 400_000 // (n_seq * H)))
+        out.append((n_seq, H, L, int(rng.choice([32, 64])), i % 2 == 0))
+    return out
+
+
+@pytest.mark.parametrize("n,H,L,D,bf", _decode_sweep())
+def test_decode_random_shapes(gpu, n, H, L, D, bf):
+    """Ragged decode on seeded random shapes against the oracle; the longest and shortest
+    lengths (max_len and 1) are always among the sequences."""
+    dtype = torch.bfloat16 if bf else torch.float32
+    case(f"decode random n={n} H={H} max_len={L} D={D} {dtype}")
+    qn, kc, vc, lens = synth.decode_inputs(n, H, L, D, seed=300 + n * H + L, bf16=bf)
+    lens[0] = L
+    lens[-1] = min(lens[-1], 1) if n > 1 else L
+    scale = scale_of(D)
+    out, ws = run_decode(qn, kc, vc, lens, scale, dtype)
+    torch.cuda.synchronize()
+    assert max_abs(host(out), oracle.decode(qn, kc, vc, lens, scale)) <= (TOL_DEC if bf else
+                                                                          TOL_F32)
+
+
 @pytest.mark.parametrize("dtype,L", [(torch.bfloat16, 2500), (torch.float32, 1300)])
 def test_decode_split_spans(gpu, dtype, L):
     """Caches longer than one workgroup chunk publish partials that the last chunk merges."""
