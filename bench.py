@@ -13,12 +13,14 @@ CPU path timed on a bounded sample on this host.
 
 Config 5 (GPT-2 124M architecture, random init, 16 prompts of U[16,256] random tokens,
 batched prefill + 128 greedy tokens) is reported under components.generate_cfg5: tokens/s,
-the decode-attention time share, and the comparison with fp32 attention.
+the decode-attention time share, the comparison with fp32 attention, and the greedy gate at
+the reference's precision (fp32 flash vs fp32 materialized attention, fp32 projections).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-generate]
     python bench.py --profile-sample     # each kernel --reps times + a copy of known size,
                                          # for rocprofv3 --pmc runs; prints no bench line
     python bench.py --generate-only      # the config 5 leg alone (for rocprofv3)
+    python bench.py --generate-only --no-gate   # ... without the fp32 greedy-gate models
 """
 from __future__ import annotations
 
@@ -73,6 +75,9 @@ def parse():
     p.add_argument("--no-generate", action="store_true", help="skip the config 5 leg")
     p.add_argument("--generate-only", action="store_true",
                    help="run only the config 5 leg (for profiling); prints no bench line")
+    p.add_argument("--no-gate", action="store_true",
+                   help="config 5 without the fp32 greedy-gate models (profiles of the "
+                        "product path)")
     p.add_argument("--prewarm-seconds", type=float, default=2.0,
                    help="untimed fwd+bwd steps before the warmup, so clocks have ramped")
     return p.parse_args()
@@ -388,10 +393,11 @@ def profile_sample(wl, reps):
 
 
 
-def generate_cfg5():
+def generate_cfg5(gate: bool = True):
     """Config 5: GPT-2 124M architecture, random init (the reference's init rules,
     src/model.cpp:121-166), 16 prompts of U[16,256] random tokens, batched prefill into the KV
-    cache, 128 greedy tokens each; then the same with fp32 attention."""
+    cache, 128 greedy tokens each; then the same with fp32 attention, and (gate) with fp32
+    flash and fp32 materialized attention over fp32 projections."""
     import numpy as np
     import torch
 
@@ -415,10 +421,11 @@ def generate_cfg5():
     m32.close()
     # the greedy gate at the reference's precision: fp32 flash attention against the GPU's own
     # fp32 materialized attention, both over fp32 projections, logits kept for the comparison
-    gate = {}
-    for name, attention in (("flash", "fp32"), ("materialized", "fp32_materialized")):
+    gate_runs = {}
+    for name, attention in ((("flash", "fp32"), ("materialized", "fp32_materialized"))
+                            if gate else ()):
         mg = gpt2.GPT2(cfg, params, GEN_N, attention=attention, projections="fp32")
-        gate[name] = mg.generate(prompts, GEN_NEW, logits=True)
+        gate_runs[name] = mg.generate(prompts, GEN_NEW, logits=True)
         mg.close()
     del params
     torch.cuda.synchronize()
@@ -429,11 +436,12 @@ def generate_cfg5():
     a, b = best["tokens"], ref["tokens"]
     div = first_divergence(a, b)
     div_margins = [float(ref["margins"][r, d]) for r, d in enumerate(div) if d < GEN_NEW]
-    gf, gm = gate["flash"], gate["materialized"]
-    gdiv = first_divergence(gf["tokens"], gm["tokens"])
-    gate_dev = max(float(np.abs(gf["logits"][:min(d + 1, GEN_NEW), r] -
-                                gm["logits"][:min(d + 1, GEN_NEW), r]).max())
-                   for r, d in enumerate(gdiv))
+    if gate:
+        gf, gm = gate_runs["flash"], gate_runs["materialized"]
+        gdiv = first_divergence(gf["tokens"], gm["tokens"])
+        gate_dev = max(float(np.abs(gf["logits"][:min(d + 1, GEN_NEW), r] -
+                                    gm["logits"][:min(d + 1, GEN_NEW), r]).max())
+                       for r, d in enumerate(gdiv))
     total_ms = t["prefill_ms"] + t["decode_ms"]
     out = {
         "config": "GPT-2 124M arch (d768 L12 H12 ff3072 ctx1024 V50257), random init, 16 "
@@ -459,7 +467,9 @@ def generate_cfg5():
             "min_margin_fp32": float(ref["margins"].min()),
             "min_margin_bf16": float(best["margins"].min()),
         },
-        "greedy_gate_fp32": {
+    }
+    if gate:
+        out["greedy_gate_fp32"] = {
             "what": "fp32 flash attention vs the GPU's own fp32 materialized attention, both "
                     "with fp32 projections (the reference's precision), same weights and prompts",
             "rows_identical": int(sum(d == GEN_NEW for d in gdiv)),
@@ -467,8 +477,7 @@ def generate_cfg5():
             "first_divergence_per_row": gdiv,
             "max_logit_difference_shared_history": gate_dev,
             "min_margin": float(gm["margins"].min()),
-        },
-    }
+        }
     print(f"[bench] generate cfg5 {json.dumps(out)}", file=sys.stderr, flush=True)
     return out
 
@@ -486,7 +495,7 @@ def main():
     import torch
 
     if args.generate_only:
-        generate_cfg5()
+        generate_cfg5(gate=not args.no_gate)
         return
     wl = Workload(args.decode_copies)
     wl.A.lib()
