@@ -178,13 +178,23 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[
 #pragma unroll
   for (int i = 0; i < NQB; ++i) {
     float ls = fwd_exp<DROP>(pb[i], s[i], mrun[i], scale_log2, keep[i], dscale);
-    if (__builtin_amdgcn_ballot_w64(!(ls < kMaxP)) != 0) {  // wave-uniform
+    // ls >= 2^64, +inf or NaN, compared on the bits: a row's first chunk with masked keys sums
+    // to NaN (exp2 of -inf - (-inf)), and this file is built assuming no NaNs, under which a
+    // floating-point compare may be folded to one that NaN fails. Each row then takes the
+    // slow path on its own first chunk, whatever its wave-mates hold (a NaN query row
+    // included), and only the rows that need it move their maximum: the others keep m (a
+    // correction of exp2(0) = 1 and the same exponentials), so no row's bits depend on
+    // another row.
+    const bool need = (__float_as_uint(ls) & 0x7fffffffu) >= __float_as_uint(kMaxP);
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {  // wave-uniform
       float mx = s[i][0];
 #pragma unroll
       for (int r = 1; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s[i][r]), s[i][r + 1]);
       // every row of a chunk the wave computes has an unmasked key, so mx is finite
       mx = max_halves(fmaxf(mx, s[i][15])) * scale_log2;
-      const float mnew = fmaxf(mrun[i], mx);
+      // the two lane halves of a row hold different keys of it, and P V sums both against one
+      // maximum: the row moves it if either half needs to
+      const float mnew = or_halves(need) ? fmaxf(mrun[i], mx) : mrun[i];
       const float corr = fast_exp2(mrun[i] - mnew);  // 0 on a row's first chunk
       mrun[i] = mnew;
       lrun[i] *= corr;

@@ -72,6 +72,12 @@ __device__ __forceinline__ float sum_halves(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+__device__ __forceinline__ bool or_halves(bool x) {
+  const uint32_t u = x ? 1u : 0u;
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return (r[0] | r[1]) != 0;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Flips the sign of the 8 bf16 values (exact).

@@ -330,6 +330,31 @@ def test_bf16_causal_prefix(gpu):
     assert not torch.equal(o1[:, cut + 1:], o2[:, cut + 1:])
 
 
+@pytest.mark.parametrize("S,bad", [(23, [22]), (19, [18]), (2, [1]), (130, [129]),
+                                   (70, list(range(40, 50)))])
+@pytest.mark.parametrize("D", [64, 32])
+def test_forward_rows_independent_of_nan_query_rows(gpu, S, bad, D):
+    """A query row's output and logsumexp depend only on its own query and the keys up to it,
+    as in the reference's fused kernel (cuda/attention.cu:17-73: one thread per query row):
+    NaN query rows (the last row included, which the rows past S of its wave read as well)
+    leave every other row bit-identical, in bf16 and fp32. Padded prompt rows of a batched
+    prefill hold whatever their buffer held, so the generation path relies on this."""
+    case(f"forward rows independent of NaN query rows S={S} D={D} bad={bad[0]}..{bad[-1]}")
+    qn, kn, vn = synth.attn_inputs(3, S, D, seed=91, bf16=True)
+    q2 = qn.copy()
+    q2[1, bad] = np.nan
+    ok = np.ones(S, bool)
+    ok[bad] = False
+    for dtype in (torch.bfloat16, torch.float32):
+        k, v = dev(kn, dtype), dev(vn, dtype)
+        o1, l1 = A.attention_forward(dev(qn, dtype), k, v, 0.125)
+        o2, l2 = A.attention_forward(dev(q2, dtype), k, v, 0.125)
+        torch.cuda.synchronize()
+        assert torch.equal(o1[:, ok], o2[:, ok]) and torch.equal(l1[:, ok], l2[:, ok]), dtype
+        assert torch.equal(o1[0], o2[0]) and torch.equal(o1[2], o2[2])
+        assert bool(torch.isnan(o2[1, bad].float()).all())
+
+
 def test_bf16_errors_raise(gpu):
     case("bf16 error paths")
     q = torch.zeros(2, 16, 48, dtype=torch.bfloat16, device="cuda")
