@@ -51,6 +51,8 @@ C_SYMBOLS = (
     "dadgpt_causal_mask",
     "dadgpt_causal_mask_zero",
     "dadgpt_scale",
+    "dadgpt_split_heads",
+    "dadgpt_merge_heads",
     "dadgpt_attention_probs",
     "dadgpt_attention_probs_backward",
     "dadgpt_decode_probs",
@@ -65,6 +67,8 @@ CXX_SYMBOLS = (
     "_Z15gpu_causal_maskPfii",
     "_Z20gpu_causal_mask_zeroPfii",
     "_Z9gpu_scalePfif",
+    "_Z15gpu_split_headsPfPKfiiii",
+    "_Z15gpu_merge_headsPfPKfiiii",
     "_Z19use_fused_attention13AttentionImpliib",
 )
 
@@ -142,6 +146,8 @@ def lib():
     L.dadgpt_causal_mask.argtypes = [vp, i, i, vp]
     L.dadgpt_causal_mask_zero.argtypes = [vp, i, i, vp]
     L.dadgpt_scale.argtypes = [vp, i64, f, vp]
+    L.dadgpt_split_heads.argtypes = [vp, vp, i, i, i, i, vp]
+    L.dadgpt_merge_heads.argtypes = [vp, vp, i, i, i, i, vp]
     L.dadgpt_attention_probs.argtypes = [vp, i, i, f, vp]
     L.dadgpt_attention_probs_backward.argtypes = [vp, vp, vp, i, i, f, vp]
     L.dadgpt_decode_probs.argtypes = [vp, vp, i, i, i, f, vp]
@@ -479,6 +485,26 @@ def scale_(x, scale: float, stream=None) -> None:
     """gpu_scale (cuda/gpu_ops.cu:513-525): x *= scale in place."""
     _rows(x, "data", x.numel())
     _check(lib().dadgpt_scale(_ptr(x), x.numel(), scale, _stream_ptr(stream)))
+
+
+def split_heads(out, inp, batch_size: int, seq_len: int, n_heads: int, d_head: int,
+                stream=None) -> None:
+    """gpu_split_heads (cuda/gpu_ops.cu:426-446): fp32 [B*S, H*dh] -> [B*H, S, dh]."""
+    n = batch_size * seq_len * n_heads * d_head
+    _rows(out, "out", n)
+    _rows(inp, "in", n)
+    _check(lib().dadgpt_split_heads(_ptr(out), _ptr(inp), batch_size, seq_len, n_heads, d_head,
+                                    _stream_ptr(stream)))
+
+
+def merge_heads(out, inp, batch_size: int, seq_len: int, n_heads: int, d_head: int,
+                stream=None) -> None:
+    """gpu_merge_heads (cuda/gpu_ops.cu:448-474): fp32 [B*H, S, dh] -> [B*S, H*dh]."""
+    n = batch_size * seq_len * n_heads * d_head
+    _rows(out, "out", n)
+    _rows(inp, "in", n)
+    _check(lib().dadgpt_merge_heads(_ptr(out), _ptr(inp), batch_size, seq_len, n_heads, d_head,
+                                    _stream_ptr(stream)))
 
 
 def attention_probs(probs, BH: int, S: int, scale: float, stream=None) -> None:

@@ -192,6 +192,26 @@ using dadgpt::bf16;
 const bf16* B(const uint16_t* p) { return reinterpret_cast<const bf16*>(p); }
 bf16* B(uint16_t* p) { return reinterpret_cast<bf16*>(p); }
 
+// Shared checks of the head split and merge: positive sizes; one workgroup of at most 256
+// lanes per token row (rows below 2^24, so the work-items fit 32 bits) and rows of fewer than
+// 2^31 elements (32-bit column indices); non-null buffers that do not overlap.
+int check_heads(const char* fn, float* out, const float* in, int B, int S, int H, int dh) {
+  if (!out || !in) return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: null buffer", fn);
+  if (B < 1 || S < 1 || H < 1 || dh < 1)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                "%s: batch_size=%d, seq_len=%d, n_heads=%d, d_head=%d must be positive", fn, B,
+                S, H, dh);
+  const long long rows = (long long)B * S, D = (long long)H * dh;
+  if (rows >= kMaxRows || D > INT32_MAX)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                "%s: %lld token rows of %lld elements exceed the launch limits", fn, rows, D);
+  const uintptr_t o = reinterpret_cast<uintptr_t>(out), i = reinterpret_cast<uintptr_t>(in);
+  const uintptr_t bytes = (uintptr_t)(rows * D) * sizeof(float);
+  if (o < i + bytes && i < o + bytes)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: out and in overlap", fn);
+  return DADGPT_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -487,6 +507,24 @@ int dadgpt_causal_mask_zero(float* grads, int n_blocks, int S, void* stream) {
   const char* fn = "dadgpt_causal_mask_zero";
   if (int st = check_blocks(fn, n_blocks, S, grads)) return st;
   return from_hip(dadgpt::launch_causal_fill(grads, n_blocks, S, 0.0f, as_stream(stream)), fn);
+}
+
+int dadgpt_split_heads(float* out, const float* in, int batch_size, int seq_len, int n_heads,
+                       int d_head, void* stream) {
+  const char* fn = "dadgpt_split_heads";
+  if (int st = check_heads(fn, out, in, batch_size, seq_len, n_heads, d_head)) return st;
+  return from_hip(dadgpt::launch_split_heads(out, in, batch_size, seq_len, n_heads, d_head,
+                                             as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_merge_heads(float* out, const float* in, int batch_size, int seq_len, int n_heads,
+                       int d_head, void* stream) {
+  const char* fn = "dadgpt_merge_heads";
+  if (int st = check_heads(fn, out, in, batch_size, seq_len, n_heads, d_head)) return st;
+  return from_hip(dadgpt::launch_merge_heads(out, in, batch_size, seq_len, n_heads, d_head,
+                                             as_stream(stream)),
+                  fn);
 }
 
 int dadgpt_scale(float* data, int64_t count, float scale, void* stream) {

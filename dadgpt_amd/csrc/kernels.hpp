@@ -114,6 +114,12 @@ hipError_t launch_attention_probs_backward(float* ds, const float* dp, const flo
                                            int S, float scale, hipStream_t stream);
 hipError_t launch_decode_probs(float* p, const int* lens, int n_seq, int H, int max_len,
                                float scale, hipStream_t stream);
+// The reference's head split [B*S, H*dh] -> [B*H, S, dh] and merge (its inverse), fp32
+// (materialized.hip). out and in do not overlap; B*S < 2^31 rows.
+hipError_t launch_split_heads(float* out, const float* in, int B, int S, int H, int dh,
+                              hipStream_t stream);
+hipError_t launch_merge_heads(float* out, const float* in, int B, int S, int H, int dh,
+                              hipStream_t stream);
 
 // Device scratch that stands in for the decode workspace in the allocation-free entry point:
 // kDecodeScratchBytes per device, held until the process ends. decode_scratch returns the

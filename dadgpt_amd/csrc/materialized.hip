@@ -14,6 +14,9 @@
 // (cuda/gpu_ops.cu:147-193), and the softmax backward is p * (dp - sum(dp * p))
 // (cuda/gpu_ops.cu:542-563), masked, then scaled (src/model.cpp:601-607). Only the order of
 // the row sums differs (a wave tree instead of a block tree).
+#include <algorithm>
+#include <type_traits>
+
 #include "common.hpp"
 #include "lanes.hpp"
 #include "kernels.hpp"
@@ -129,6 +132,43 @@ __global__ void scale_kernel(float* __restrict__ x, long long n, float scale) {
     x[i] *= scale;
 }
 
+// The head split and merge (cuda/gpu_ops.cu:426-474), a pure permutation between the
+// token-major [B*S, H*dh] layout and [B*H, S, dh]. One workgroup per token row (b, s): its
+// threads walk the row in W-float pieces (16 bytes when dh and both buffers allow), so the
+// token-major side is one contiguous run and the head-major side one contiguous run of dh
+// floats per head. MERGE runs the other direction.
+template <bool MERGE, int W>
+__global__ __launch_bounds__(256) void heads_kernel(float* __restrict__ out,
+                                                    const float* __restrict__ in, int S, int H,
+                                                    int dh) {
+  using V = std::conditional_t<W == 4, f32x4, float>;
+  const int row = blockIdx.x;  // b * S + s
+  const int b = row / S, s = row - b * S;
+  const int D = H * dh;
+  const size_t tok = (size_t)row * D;
+  for (int c = W * threadIdx.x; c < D; c += W * blockDim.x) {
+    const int h = c / dh, x = c - h * dh;
+    const size_t head = (((size_t)b * H + h) * S + s) * dh + x;
+    const size_t src = MERGE ? head : tok + c, dst = MERGE ? tok + c : head;
+    *reinterpret_cast<V*>(out + dst) = *reinterpret_cast<const V*>(in + src);
+  }
+}
+
+template <bool MERGE>
+hipError_t launch_heads(float* out, const float* in, int B, int S, int H, int dh,
+                        hipStream_t stream) {
+  const bool wide = dh % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(in) % 16 == 0;
+  const int pieces = wide ? H * dh / 4 : H * dh;
+  const int threads = std::min(256, (pieces + 63) / 64 * 64);
+  const unsigned rows = (unsigned)((long long)B * S);
+  if (wide)
+    heads_kernel<MERGE, 4><<<rows, threads, 0, stream>>>(out, in, S, H, dh);
+  else
+    heads_kernel<MERGE, 1><<<rows, threads, 0, stream>>>(out, in, S, H, dh);
+  return hipGetLastError();
+}
+
 unsigned row_blocks(long long rows) {
   return (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
 }
@@ -192,6 +232,16 @@ hipError_t launch_decode_probs(float* p, const int* lens, int n_seq, int H, int 
                                float scale, hipStream_t stream) {
   return launch_softmax<kLength>(p, p, (long long)n_seq * H, max_len, 1, scale, lens, H,
                                  stream);
+}
+
+hipError_t launch_split_heads(float* out, const float* in, int B, int S, int H, int dh,
+                              hipStream_t stream) {
+  return launch_heads<false>(out, in, B, S, H, dh, stream);
+}
+
+hipError_t launch_merge_heads(float* out, const float* in, int B, int S, int H, int dh,
+                              hipStream_t stream) {
+  return launch_heads<true>(out, in, B, S, H, dh, stream);
 }
 
 }  // namespace dadgpt

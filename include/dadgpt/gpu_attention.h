@@ -265,6 +265,17 @@ int dadgpt_causal_mask(float* scores, int n_blocks, int S, void* stream);
 int dadgpt_causal_mask_zero(float* grads, int n_blocks, int S, void* stream);
 /* gpu_scale (cuda/gpu_ops.cuh:110, cuda/gpu_ops.cu:513-525): data[i] *= scale. */
 int dadgpt_scale(float* data, int64_t count, float scale, void* stream);
+/* gpu_split_heads (cuda/gpu_ops.cuh:99-100, cuda/gpu_ops.cu:426-446): fp32
+ * in [batch_size * seq_len, n_heads * d_head] -> out [batch_size * n_heads, seq_len, d_head],
+ * out[(b*H + h)*S*dh + s*dh + x] = in[(b*S + s)*H*dh + h*dh + x]. out and in must not overlap.
+ * The attention entry points above read and write the token-major layout in place
+ * (_strided, _tokens), so the product path needs no split pass. */
+int dadgpt_split_heads(float* out, const float* in, int batch_size, int seq_len, int n_heads,
+                       int d_head, void* stream);
+/* gpu_merge_heads (cuda/gpu_ops.cuh:102-103, cuda/gpu_ops.cu:448-474): the inverse,
+ * [batch_size * n_heads, seq_len, d_head] -> [batch_size * seq_len, n_heads * d_head]. */
+int dadgpt_merge_heads(float* out, const float* in, int batch_size, int seq_len, int n_heads,
+                       int d_head, void* stream);
 
 /* scores [BH, S, S] -> probabilities in place: x scale, -1e9 above the diagonal, row softmax
  * (gpu_scale + gpu_causal_mask + gpu_softmax, src/model.cpp:407-409, in one pass). */

@@ -364,3 +364,48 @@ def test_decode_probs_and_materialized_decode(gpu):
         want = _softmax64(s[r, :Ls].astype(np.float32) * np.float32(scale))
         assert max_abs(got[r, :Ls], want) <= 1e-6
         assert np.all(got[r, Ls:] == 0.0)
+
+
+def _split_np(x, B, S, H, dh):
+    """[B*S, H*dh] -> [B*H, S, dh] by index arithmetic (cuda/gpu_ops.cu:426-446)."""
+    return x.reshape(B, S, H, dh).transpose(0, 2, 1, 3).reshape(B * H, S, dh)
+
+
+@pytest.mark.parametrize("B,S,H,dh", [(16, 1024, 12, 64), (2, 7, 3, 32), (1, 5, 4, 3),
+                                      (3, 33, 12, 64)])
+def test_split_merge_heads_reference_symbols(gpu, B, S, H, dh):
+    """gpu_split_heads / gpu_merge_heads under their mangled reference names
+    (cuda/gpu_ops.cuh:98-104), null stream: bit-exact against the numpy permutation, the
+    merge inverts the split, and the C ABI on a stream gives the same bits. (1, 5, 4, 3) has
+    d_head not a multiple of 4 (the one-float path); (3, 33, 12, 64) is also run from an input
+    4 bytes past a 16-byte boundary (the one-float path with d_head 64)."""
+    case(f"split/merge heads B={B} S={S} H={H} dh={dh}")
+    L = A.lib()
+    fns = {}
+    for key, name in (("split", "_Z15gpu_split_headsPfPKfiiii"),
+                      ("merge", "_Z15gpu_merge_headsPfPKfiiii")):
+        f = getattr(L, name)
+        f.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int] * 4
+        f.restype = None
+        fns[key] = f
+    n = B * S * H * dh
+    x = synth.normal((n,), 950 + dh)
+    want = _split_np(x, B, S, H, dh)
+    for off in ((0, 1) if (B, S) == (3, 33) else (0,)):
+        src = torch.from_numpy(np.concatenate([np.zeros(off, np.float32), x])).to("cuda")
+        xin = src[off:]
+        heads = torch.full((n,), -7.0, device="cuda")
+        back = torch.full((n,), -7.0, device="cuda")
+        torch.cuda.synchronize()
+        fns["split"](heads.data_ptr(), xin.data_ptr(), B, S, H, dh)
+        fns["merge"](back.data_ptr(), heads.data_ptr(), B, S, H, dh)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(heads).reshape(B * H, S, dh), want), off
+        assert np.array_equal(host(back), x), off
+    h2 = torch.empty(n, device="cuda")
+    b2 = torch.empty(n, device="cuda")
+    A.split_heads(h2, dev(x), B, S, H, dh)
+    A.merge_heads(b2, h2, B, S, H, dh)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(h2).reshape(B * H, S, dh), want)
+    assert np.array_equal(host(b2), x)
