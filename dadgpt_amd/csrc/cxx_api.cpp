@@ -4,6 +4,7 @@
 #include <stdexcept>
 #include <string>
 
+#include "dadgpt/attention_impl.hpp"
 #include "dadgpt/gpu_attention.h"
 #include "dadgpt/gpu_ops_attention.hpp"
 
@@ -48,6 +49,16 @@ void gpu_causal_mask_zero(float* grads, int num_blocks, int seq_len) {
 
 void gpu_scale(float* data, int size, float scale) {
   throw_if(dadgpt_scale(data, size, scale, nullptr));
+}
+
+void gpu_split_heads(float* out, const float* in, int batch_size, int seq_len, int n_heads,
+                     int d_head) {
+  throw_if(dadgpt_split_heads(out, in, batch_size, seq_len, n_heads, d_head, nullptr));
+}
+
+void gpu_merge_heads(float* out, const float* in, int batch_size, int seq_len, int n_heads,
+                     int d_head) {
+  throw_if(dadgpt_merge_heads(out, in, batch_size, seq_len, n_heads, d_head, nullptr));
 }
 
 bool use_fused_attention(AttentionImpl impl, int d_head, int ctx_len, bool attn_dropout) {

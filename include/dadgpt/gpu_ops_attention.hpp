@@ -33,7 +33,17 @@ void gpu_causal_mask_zero(float* grads, int num_blocks, int seq_len);
 // cuda/gpu_ops.cuh:110
 void gpu_scale(float* data, int size, float scale);
 
-// src/model.hpp:80 and the predicate of src/model.cpp:183-197 without the Model: the caller
-// passes its implementation choice, head size and context length.
-enum class AttentionImpl { Auto, Fused, Materialized };
+// cuda/gpu_ops.cuh:98-104: [B*S, H*dh] <-> [B*H, S, dh], fp32, null stream. The attention
+// calls of <dadgpt/gpu_attention.h> also read and write the token-major layout in place.
+void gpu_split_heads(float* out, const float* in, int batch_size, int seq_len, int n_heads,
+                     int d_head);
+void gpu_merge_heads(float* out, const float* in, int batch_size, int seq_len, int n_heads,
+                     int d_head);
+
+// The predicate of src/model.cpp:183-197 without the Model: the caller passes its
+// implementation choice, head size and context length. AttentionImpl is the reference's own
+// enum (src/model.hpp:81, `enum class AttentionImpl { Auto, Fused, Materialized };`): it is only
+// declared here, so this header can be included before or after the reference's model.hpp.
+// Callers without model.hpp include <dadgpt/attention_impl.hpp> for the definition.
+enum class AttentionImpl;
 bool use_fused_attention(AttentionImpl impl, int d_head, int ctx_len, bool attn_dropout);

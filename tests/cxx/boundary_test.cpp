@@ -1,12 +1,14 @@
 // Links against libdadgpt_attn.so through the reference's own wrapper names and C++
 // signatures (cuda/gpu_ops.cuh:57,76,106-122; src/model.hpp:80) and checks their host-side
 // behaviour, which needs no GPU: the supported() and fused/materialized predicates, and the
-// std::runtime_error thrown for an unsupported d_head (message as cuda/attention.cu:238,251)
-// and for a null buffer. Built and run by tests/test_capi.py.
+// std::runtime_error thrown for an unsupported d_head (message as cuda/attention.cu:238,251),
+// for a null buffer and for bad head split/merge shapes (cuda/gpu_ops.cuh:98-104). Built and
+// run by tests/test_capi.py.
 #include <cstdio>
 #include <stdexcept>
 #include <string>
 
+#include "dadgpt/attention_impl.hpp"
 #include "dadgpt/gpu_attention.h"
 #include "dadgpt/gpu_ops_attention.hpp"
 
@@ -56,6 +58,12 @@ int main() {
   EXPECT(m.find("null") != std::string::npos);
   m = thrown([&] { gpu_softmax_backward(p, p, nullptr, 4, 64); });
   EXPECT(m.find("null") != std::string::npos);
+  m = thrown([&] { gpu_split_heads(nullptr, p, 2, 16, 4, 64); });
+  EXPECT(m.find("null") != std::string::npos);
+  m = thrown([&] { gpu_merge_heads(p + 4096, p, 2, 0, 4, 64); });
+  EXPECT(m.find("positive") != std::string::npos);
+  m = thrown([&] { gpu_split_heads(p + 16, p, 2, 16, 4, 64); });  // overlapping buffers
+  EXPECT(m.find("overlap") != std::string::npos);
   EXPECT(use_fused_attention(AttentionImpl::Fused, 64, 64, false));
   EXPECT(!use_fused_attention(AttentionImpl::Fused, 64, 64, true));
   EXPECT(!use_fused_attention(AttentionImpl::Fused, 48, 1024, false));

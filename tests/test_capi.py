@@ -307,3 +307,19 @@ def test_cxx_reference_names_link_and_throw(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     assert r.stdout.strip().endswith("OK")
+
+
+@pytest.mark.parametrize("model_hpp_first", [True, False])
+def test_cxx_header_composes_with_reference_enum(tmp_path, model_hpp_first):
+    """The drop-in header only declares AttentionImpl, so a caller that also includes the
+    reference's model.hpp (which defines it, src/model.hpp:81) compiles in either include order
+    and links use_fused_attention (a full definition in the header would be a redefinition)."""
+    exe = tmp_path / "model_hpp_order"
+    libdir = os.path.dirname(A.LIB_PATH)
+    flags = ["-DMODEL_HPP_FIRST"] if model_hpp_first else []
+    subprocess.run(["g++", "-std=c++20", "-O1", *flags, f"-I{ROOT}/include",
+                    os.path.join(ROOT, "tests", "cxx", "model_hpp_order_test.cpp"),
+                    f"-L{libdir}", "-ldadgpt_attn", f"-Wl,-rpath,{libdir}", "-o", str(exe)],
+                   check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "OK", r.stdout + r.stderr
