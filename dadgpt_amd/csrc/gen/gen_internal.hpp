@@ -91,26 +91,40 @@ hipError_t bias_gelu(O* out, const float* y, const bf16* bias, int rows, int col
 template <typename T>
 hipError_t gather_rows(T* out, const T* in, const int* idx, int rows, int d, hipStream_t s);
 
+// Where each row of a generate call stops (src/generate.cpp:121-135): stop[b] is the row's
+// stop token (-1: none), limit[b] the sequence length (prompt + generated) at which it ends;
+// done[b] is set once the row has stopped, and ndone counts the stopped rows.
+struct RowStop {
+  const int* stop;
+  const int* limit;
+  int* done;
+  int* ndone;
+};
+
 // Greedy pick per row of logits [n, V]: the first maximum (as std::max_element) and its
 // margin over the runner-up, stored at step = pos[b] - (prompt_len[b] - 1) in tokens
 // [step*n + b] and margins; then the decode state advances: tok[b] = pick, pos[b] += 1,
 // cache_len[b] = pos[b] + 1, and the next decode step's input row is embedded:
 // x[b] = wte[tok[b]] + wpe[pos[b]] (d floats; skipped where pos[b] >= ctx, past the last step).
 // A row with no comparable logit (all NaN) picks column 0, as std::max_element does.
+// A pick equal to the row's stop token, or one that brings the row to its length limit, stops
+// the row (rs.done[b] = 1, rs.ndone += 1) after that advance. A stopped row emits nothing more
+// and keeps its state: every later step re-feeds its last token at its last position (the
+// step repeats, appending the same K/V to the same cache row), so it stays inside its context.
 // Two launches: 32 blocks per row reduce slices into candidates (scratch of
 // pick_scratch_floats(n, 0) floats), then one block per row merges them and embeds.
 size_t pick_scratch_floats(int n, int parts);
 hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
-                          const int* prompt_len, const float* logits, float* scratch, int n,
-                          int V, float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
-                          hipStream_t s);
+                          const int* prompt_len, RowStop rs, const float* logits,
+                          float* scratch, int n, int V, float* x, const bf16* wte,
+                          const bf16* wpe, int d, int ctx, hipStream_t s);
 // The same pick from candidates already reduced per workgroup by the logits projection
 // (kEpiStore with SkinnyArgs::cand): `parts` candidates per row in three planes of `rows`
 // rows (values, columns, runner-up values). One launch.
 hipError_t pick_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
-                        const int* prompt_len, const float* cand, int parts, int rows, int n,
-                        int V, float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
-                        hipStream_t s);
+                        const int* prompt_len, RowStop rs, const float* cand, int parts,
+                        int rows, int n, int V, float* x, const bf16* wte, const bf16* wpe,
+                        int d, int ctx, hipStream_t s);
 
 // ---- skinny projections of the decode step (skinny.hip) ----
 

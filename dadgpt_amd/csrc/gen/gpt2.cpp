@@ -151,6 +151,11 @@ struct dadgpt_gpt2 {
   // packed row of each prompt's last token
   int *rowmap = nullptr, *lastrow = nullptr;
   int *cur_tok = nullptr, *cur_pos = nullptr, *cache_len = nullptr;
+  // where each row stops (RowStop): stop token, length limit, stopped flag; the stopped-row
+  // count and its pinned host copies (two slots, read one check late)
+  int *stop_tok = nullptr, *limit = nullptr, *done = nullptr, *ndone = nullptr;
+  int* h_ndone = nullptr;
+  hipEvent_t ndone_ev[2] = {nullptr, nullptr};
   int* out_tok = nullptr;       // [ctx_len, max_batch]: every step any call can take
   float* out_margin = nullptr;
   std::vector<hipEvent_t> events;
@@ -158,6 +163,7 @@ struct dadgpt_gpt2 {
   std::map<int, hipGraphExec_t> graphs;  // captured decode step per batch size
 
   const bf16* P(size_t offset) const { return params + offset; }
+  RowStop row_stop() const { return RowStop{stop_tok, limit, done, ndone}; }
 
   int alloc(void** p, size_t bytes, const char* what) {
     if (hipMalloc(p, bytes < 16 ? 16 : bytes) != hipSuccess)
@@ -350,7 +356,7 @@ int head(dadgpt_gpt2* m, int n) {
   TRY(proj(m, m->logits, in_h(m), m->P(m->off.tok_emb), m->emb32, n, c.d_model, c.vocab_size,
            true));
   TRY_HIP(argmax_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
-                         m->lens, m->logits, m->pick, n, c.vocab_size, m->x,
+                         m->lens, m->row_stop(), m->logits, m->pick, n, c.vocab_size, m->x,
                          m->P(m->off.tok_emb), m->P(m->off.pos_emb), c.d_model, c.ctx_len, s),
           "argmax_advance");
   return DADGPT_OK;
@@ -431,7 +437,8 @@ int decode_step_skinny(dadgpt_gpt2* m, int n, hipEvent_t* attn_ev) {
   lg.cand = m->pick;  // each workgroup's greedy candidate per row
   TRY_HIP(skinny_gemm(kProRowsBlocked, kEpiStore, lg, s), "skinny logits");
   TRY_HIP(pick_advance(m->out_tok, m->out_margin, m->cur_tok, m->cur_pos, m->cache_len,
-                       m->lens, m->pick, skinny_store_parts(c.vocab_size), kSkinnyRows, n,
+                       m->lens, m->row_stop(), m->pick, skinny_store_parts(c.vocab_size),
+                       kSkinnyRows, n,
                        c.vocab_size, m->x, m->P(m->off.tok_emb), m->P(m->off.pos_emb), d,
                        c.ctx_len, s),
           "pick_advance");
@@ -533,6 +540,9 @@ void dadgpt_gpt2_destroy(dadgpt_gpt2* m) {
   if (!m) return;
   if (m->stream) (void)hipStreamSynchronize(m->stream);
   for (hipEvent_t e : m->events) (void)hipEventDestroy(e);
+  for (hipEvent_t e : m->ndone_ev)
+    if (e) (void)hipEventDestroy(e);
+  if (m->h_ndone) (void)hipHostFree(m->h_ndone);
   for (auto& [n, g] : m->graphs) (void)hipGraphExecDestroy(g);
   for (void* p : m->allocs) (void)hipFree(p);
   if (m->blas) dadgpt_blas_destroy(m->blas);
@@ -614,7 +624,9 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
                                            skinny_store_parts(c.vocab_size)),
                        "pick scratch")) ||
       (st = m->alloc_n(&m->lse, rows * c.n_heads, "lse")) ||
-      (!proj32 && (st = m->alloc_n(&m->h, rows * d, "ln out"))) ||
+      // (the decode step's final LayerNorm writes, and the skinny logits read, 16 K-blocked
+      // rows whatever max_batch * ctx_len is)
+      (!proj32 && (st = m->alloc_n(&m->h, std::max(rows, (size_t)kSkinnyRows) * d, "ln out"))) ||
       (!proj32 && (st = m->alloc_n(&m->a, rows * d, "attn in"))) ||
       // (the skinny fc1 writes 16 K-blocked rows, whatever max_batch is)
       (!proj32 && (st = m->alloc_n(&m->g, std::max(rows, (size_t)kSkinnyRows) * c.d_ff,
@@ -637,6 +649,10 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
       (st = m->alloc_n(&m->cur_tok, max_batch, "cur_tok")) ||
       (st = m->alloc_n(&m->cur_pos, max_batch, "cur_pos")) ||
       (st = m->alloc_n(&m->cache_len, max_batch, "cache_len")) ||
+      (st = m->alloc_n(&m->stop_tok, max_batch, "stop tokens")) ||
+      (st = m->alloc_n(&m->limit, max_batch, "length limits")) ||
+      (st = m->alloc_n(&m->done, max_batch, "stopped rows")) ||
+      (st = m->alloc_n(&m->ndone, 1, "stopped count")) ||
       (st = m->alloc_n(&m->out_tok, rows, "tokens out")) ||
       (st = m->alloc_n(&m->out_margin, rows, "margins out")) ||
       // materialized attention: the prefill's [n*H, S, S] probabilities (the decode's
@@ -697,6 +713,23 @@ int dadgpt_gpt2_create(const dadgpt_gpt2_config* config, const uint16_t* params,
     if (hipMemsetAsync(m->ws, 0, m->ws_bytes, m->stream) != hipSuccess)
       return bail(fail(DADGPT_ERR_HIP, "dadgpt_gpt2_create: workspace clear failed"));
   }
+  // Split heads: a packed prefill writes only the prompt rows. The padded K/V rows of fp32
+  // attention are multiplied by exact-zero probabilities and must not hold NaN or Inf bit
+  // patterns; the padded Q rows are discarded queries, kept finite too (zero until a call
+  // writes them).
+  if (hipMemsetAsync(m->qh, 0, rows * d * ab, m->stream) != hipSuccess ||
+      (m->fp32 && (hipMemsetAsync(m->kh, 0, rows * d * ab, m->stream) != hipSuccess ||
+                   hipMemsetAsync(m->vh, 0, rows * d * ab, m->stream) != hipSuccess)))
+    return bail(fail(DADGPT_ERR_HIP, "dadgpt_gpt2_create: split-head clear failed"));
+  if (hipHostMalloc((void**)&m->h_ndone, 2 * sizeof(int), hipHostMallocDefault) != hipSuccess) {
+    m->h_ndone = nullptr;
+    return bail(fail(DADGPT_ERR_HIP, "dadgpt_gpt2_create: hipHostMalloc failed"));
+  }
+  for (hipEvent_t& e : m->ndone_ev)
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+      e = nullptr;
+      return bail(fail(DADGPT_ERR_HIP, "dadgpt_gpt2_create: hipEventCreate failed"));
+    }
   std::vector<int> ones(max_batch, 1), zeros(max_batch, 0);
   if (hipMemcpyAsync(m->ones, ones.data(), max_batch * sizeof(int), hipMemcpyHostToDevice,
                      m->stream) != hipSuccess ||
@@ -714,40 +747,32 @@ int dadgpt_gpt2_set_graphs(dadgpt_gpt2* m, int enable) {
   return DADGPT_OK;
 }
 
-int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* prompt_lens,
-                         int n, int prompt_stride, int new_tokens, int32_t* tokens,
-                         float* margins, float* logits, dadgpt_gpt2_timing* timing) {
-  const char* fn = "dadgpt_gpt2_generate";
-  if (!m || !prompts || !prompt_lens || !tokens)
-    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: null argument", fn);
+}  // extern "C"
+
+namespace {
+
+// Greedy generation over validated prompts (1 <= len[b] <= prompt_stride, tokens in the
+// vocabulary, len[b] < limit[b] <= ctx_len): row b stops at its stop token (stop[b], -1 for
+// none) or when it reaches limit[b] tokens, prompt included (src/generate.cpp:121-135).
+// max_new = max_b (limit[b] - len[b]) picks at most. tk/mg receive the picks and margins
+// step-major [max_new][n]: row b's entries are valid up to its last pick. With early_exit, the
+// step loop ends once every row has stopped (checked every kCheck steps, one check late, so
+// the host never waits on a step it has just queued).
+int generate_core(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* prompt_lens, int n,
+                  int prompt_stride, const int* limit, const int* stop, int max_new,
+                  bool early_exit, std::vector<int>& tk, std::vector<float>& mg, float* logits,
+                  dadgpt_gpt2_timing* timing) {
   const auto& c = m->c;
-  if (n < 1 || n > m->max_batch || new_tokens < 1)
-    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: n=%d (max_batch %d), new_tokens=%d", fn, n,
-                m->max_batch, new_tokens);
   int S = 0;
-  for (int b = 0; b < n; ++b) {
-    const int len = prompt_lens[b];
-    if (len < 1 || len > prompt_stride || len + new_tokens > c.ctx_len)
-      return fail(DADGPT_ERR_INVALID_ARGUMENT,
-                  "%s: prompt %d has %d tokens (stride %d); prompt + %d new tokens must fit "
-                  "the context of %d",
-                  fn, b, len, prompt_stride, new_tokens, c.ctx_len);
-    for (int t = 0; t < len; ++t) {
-      const int tok = prompts[(size_t)b * prompt_stride + t];
-      if (tok < 0 || tok >= c.vocab_size)
-        return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: token %d of prompt %d is %d (vocab %d)",
-                    fn, t, b, tok, c.vocab_size);
-    }
-    S = len > S ? len : S;
-  }
+  for (int b = 0; b < n; ++b) S = std::max(S, (int)prompt_lens[b]);
   hipStream_t s = m->stream;
-  const size_t outs = (size_t)new_tokens * n;  // <= ctx_len * max_batch, the buffers' size
+  const size_t outs = (size_t)max_new * n;  // <= ctx_len * max_batch, the buffers' size
 
   // padded prompt rows, lengths, the position before the first generated token, and the
   // packed prefill rows (every prompt position once, no padding): their padded positions and
   // each prompt's last one
   std::vector<int> tok((size_t)n * S, 0), len(prompt_lens, prompt_lens + n), pos(n), rowmap,
-      lastrow(n);
+      lastrow(n), stops(n, -1), limits(limit, limit + n);
   rowmap.reserve((size_t)n * S);
   for (int b = 0; b < n; ++b) {
     for (int t = 0; t < len[b]; ++t) {
@@ -756,6 +781,7 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
     }
     lastrow[b] = (int)rowmap.size() - 1;
     pos[b] = len[b] - 1;
+    if (stop) stops[b] = stop[b];
   }
   const int rows = (int)rowmap.size();
   TRY_HIP(hipMemcpyAsync(m->tok_in, tok.data(), tok.size() * sizeof(int), hipMemcpyHostToDevice, s),
@@ -770,8 +796,14 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
           "hipMemcpyAsync(lens)");
   TRY_HIP(hipMemcpyAsync(m->cur_pos, pos.data(), n * sizeof(int), hipMemcpyHostToDevice, s),
           "hipMemcpyAsync(pos)");
+  TRY_HIP(hipMemcpyAsync(m->stop_tok, stops.data(), n * sizeof(int), hipMemcpyHostToDevice, s),
+          "hipMemcpyAsync(stop tokens)");
+  TRY_HIP(hipMemcpyAsync(m->limit, limits.data(), n * sizeof(int), hipMemcpyHostToDevice, s),
+          "hipMemcpyAsync(length limits)");
+  TRY_HIP(hipMemsetAsync(m->done, 0, n * sizeof(int), s), "hipMemsetAsync(stopped rows)");
+  TRY_HIP(hipMemsetAsync(m->ndone, 0, sizeof(int), s), "hipMemsetAsync(stopped count)");
 
-  const int steps = new_tokens - 1;
+  const int steps = max_new - 1;
   const bool timed = timing != nullptr;
   // Only a decode step made of this library's own kernels is captured and replayed (the
   // skinny step of up to 16 sequences with bf16 projections and flash decode attention). A
@@ -800,7 +832,19 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
   // With graphs, step 1 runs eagerly (it builds any missing hipBLASLt plan) and every later
   // step replays the captured step. Without graphs, timing brackets each attention launch.
   const bool attn_events = timed && !graphs;
+  constexpr int kCheck = 16;
+  int ran = 0;
   for (int t = 1; t <= steps; ++t) {
+    if (early_exit && t % kCheck == 0) {
+      const int slot = (t / kCheck) & 1;
+      if (t >= 2 * kCheck) {  // the count copied kCheck steps ago
+        TRY_HIP(hipEventSynchronize(m->ndone_ev[slot ^ 1]), "hipEventSynchronize");
+        if (m->h_ndone[slot ^ 1] >= n) break;
+      }
+      TRY_HIP(hipMemcpyAsync(m->h_ndone + slot, m->ndone, sizeof(int), hipMemcpyDeviceToHost, s),
+              "hipMemcpyAsync(stopped count)");
+      TRY_HIP(hipEventRecord(m->ndone_ev[slot], s), "hipEventRecord");
+    }
     if (graphs && t > 1) {
       hipGraphExec_t g = nullptr;
       TRY(step_graph(m, n, &g));
@@ -809,35 +853,161 @@ int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* 
       TRY(decode_step(m, n, attn_events ? ev + 3 + 2 * (size_t)(t - 1) * c.n_layers : nullptr));
     }
     if (logits) TRY(copy_logits(m, logits, n, t));
+    ran = t;
   }
   if (timed) TRY_HIP(hipEventRecord(ev[2], s), "hipEventRecord");
 
-  std::vector<int> tk(outs);
-  std::vector<float> mg(outs);
+  tk.assign(outs, 0);
+  mg.assign(outs, 0.f);
   TRY_HIP(hipMemcpyAsync(tk.data(), m->out_tok, outs * sizeof(int), hipMemcpyDeviceToHost, s),
           "hipMemcpyAsync(tokens)");
   TRY_HIP(hipMemcpyAsync(mg.data(), m->out_margin, outs * sizeof(float), hipMemcpyDeviceToHost,
                          s),
           "hipMemcpyAsync(margins)");
   TRY_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
-  for (int b = 0; b < n; ++b)
-    for (int t = 0; t < new_tokens; ++t) {
-      tokens[(size_t)b * new_tokens + t] = tk[(size_t)t * n + b];
-      if (margins) margins[(size_t)b * new_tokens + t] = mg[(size_t)t * n + b];
-    }
   if (timed) {
     float ms = 0.f;
-    timing->decode_steps = steps;
+    timing->decode_steps = ran;
     TRY_HIP(hipEventElapsedTime(&ms, ev[0], ev[1]), "hipEventElapsedTime");
     timing->prefill_ms = ms;
     TRY_HIP(hipEventElapsedTime(&ms, ev[1], ev[2]), "hipEventElapsedTime");
     timing->decode_ms = logits ? NAN : ms;  // per-step host copies would be counted
     double attn = 0.0;
-    for (size_t i = 0; attn_events && i < (size_t)steps * c.n_layers; ++i) {
+    for (size_t i = 0; attn_events && i < (size_t)ran * c.n_layers; ++i) {
       TRY_HIP(hipEventElapsedTime(&ms, ev[3 + 2 * i], ev[4 + 2 * i]), "hipEventElapsedTime");
       attn += ms;
     }
     timing->decode_attn_ms = attn_events ? (float)attn : -1.0f;
+  }
+  return DADGPT_OK;
+}
+
+// Prompts of n rows: 1 <= len <= stride and every token in the vocabulary.
+int check_prompts(const dadgpt_gpt2* m, const char* fn, const int32_t* prompts,
+                  const int32_t* prompt_lens, int n, int prompt_stride) {
+  for (int b = 0; b < n; ++b) {
+    const int len = prompt_lens[b];
+    if (len < 1 || len > prompt_stride)
+      return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: prompt %d has %d tokens (stride %d)", fn, b,
+                  len, prompt_stride);
+    for (int t = 0; t < len; ++t) {
+      const int tok = prompts[(size_t)b * prompt_stride + t];
+      if (tok < 0 || tok >= m->c.vocab_size)
+        return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: token %d of prompt %d is %d (vocab %d)",
+                    fn, t, b, tok, m->c.vocab_size);
+    }
+  }
+  return DADGPT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dadgpt_gpt2_truncate_prompt(const int32_t* prompt, int len, int max_len, int ctx_len,
+                                int32_t* out, int32_t* out_len) {
+  if (!prompt || !out || !out_len || len < 1 || ctx_len < 1)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                "dadgpt_gpt2_truncate_prompt: null buffer, len %d or ctx_len %d", len, ctx_len);
+  // src/generate.cpp:97-110: the limit is capped at the context; a prompt that leaves no room
+  // keeps its first token and its last max_len - 2 tokens
+  const int eff = std::min(max_len, ctx_len);
+  if (len >= eff && len > 1) {
+    const int keep = std::max(eff - 2, 0);
+    // (prompt and out may be the same buffer: the kept tail moves towards the front)
+    out[0] = prompt[0];
+    std::copy(prompt + (len - keep), prompt + len, out + 1);
+    *out_len = 1 + keep;
+  } else {
+    if (out != prompt) std::copy(prompt, prompt + len, out);
+    *out_len = len;
+  }
+  return DADGPT_OK;
+}
+
+int dadgpt_gpt2_generate(dadgpt_gpt2* m, const int32_t* prompts, const int32_t* prompt_lens,
+                         int n, int prompt_stride, int new_tokens, int32_t* tokens,
+                         float* margins, float* logits, dadgpt_gpt2_timing* timing) {
+  const char* fn = "dadgpt_gpt2_generate";
+  if (!m || !prompts || !prompt_lens || !tokens)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: null argument", fn);
+  const auto& c = m->c;
+  if (n < 1 || n > m->max_batch || new_tokens < 1)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: n=%d (max_batch %d), new_tokens=%d", fn, n,
+                m->max_batch, new_tokens);
+  TRY(check_prompts(m, fn, prompts, prompt_lens, n, prompt_stride));
+  std::vector<int> limit(n);
+  for (int b = 0; b < n; ++b) {
+    if (prompt_lens[b] + new_tokens > c.ctx_len)
+      return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                  "%s: prompt %d has %d tokens; prompt + %d new tokens must fit the context of "
+                  "%d",
+                  fn, b, prompt_lens[b], new_tokens, c.ctx_len);
+    limit[b] = prompt_lens[b] + new_tokens;
+  }
+  std::vector<int> tk;
+  std::vector<float> mg;
+  TRY(generate_core(m, prompts, prompt_lens, n, prompt_stride, limit.data(), nullptr, new_tokens,
+                    false, tk, mg, logits, timing));
+  for (int b = 0; b < n; ++b)
+    for (int t = 0; t < new_tokens; ++t) {
+      tokens[(size_t)b * new_tokens + t] = tk[(size_t)t * n + b];
+      if (margins) margins[(size_t)b * new_tokens + t] = mg[(size_t)t * n + b];
+    }
+  return DADGPT_OK;
+}
+
+int dadgpt_gpt2_generate_tokens(dadgpt_gpt2* m, const int32_t* prompts,
+                                const int32_t* prompt_lens, int n, int prompt_stride,
+                                int max_len, const int32_t* stop_tokens, int32_t* out,
+                                int out_stride, int32_t* out_lens) {
+  const char* fn = "dadgpt_gpt2_generate_tokens";
+  if (!m || !prompts || !prompt_lens || !out || !out_lens)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: null argument", fn);
+  const auto& c = m->c;
+  const int eff = std::min(max_len, c.ctx_len);
+  if (n < 1 || n > m->max_batch || out_stride < std::max(eff, 1))
+    return fail(DADGPT_ERR_INVALID_ARGUMENT,
+                "%s: n=%d (max_batch %d), out_stride %d (needs %d)", fn, n, m->max_batch,
+                out_stride, std::max(eff, 1));
+  TRY(check_prompts(m, fn, prompts, prompt_lens, n, prompt_stride));
+  // each row's (truncated) prompt goes to its output row; rows with room to generate form
+  // the batch, in order
+  std::vector<int> act, act_len, limit, stop;
+  std::vector<int32_t> act_prompts((size_t)n * out_stride);
+  for (int b = 0; b < n; ++b) {
+    int32_t* row = out + (size_t)b * out_stride;
+    int32_t len = 0;
+    TRY(dadgpt_gpt2_truncate_prompt(prompts + (size_t)b * prompt_stride, prompt_lens[b],
+                                    max_len, c.ctx_len, row, &len));
+    out_lens[b] = len;
+    if (len < eff) {
+      std::copy(row, row + len, act_prompts.data() + act.size() * out_stride);
+      act.push_back(b);
+      act_len.push_back(len);
+      limit.push_back(eff);
+      stop.push_back(stop_tokens ? stop_tokens[b] : -1);
+    }
+  }
+  if (act.empty()) return DADGPT_OK;
+  const int na = (int)act.size();
+  int max_new = 0;
+  for (int j = 0; j < na; ++j) max_new = std::max(max_new, eff - act_len[j]);
+  std::vector<int> tk;
+  std::vector<float> mg;
+  TRY(generate_core(m, act_prompts.data(), act_len.data(), na, out_stride, limit.data(),
+                    stop.data(), max_new, true, tk, mg, nullptr, nullptr));
+  // each row's picks up to and including its stop token, or up to its length limit
+  for (int j = 0; j < na; ++j) {
+    const int b = act[j];
+    int32_t* row = out + (size_t)b * out_stride;
+    int len = out_lens[b];
+    for (int t = 0; len < eff; ++t) {
+      const int tok = tk[(size_t)t * na + j];
+      row[len++] = tok;
+      if (tok == stop[j]) break;
+    }
+    out_lens[b] = len;
   }
   return DADGPT_OK;
 }

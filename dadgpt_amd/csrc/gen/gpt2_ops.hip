@@ -228,13 +228,23 @@ __global__ __launch_bounds__(256) void pick_partial_kernel(float* pv1, int* pi1,
 // launch would otherwise be that embedding).
 __global__ __launch_bounds__(256) void pick_final_kernel(int* tokens, float* margins, int* tok,
                                                          int* pos, int* cache_len,
-                                                         const int* prompt_len, const float* pv1,
-                                                         const int* pi1, const float* pv2,
-                                                         int parts, int n, int V, float* x,
-                                                         const bf16* wte, const bf16* wpe, int d,
-                                                         int ctx) {
+                                                         const int* prompt_len, RowStop rs,
+                                                         const float* pv1, const int* pi1,
+                                                         const float* pv2, int parts, int n,
+                                                         int V, float* x, const bf16* wte,
+                                                         const bf16* wpe, int d, int ctx) {
   __shared__ Pick s_wave[4];
   const int b = blockIdx.x, t = threadIdx.x;
+  if (rs.done[b]) {
+    // a stopped row: re-feed its last token at its last position (set by the pick that
+    // stopped it, so both are in range); nothing is emitted and no state advances
+    const int p0 = pos[b];
+    const bf16* te = wte + (size_t)tok[b] * d;
+    const bf16* pe = wpe + (size_t)p0 * d;
+    if (p0 >= 0 && p0 < ctx)
+      for (int c = t; c < d; c += 256) x[(size_t)b * d + c] = (float)te[c] + (float)pe[c];
+    return;
+  }
   Pick p = pick_none();
   // kPer candidates per thread are loaded before any is merged: one memory round trip per
   // batch instead of one per candidate (the merge order does not change the result)
@@ -274,6 +284,12 @@ __global__ __launch_bounds__(256) void pick_final_kernel(int* tokens, float* mar
     tok[b] = pick;
     pos[b] = pos_old + 1;
     cache_len[b] = pos_old + 2;
+    // src/generate.cpp:131: the stop token ends the row, and so does its length limit
+    // (pos_old + 2 tokens: the prompt and the picks so far, this one included)
+    if (pick == rs.stop[b] || pos_old + 2 >= rs.limit[b]) {
+      rs.done[b] = 1;
+      atomicAdd(rs.ndone, 1);
+    }
   }
   const int np = pos_old + 1;
   if (np >= 0 && np < ctx) {  // the input row of the step that feeds this pick
@@ -389,27 +405,27 @@ size_t pick_scratch_floats(int n, int parts) {
 }
 
 hipError_t argmax_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
-                          const int* prompt_len, const float* logits, float* scratch, int n,
-                          int V, float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
-                          hipStream_t s) {
+                          const int* prompt_len, RowStop rs, const float* logits,
+                          float* scratch, int n, int V, float* x, const bf16* wte,
+                          const bf16* wpe, int d, int ctx, hipStream_t s) {
   float* pv1 = scratch;
   int* pi1 = reinterpret_cast<int*>(scratch + (size_t)n * kPickParts);
   float* pv2 = scratch + (size_t)2 * n * kPickParts;
   pick_partial_kernel<<<dim3(n, kPickParts), 256, 0, s>>>(pv1, pi1, pv2, logits, V);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-  pick_final_kernel<<<n, 256, 0, s>>>(tokens, margins, tok, pos, cache_len, prompt_len, pv1,
+  pick_final_kernel<<<n, 256, 0, s>>>(tokens, margins, tok, pos, cache_len, prompt_len, rs, pv1,
                                       pi1, pv2, kPickParts, n, V, x, wte, wpe, d, ctx);
   return hipGetLastError();
 }
 
 hipError_t pick_advance(int* tokens, float* margins, int* tok, int* pos, int* cache_len,
-                        const int* prompt_len, const float* cand, int parts, int rows, int n,
-                        int V, float* x, const bf16* wte, const bf16* wpe, int d, int ctx,
-                        hipStream_t s) {
+                        const int* prompt_len, RowStop rs, const float* cand, int parts,
+                        int rows, int n, int V, float* x, const bf16* wte, const bf16* wpe,
+                        int d, int ctx, hipStream_t s) {
   const float* pv1 = cand;
   const int* pi1 = reinterpret_cast<const int*>(cand + (size_t)rows * parts);
   const float* pv2 = cand + (size_t)2 * rows * parts;
-  pick_final_kernel<<<n, 256, 0, s>>>(tokens, margins, tok, pos, cache_len, prompt_len, pv1,
+  pick_final_kernel<<<n, 256, 0, s>>>(tokens, margins, tok, pos, cache_len, prompt_len, rs, pv1,
                                       pi1, pv2, parts, n, V, x, wte, wpe, d, ctx);
   return hipGetLastError();
 }

@@ -46,6 +46,8 @@ GEN_SYMBOLS = (
     "dadgpt_gpt2_destroy",
     "dadgpt_gpt2_set_graphs",
     "dadgpt_gpt2_generate",
+    "dadgpt_gpt2_truncate_prompt",
+    "dadgpt_gpt2_generate_tokens",
 )
 
 
@@ -112,6 +114,8 @@ def gen_lib():
     L.dadgpt_gpt2_destroy.restype = None
     L.dadgpt_gpt2_set_graphs.argtypes = [vp, i]
     L.dadgpt_gpt2_generate.argtypes = [vp, vp, vp, i, i, i, vp, vp, vp, ctypes.POINTER(Timing)]
+    L.dadgpt_gpt2_truncate_prompt.argtypes = [vp, i, i, i, vp, vp]
+    L.dadgpt_gpt2_generate_tokens.argtypes = [vp, vp, vp, i, i, i, vp, vp, i, vp]
     for name in GEN_SYMBOLS:
         if name not in ("dadgpt_gen_last_error", "dadgpt_blas_destroy", "dadgpt_gpt2_destroy",
                         "dadgpt_gpt2_param_count"):
@@ -259,6 +263,18 @@ def init_params(cfg, seed: int, device="cuda") -> torch.Tensor:
     return params
 
 
+def truncate_prompt(prompt, max_len: int, ctx_len: int) -> list:
+    """generate_tokens' prompt truncation (src/generate.cpp:97-110), as the library applies
+    it: with eff = min(max_len, ctx_len), a prompt of at least eff tokens (and more than one)
+    keeps its first token and its last max(eff - 2, 0) tokens."""
+    p = np.ascontiguousarray(np.asarray(prompt, np.int32))
+    out = np.zeros(max(len(p), 1), np.int32)
+    n = ctypes.c_int32()
+    _check(gen_lib().dadgpt_gpt2_truncate_prompt(p.ctypes.data, len(p), max_len, ctx_len,
+                                                 out.ctypes.data, ctypes.byref(n)))
+    return [int(t) for t in out[:n.value]]
+
+
 # Attention of a model (include/dadgpt/gpt2_generate.h DADGPT_GPT2_ATTN_*), and the flag for
 # fp32 projections (DADGPT_GPT2_FP32_PROJECTIONS).
 ATTENTION = {"bf16": 0, "fp32": 1, "fp32_materialized": 2}
@@ -330,3 +346,30 @@ class GPT2:
                              "decode_attn_ms": tm.decode_attn_ms,
                              "decode_steps": tm.decode_steps}
         return out
+
+    def generate_tokens(self, prompts, max_len: int, stop_tokens=None):
+        """generate_tokens (src/generate.cpp:94-139) with greedy sampling for a batch: each
+        row's prompt is truncated as truncate_prompt does, then greedy picks are appended until
+        the row holds min(max_len, ctx_len) tokens or picks its stop token (kept as its last
+        token). stop_tokens: one per row (-1 for none), or None. Returns one list per row:
+        the truncated prompt followed by the picks."""
+        n = len(prompts)
+        lens = np.array([len(p) for p in prompts], np.int32)
+        stride = int(lens.max())
+        pad = np.zeros((n, stride), np.int32)
+        for b, p in enumerate(prompts):
+            pad[b, :len(p)] = np.asarray(p, np.int32)
+        stops = None
+        if stop_tokens is not None:
+            stops = np.ascontiguousarray(np.asarray(stop_tokens, np.int32))
+            if stops.shape != (n,):
+                raise ValueError("stop_tokens needs one entry per prompt")
+        out_stride = max(min(max_len, self.cfg.ctx_len), 1)
+        out = np.zeros((n, out_stride), np.int32)
+        out_lens = np.zeros(n, np.int32)
+        torch.cuda.synchronize()
+        _check(gen_lib().dadgpt_gpt2_generate_tokens(
+            self._m, pad.ctypes.data, lens.ctypes.data, n, stride, max_len,
+            None if stops is None else stops.ctypes.data, out.ctypes.data, out_stride,
+            out_lens.ctypes.data))
+        return [[int(t) for t in out[b, :out_lens[b]]] for b in range(n)]

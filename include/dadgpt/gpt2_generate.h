@@ -104,10 +104,35 @@ int dadgpt_gpt2_set_graphs(dadgpt_gpt2* model, int enable);
  * top-2 logit of each pick); logits [new_tokens, n, vocab] or NULL (every step's logits: for
  * tests, it synchronises per step); timing or NULL.
  * Token t of row b is the first maximum of the logits after the prompt and tokens 0..t-1
- * (std::max_element, src/generate.cpp:34-37). No stop token: exactly new_tokens per row. */
+ * (std::max_element, src/generate.cpp:34-37). No stop token: exactly new_tokens per row (for
+ * the reference's stop token and prompt truncation, dadgpt_gpt2_generate_tokens below). */
 int dadgpt_gpt2_generate(dadgpt_gpt2* model, const int32_t* prompts, const int32_t* prompt_lens,
                          int n, int prompt_stride, int new_tokens, int32_t* tokens,
                          float* margins, float* logits, dadgpt_gpt2_timing* timing);
+
+/* The prompt truncation of generate_tokens (src/generate.cpp:97-110), on the host: with
+ * eff = min(max_len, ctx_len), a prompt of len >= eff tokens (len > 1) becomes its first token
+ * followed by its last max(eff - 2, 0) tokens; any other prompt is copied unchanged. Writes
+ * out (room for len tokens) and *out_len (>= 1); DADGPT_ERR_INVALID_ARGUMENT for null
+ * buffers, len < 1 or ctx_len < 1. */
+int dadgpt_gpt2_truncate_prompt(const int32_t* prompt, int len, int max_len, int ctx_len,
+                                int32_t* out, int32_t* out_len);
+
+/* generate_tokens (src/generate.cpp:94-139) with greedy sampling, for n <= max_batch prompts at
+ * once. Per row, as the reference does for its one sequence:
+ *   - max_len is capped at ctx_len, and the prompt is truncated as
+ *     dadgpt_gpt2_truncate_prompt does;
+ *   - greedy picks are appended until the row holds max_len tokens or picks its stop token
+ *     (stop_tokens[b]; -1, or stop_tokens NULL, for none), which is kept as its last token.
+ * Rows are independent: a row that stops emits nothing more while the others continue, and
+ * its tokens are those it gets in a batch of its own. A row whose (truncated) prompt already
+ * holds max_len tokens is returned as it is.
+ * Outputs (host): out [n, out_stride] with out_stride >= max(min(max_len, ctx_len), 1), row b
+ * holding the truncated prompt followed by the picks; out_lens[b] its length. */
+int dadgpt_gpt2_generate_tokens(dadgpt_gpt2* model, const int32_t* prompts,
+                                const int32_t* prompt_lens, int n, int prompt_stride,
+                                int max_len, const int32_t* stop_tokens, int32_t* out,
+                                int out_stride, int32_t* out_lens);
 
 #ifdef __cplusplus
 }

@@ -19,9 +19,14 @@ decode of the product must equal it, which is the reference's own KV-cache invar
 attention (LayerNorm outputs, Q/K/V, the attention output, the GELU output), so the remaining
 difference is accumulation order only.
 
-Pinning: ``layernorm``, ``gelu`` and the whole ``forward`` are checked in ``tests/test_gpt2.py``
-against the reference's own CPU operators (``src/tensor_ops.cpp:6-123`` compiled into
-``oracle/_ref``) composed in the order of ``model_forward``.
+Pinning: ``layernorm``, ``gelu`` and the whole ``forward`` are checked in
+``tests/test_x_generate.py`` against the reference's own CPU operators
+(``src/tensor_ops.cpp:6-123`` compiled into ``oracle/_ref``) composed in the order of
+``model_forward``. ``truncate_prompt`` and ``generate_tokens`` restate
+``src/generate.cpp:94-139`` (which does not compile here: it needs the CUDA model and
+``<format>``); the same tests pin them by hand-worked cases of the reference's index arithmetic
+and by invariants (the first token and a suffix survive truncation; a stop token cuts the
+no-stop continuation at its first occurrence).
 """
 from __future__ import annotations
 
@@ -136,3 +141,31 @@ def greedy(params, cfg, prompt, new_tokens: int, round_bf16: bool = False):
         rows.append(row)
         seq.append(t)
     return np.array(toks, np.int32), np.stack(rows)
+
+
+def truncate_prompt(prompt, max_len: int, ctx_len: int) -> list:
+    """The prompt truncation of generate_tokens (src/generate.cpp:97-110): the length limit is
+    min(max_len, ctx_len); a prompt of at least that many tokens (and more than one) becomes
+    its first token followed by its last max(limit - 2, 0) tokens."""
+    limit = min(max_len, ctx_len)
+    toks = [int(t) for t in prompt]
+    if len(toks) >= limit and len(toks) > 1:
+        keep = max(limit - 2, 0)
+        return [toks[0]] + (toks[len(toks) - keep:] if keep else [])
+    return toks
+
+
+def generate_tokens(params, cfg, prompt, max_len: int, stop_token: int = -1,
+                    round_bf16: bool = False) -> list:
+    """generate_tokens (src/generate.cpp:94-139) with greedy sample_token (:34-37): truncate,
+    then append the first maximum of the last row's logits until the sequence holds
+    min(max_len, ctx_len) tokens or the pick is the stop token (kept). Returns the whole
+    sequence, truncated prompt included."""
+    limit = min(max_len, cfg["ctx_len"])
+    seq = truncate_prompt(prompt, max_len, cfg["ctx_len"])
+    while len(seq) < limit:
+        t = int(np.argmax(forward(params, cfg, seq, round_bf16)[-1]))
+        seq.append(t)
+        if t == stop_token or len(seq) >= limit:
+            break
+    return seq

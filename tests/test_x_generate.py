@@ -103,6 +103,128 @@ def test_oracle_greedy_is_causal_recompute():
     np.testing.assert_allclose(full[len(prompt) - 1:], rows[:4], rtol=0, atol=1e-5)
 
 
+# Hand-worked cases of src/generate.cpp:97-110 (limit = min(max_len, ctx_len); a prompt of
+# len >= limit, len > 1, keeps token 0 and its last max(limit - 2, 0) tokens): (len, max_len,
+# ctx_len, indices of the prompt that are kept).
+TRUNC_CASES = [
+    (10, 6, 1024, [0, 6, 7, 8, 9]),          # keep 4
+    (10, 11, 1024, list(range(10))),         # room left: unchanged
+    (10, 10, 1024, [0] + list(range(2, 10))),  # len == limit: one token goes
+    (10, 100, 8, [0] + list(range(4, 10))),  # the context caps the limit (keep 6)
+    (1, 0, 8, [0]),                          # a single token is never truncated
+    (3, 1, 8, [0]),                          # keep max(-1, 0) = 0
+    (3, 2, 8, [0]),                          # keep 0
+    (3, 3, 8, [0, 2]),                       # keep 1
+    (5, -4, 8, [0]),                         # a negative limit keeps the first token
+    (7, 8, 8, list(range(7))),               # len = limit - 1: unchanged
+]
+
+
+def _trunc_pins(fn):
+    """Every pin of a truncation function: the hand-worked cases, then invariants over a
+    grid (the first token and a suffix survive; a truncated prompt leaves room for one token
+    when the limit allows; truncation is idempotent). Returns the first failure or None."""
+    for n, max_len, ctx, keep in TRUNC_CASES:
+        prompt = [100 + i for i in range(n)]
+        got = list(fn(prompt, max_len, ctx))
+        if got != [prompt[i] for i in keep]:
+            return ("case", n, max_len, ctx, got)
+    for n in range(1, 13):
+        prompt = [50 + 3 * i for i in range(n)]
+        for ctx in (1, 2, 5, 9, 16):
+            for max_len in range(-2, 19):
+                got = list(fn(prompt, max_len, ctx))
+                limit = min(max_len, ctx)
+                if not got or got[0] != prompt[0]:
+                    return ("first", n, max_len, ctx, got)
+                if len(got) > 1 and got[1:] != prompt[n - (len(got) - 1):]:
+                    return ("suffix", n, max_len, ctx, got)
+                if limit >= 2 and len(got) >= limit:
+                    return ("room", n, max_len, ctx, got)
+                if (n < limit or n == 1) and got != prompt:
+                    return ("unchanged", n, max_len, ctx, got)
+                if n >= limit and n > 1 and len(got) != max(limit - 1, 1):
+                    return ("length", n, max_len, ctx, got)
+                if list(fn(got, max_len, ctx)) != got:
+                    return ("idempotent", n, max_len, ctx, got)
+    return None
+
+
+def _trunc_bug(bug):
+    """The oracle's truncation with one plausible mistake. (Dropping the reference's len > 1
+    guard changes nothing: a one-token prompt keeps its token either way.)"""
+    def fn(prompt, max_len, ctx):
+        limit = max_len if bug == "no_ctx_cap" else min(max_len, ctx)
+        toks = list(prompt)
+        cond = len(toks) > limit if bug == "strict_compare" else len(toks) >= limit
+        if cond and len(toks) > 1:
+            keep = max(limit - 2, 0)
+            if bug == "keep_off_by_one":
+                keep = max(limit - 1, 0)
+            if bug == "keep_too_few":
+                keep = max(limit - 3, 0)
+            tail = toks[len(toks) - keep:] if keep else []
+            if bug == "head_not_tail":
+                tail = toks[1:1 + keep]
+            return tail if bug == "drops_first" else [toks[0]] + tail
+        return toks
+    return fn
+
+
+def test_truncation_oracle_pins():
+    """The oracle's truncation passes every pin."""
+    assert _trunc_pins(G.truncate_prompt) is None
+
+
+@pytest.mark.parametrize("bug", ["no_ctx_cap", "strict_compare", "keep_off_by_one",
+                                 "keep_too_few", "head_not_tail", "drops_first"])
+def test_truncation_pins_catch_mistakes(bug):
+    assert _trunc_pins(_trunc_bug(bug)) is not None, bug
+
+
+def test_library_truncation_equals_oracle():
+    """dadgpt_gpt2_truncate_prompt (the host half of dadgpt_gpt2_generate_tokens) against the
+    oracle over the pin grid, and its argument checks."""
+    from dadgpt_amd import attention as A
+    from dadgpt_amd import gpt2
+
+    assert _trunc_pins(gpt2.truncate_prompt) is None
+    for n in range(1, 40, 3):
+        prompt = list(range(7, 7 + n))
+        for ctx in (1, 4, 16, 1024):
+            for max_len in (-1, 0, 1, 2, 3, n - 1, n, n + 1, 2000):
+                assert gpt2.truncate_prompt(prompt, max_len, ctx) == \
+                    G.truncate_prompt(prompt, max_len, ctx), (n, max_len, ctx)
+    with pytest.raises(A.AttentionError):
+        gpt2.truncate_prompt([], 5, 8)
+    with pytest.raises(A.AttentionError):
+        gpt2.truncate_prompt([1, 2], 5, 0)
+
+
+def test_oracle_stop_token_cuts_the_greedy_continuation():
+    """generate_tokens with a stop token equals the no-stop continuation cut after the stop
+    token's first occurrence among the picks (src/generate.cpp:131), and the sequence never
+    exceeds min(max_len, ctx_len); the picks themselves are greedy()'s."""
+    cfg = dict(d_model=64, n_layers=1, n_heads=2, d_ff=64, ctx_len=24, vocab_size=13)
+    n = G.offsets(cfg)["total"][0]
+    params = synth.normal((n,), 9) * np.float32(0.3)
+    prompt = [3, 1, 4, 1, 5]
+    full = G.generate_tokens(params, cfg, prompt, 18)
+    assert len(full) == 18 and full[:5] == prompt
+    toks, _ = G.greedy(params, cfg, prompt, 13)
+    assert full[5:] == [int(t) for t in toks]
+    for k in (0, 2, 7):
+        stop = full[5 + k]
+        first = full[5:].index(stop)
+        assert G.generate_tokens(params, cfg, prompt, 18, stop) == full[:5 + first + 1]
+    assert G.generate_tokens(params, cfg, prompt, 500) == G.generate_tokens(params, cfg, prompt,
+                                                                              24)
+    assert len(G.generate_tokens(params, cfg, prompt, 500)) == 24
+    long = list(range(13)) * 3  # 39 tokens, ctx 24: truncated to 23, one pick
+    out = G.generate_tokens(params, cfg, long, 100)
+    assert out[:23] == G.truncate_prompt(long, 100, 24) and len(out) == 24
+
+
 def gen_header_functions():
     names = set()
     for h in ("gpt2_generate.h", "gpu_matmul.h"):
@@ -341,6 +463,102 @@ def test_generate_rejects_overflowing_context(gpu):
         model.generate([[1] * 60], 5)  # 60 + 5 > ctx 64
     with pytest.raises(A.AttentionError):
         model.generate([[1, 2, cfg["vocab_size"]]], 2)
+    model.close()
+
+
+def _cut_at_stop(seq, n_prompt, stop):
+    """A generated sequence cut after the first pick equal to stop (prompt untouched)."""
+    picks = list(seq[n_prompt:])
+    return list(seq[:n_prompt]) + (picks[:picks.index(stop) + 1] if stop in picks else picks)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cfg", [TINY, TINY64, MID], ids=["skinny_graph", "hipblaslt_eager",
+                                                           "mid"])
+def test_generate_tokens_stop_token_leaves_other_rows_unchanged(gpu, cfg):
+    """generate_tokens (src/generate.cpp:94-139) for a batch: with one row's stop token set to
+    a token it picks mid-way, that row ends right after the stop token's first occurrence and
+    every other row is token for token the run without stop tokens; each row with no stop
+    token equals dadgpt_gpt2_generate of its prompt alone for max_len - len tokens."""
+    case(f"generate_tokens stop token, d_model={cfg['d_model']}")
+    model, _ = _gpu_model(cfg, seed=27, max_batch=4)
+    prompts = _prompts(cfg, [6, 19, 2, 11], 1000)
+    max_len = 34
+    free = model.generate_tokens(prompts, max_len)
+    for b, p in enumerate(prompts):
+        assert len(free[b]) == max_len and free[b][:len(p)] == p
+        alone = model.generate([p], max_len - len(p))["tokens"][0]
+        assert free[b][len(p):] == [int(t) for t in alone], b
+    for row, k in ((1, 4), (0, 0), (3, max_len - 12)):
+        stops = [-1] * 4
+        stops[row] = free[row][len(prompts[row]) + k]
+        got = model.generate_tokens(prompts, max_len, stops)
+        for b in range(4):
+            want = _cut_at_stop(free[b], len(prompts[b]), stops[b]) if b == row else free[b]
+            assert got[b] == want, (row, k, b)
+        assert len(got[row]) <= len(prompts[row]) + k + 1
+    # every row stops at its first pick: with the limit at the context (more than 32 steps)
+    # the step loop ends early; the picks are kept
+    firsts = [free[b][len(p)] for b, p in enumerate(prompts)]
+    got = model.generate_tokens(prompts, cfg["ctx_len"], firsts)
+    assert got == [p + [firsts[b]] for b, p in enumerate(prompts)]
+    model.close()
+
+
+@pytest.mark.gpu
+def test_generate_tokens_truncates_and_matches_oracle(gpu):
+    """A prompt longer than the context is truncated as the reference does (first token plus
+    the last ctx_len - 2) and continued to the context; a prompt with no room is returned as
+    it is; short prompts run to max_len. Picks against the oracle's generate_tokens, exact
+    except at near-ties (the oracle's top-1/top-2 margin within twice the logit tolerance)."""
+    import torch  # noqa: F401
+
+    cfg = TINY
+    case("generate_tokens truncation vs oracle")
+    model, params = _gpu_model(cfg, seed=28, max_batch=3)
+    ctx = cfg["ctx_len"]
+    prompts = _prompts(cfg, [ctx + 9, 4, 30], 1100)
+    for max_len, stops in ((200, None), (40, [-1, -1, -1]), (31, None)):
+        got = model.generate_tokens(prompts, max_len, stops)
+        for b, p in enumerate(prompts):
+            limit = min(max_len, ctx)
+            seq = G.truncate_prompt(p, max_len, ctx)
+            assert got[b][:len(seq)] == seq, (max_len, b)
+            assert len(got[b]) == max(limit, len(seq)), (max_len, b, len(got[b]))
+            while len(seq) < len(got[b]):
+                ref = G.forward(params, cfg, seq, round_bf16=True)[-1]
+                top = np.sort(ref)[-2:]
+                t = got[b][len(seq)]
+                if top[1] - top[0] > 2 * TOL_LOGIT:
+                    assert t == int(np.argmax(ref)), (max_len, b, len(seq))
+                seq.append(t)  # teacher forcing on the GPU's history
+    model.close()
+
+
+# Fewer prompt rows (max_batch * ctx_len) than the skinny decode kernels' 16 K-blocked rows
+SMALLCTX = dict(d_model=128, n_layers=2, n_heads=4, d_ff=512, ctx_len=8, vocab_size=512)
+
+
+@pytest.mark.gpu
+def test_generate_short_context_single_row_matches_oracle(gpu):
+    """max_batch 1 and ctx_len 8: the decode step's final LayerNorm writes, and the skinny
+    logits projection reads, 16 K-blocked rows of the LayerNorm output buffer whatever the
+    batch (it is allocated for max(rows, 16)); teacher-forced against the oracle."""
+    cfg = SMALLCTX
+    case("generate vs oracle, ctx_len 8, max_batch 1")
+    model, params = _gpu_model(cfg, seed=29, max_batch=1)
+    prompt = _prompts(cfg, [3], 1200)[0]
+    new = 5
+    out = model.generate([prompt], new, logits=True)
+    seq = list(prompt)
+    for t in range(new):
+        ref = G.forward(params, cfg, seq, round_bf16=True)[-1]
+        got = out["logits"][t, 0]
+        assert np.abs(got - ref).max() <= TOL_LOGIT, (t, np.abs(got - ref).max())
+        assert out["tokens"][0, t] == int(np.argmax(got))
+        seq.append(int(out["tokens"][0, t]))
+    # to the context: the same 5 picks
+    assert model.generate_tokens([prompt], 100)[0] == [int(t) for t in seq]
     model.close()
 
 
