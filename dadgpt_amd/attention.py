@@ -55,6 +55,8 @@ C_SYMBOLS = (
     "dadgpt_merge_heads",
     "dadgpt_attention_probs",
     "dadgpt_attention_probs_backward",
+    "dadgpt_attention_dropout",
+    "dadgpt_attention_probs_backward_dropout",
     "dadgpt_decode_probs",
     "dadgpt_use_fused_attention",
 )
@@ -150,6 +152,8 @@ def lib():
     L.dadgpt_merge_heads.argtypes = [vp, vp, i, i, i, i, vp]
     L.dadgpt_attention_probs.argtypes = [vp, i, i, f, vp]
     L.dadgpt_attention_probs_backward.argtypes = [vp, vp, vp, i, i, f, vp]
+    L.dadgpt_attention_dropout.argtypes = [vp, vp, i, i, f, u64, vp]
+    L.dadgpt_attention_probs_backward_dropout.argtypes = [vp, vp, vp, i, i, f, f, u64, vp]
     L.dadgpt_decode_probs.argtypes = [vp, vp, i, i, i, f, vp]
     L.dadgpt_use_fused_attention.argtypes = [i, i, i, i]
     _lib = L
@@ -520,6 +524,27 @@ def attention_probs_backward(dscores, dprobs, probs, BH: int, S: int, scale: flo
         _rows(t, n, BH * S * S)
     _check(lib().dadgpt_attention_probs_backward(_ptr(dscores), _ptr(dprobs), _ptr(probs), BH, S,
                                                  scale, _stream_ptr(stream)))
+
+
+def attention_dropout(dropped, probs, BH: int, S: int, dropout_p: float, seed: int,
+                      stream=None) -> None:
+    """dropped = probs * keep / (1 - dropout_p) over [BH,S,S] (src/model.cpp:406-416), with the
+    flash _dropout entry points' mask; dropped may be probs."""
+    _rows(dropped, "dropped", BH * S * S)
+    _rows(probs, "probs", BH * S * S)
+    _check(lib().dadgpt_attention_dropout(_ptr(dropped), _ptr(probs), BH, S, dropout_p, seed,
+                                          _stream_ptr(stream)))
+
+
+def attention_probs_backward_dropout(dscores, dprobs, probs, BH: int, S: int, scale: float,
+                                     dropout_p: float, seed: int, stream=None) -> None:
+    """attention_probs_backward after the dropout backward (src/model.cpp:594-607): dprobs (of
+    the dropped probabilities) times keep / (1 - dropout_p), softmax backward against probs."""
+    for t, n in ((dscores, "dscores"), (dprobs, "dprobs"), (probs, "probs")):
+        _rows(t, n, BH * S * S)
+    _check(lib().dadgpt_attention_probs_backward_dropout(
+        _ptr(dscores), _ptr(dprobs), _ptr(probs), BH, S, scale, dropout_p, seed,
+        _stream_ptr(stream)))
 
 
 def decode_probs(probs, lens, n_seq: int, n_heads: int, max_len: int, scale: float,

@@ -557,6 +557,34 @@ int dadgpt_attention_probs_backward(float* dscores, const float* dprobs, const f
                   fn);
 }
 
+int dadgpt_attention_dropout(float* dropped, const float* probs, int BH, int S, float dropout_p,
+                             uint64_t seed, void* stream) {
+  const char* fn = "dadgpt_attention_dropout";
+  if (int st = check_blocks(fn, BH, S, dropped)) return st;
+  if (int st = check_blocks(fn, BH, S, probs)) return st;
+  if (int st = check_dropout(fn, dropout_p)) return st;
+  const dadgpt::Dropout drop{dropout_p, seed};
+  return from_hip(dadgpt::launch_attention_dropout(dropped, probs, BH, S, drop, as_stream(stream)),
+                  fn);
+}
+
+int dadgpt_attention_probs_backward_dropout(float* dscores, const float* dprobs,
+                                            const float* probs, int BH, int S, float scale,
+                                            float dropout_p, uint64_t seed, void* stream) {
+  const char* fn = "dadgpt_attention_probs_backward_dropout";
+  if (int st = check_blocks(fn, BH, S, dscores)) return st;
+  if (int st = check_blocks(fn, BH, S, dprobs)) return st;
+  if (int st = check_blocks(fn, BH, S, probs)) return st;
+  if (!std::isfinite(scale))
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "%s: scale must be finite", fn);
+  if (int st = check_dropout(fn, dropout_p)) return st;
+  const dadgpt::Dropout drop{dropout_p, seed};
+  return from_hip(dadgpt::launch_attention_probs_backward_dropout(dscores, dprobs, probs, BH, S,
+                                                                  scale, drop,
+                                                                  as_stream(stream)),
+                  fn);
+}
+
 int dadgpt_decode_probs(float* probs, const int32_t* lens, int n_seq, int n_heads, int max_len,
                         float scale, void* stream) {
   const char* fn = "dadgpt_decode_probs";

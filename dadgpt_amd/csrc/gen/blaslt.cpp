@@ -12,7 +12,7 @@
 // soname too, so it must be opened before PyTorch loads its rocRoller: the Python package
 // does that at import (dadgpt_blas_open); opened later, dlopen fails and every handle creation
 // reports why. dadgpt_blas_create also refuses a copy whose reported version differs from the
-// headers'.
+// headers', and a HIP runtime that no GPU test has run this hipBLASLt on (stack_supported).
 //
 // Row-major to column-major: a row-major X[R,C] is the column-major X^T (C rows, R cols,
 // leading dimension C), so the row-major product out = op(a) op(b) is the column-major
@@ -112,6 +112,20 @@ const LtApi* api() {
 
 constexpr int kCompiledVersion =
     HIPBLASLT_VERSION_MAJOR * 100000 + HIPBLASLT_VERSION_MINOR * 100 + HIPBLASLT_VERSION_PATCH;
+// HIP runtimes (major, minor) that the GPU tests run this hipBLASLt on: PyTorch's ROCm 7.0
+// runtime (the Python test suite, which loads PyTorch's libamdhip64 first) and the 7.2 runtime
+// of the ROCm installation whose hipBLASLt this is (tests/cxx/blas_stack_test.cpp, a C++ caller
+// without PyTorch). The hipBLASLt must be the version the headers declare.
+constexpr int kTestedRuntimes[][2] = {{7, 0}, {7, 2}};
+
+bool stack_supported(int hip_runtime, int hipblaslt) {
+  if (hipblaslt != kCompiledVersion) return false;
+  const int major = hip_runtime / 10000000, minor = hip_runtime / 100000 % 100;
+  for (const auto& t : kTestedRuntimes)
+    if (t[0] == major && t[1] == minor) return true;
+  return false;
+}
+
 constexpr size_t kWorkspaceBytes = 32u << 20;
 constexpr int kCandidates = 16;
 
@@ -302,6 +316,13 @@ hipblasComputeType_t f32_compute() {
 
 bool valid_op(int op) { return op == 'N' || op == 'A' || op == 'B'; }
 
+// hipBLASLt ends the process when a handle is created with no device visible, so every
+// handle creation checks for one first.
+bool have_device() {
+  int n = 0;
+  return hipGetDeviceCount(&n) == hipSuccess && n > 0;
+}
+
 }  // namespace
 
 int gemm(dadgpt_blas* h, float* out, const bf16* a, const bf16* b, int M, int K, int N,
@@ -332,6 +353,7 @@ int dadgpt_blas_create(dadgpt_blas** out) {
   if (!out) return fail(DADGPT_ERR_INVALID_ARGUMENT, "dadgpt_blas_create: null argument");
   const LtApi* L = api();
   if (!L) return fail(DADGPT_ERR_UNSUPPORTED, "dadgpt_blas_create: %s", g_api_error.c_str());
+  if (!have_device()) return fail(DADGPT_ERR_HIP, "dadgpt_blas_create: no HIP device visible");
   auto* h = new dadgpt_blas();
   hipblasStatus_t s = L->create(&h->lt);
   if (s != HIPBLAS_STATUS_SUCCESS) {
@@ -346,6 +368,16 @@ int dadgpt_blas_create(dadgpt_blas** out) {
                 "dadgpt_blas_create: " DADGPT_HIPBLASLT_SO " reports version %d, these sources "
                 "were compiled against %d",
                 version, kCompiledVersion);
+  }
+  int runtime = 0;
+  if (hipRuntimeGetVersion(&runtime) != hipSuccess || !stack_supported(runtime, version)) {
+    L->destroy(h->lt);
+    delete h;
+    return fail(DADGPT_ERR_UNSUPPORTED,
+                "dadgpt_blas_create: HIP runtime %d.%d.%d with hipBLASLt %d is not a combination "
+                "the GPU tests cover (HIP 7.0 or 7.2 with hipBLASLt %d)",
+                runtime / 10000000, runtime / 100000 % 100, runtime % 100000, version,
+                kCompiledVersion);
   }
   if (hipMalloc(&h->workspace, kWorkspaceBytes) != hipSuccess) {
     L->destroy(h->lt);
@@ -364,6 +396,26 @@ void dadgpt_blas_destroy(dadgpt_blas* h) {
   (void)hipFree(h->workspace);
   L->destroy(h->lt);
   delete h;
+}
+
+int dadgpt_blas_stack_versions(int* hip_runtime, int* hipblaslt) {
+  if (!hip_runtime || !hipblaslt)
+    return fail(DADGPT_ERR_INVALID_ARGUMENT, "dadgpt_blas_stack_versions: null argument");
+  *hip_runtime = -1;
+  *hipblaslt = -1;
+  if (hipRuntimeGetVersion(hip_runtime) != hipSuccess) *hip_runtime = -1;
+  const LtApi* L = api();
+  if (!L) return fail(DADGPT_ERR_UNSUPPORTED, "dadgpt_blas_stack_versions: %s", g_api_error.c_str());
+  hipblasLtHandle_t lt = nullptr;
+  if (have_device() && L->create(&lt) == HIPBLAS_STATUS_SUCCESS) {
+    if (L->get_version(lt, hipblaslt) != HIPBLAS_STATUS_SUCCESS) *hipblaslt = -1;
+    L->destroy(lt);
+  }
+  return DADGPT_OK;
+}
+
+int dadgpt_blas_stack_supported(int hip_runtime, int hipblaslt) {
+  return stack_supported(hip_runtime, hipblaslt) ? 1 : 0;
 }
 
 int dadgpt_blas_library_version(dadgpt_blas* h) {

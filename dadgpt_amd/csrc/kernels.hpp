@@ -114,6 +114,14 @@ hipError_t launch_attention_probs_backward(float* ds, const float* dp, const flo
                                            int S, float scale, hipStream_t stream);
 hipError_t launch_decode_probs(float* p, const int* lens, int n_seq, int H, int max_len,
                                float scale, hipStream_t stream);
+// Attention-probability dropout of the materialized path, with the flash kernels' mask
+// (dropout.hpp): out [BH, S, S] = p * keep / (1 - drop.p) (out may be p); and the backward row
+// pass ds = causal_zero(softmax_backward(dpd * keep / (1 - drop.p), p)) * scale (ds may be dpd).
+hipError_t launch_attention_dropout(float* out, const float* p, int BH, int S,
+                                   const Dropout& drop, hipStream_t stream);
+hipError_t launch_attention_probs_backward_dropout(float* ds, const float* dpd, const float* p,
+                                                   int BH, int S, float scale,
+                                                   const Dropout& drop, hipStream_t stream);
 // The reference's head split [B*S, H*dh] -> [B*H, S, dh] and merge (its inverse), fp32
 // (materialized.hip). out and in do not overlap; B*S < 2^31 rows.
 hipError_t launch_split_heads(float* out, const float* in, int B, int S, int H, int dh,

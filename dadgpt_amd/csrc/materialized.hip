@@ -18,6 +18,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "dropout.hpp"
 #include "lanes.hpp"
 #include "kernels.hpp"
 
@@ -132,6 +133,100 @@ __global__ void scale_kernel(float* __restrict__ x, long long n, float scale) {
     x[i] *= scale;
 }
 
+// Attention-probability dropout on the materialized path, with the flash kernels' mask
+// (dropout.hpp): element (r, c) of the [BH*S, S] probabilities is row r = bh*S + query and key
+// c. Each lane owns 8 consecutive columns per step, whose keep bits are one Philox block;
+// rows whose columns are not 16-byte pieces take the per-element path (V = 1).
+template <int V, typename F>
+__device__ __forceinline__ void row_groups(const float* row, int cols, int lane,
+                                           const DropParams& dr, long long r, F f) {
+  for (int c0 = 8 * lane; c0 < cols; c0 += 512) {
+    const uint32_t bits = keep8(dr, (uint64_t)r, (uint32_t)c0 >> 3);
+    if constexpr (V == 4) {  // cols % 8 == 0: the group is whole
+      const f32x4 a = *reinterpret_cast<const f32x4*>(row + c0);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(row + c0 + 4);
+      f(c0, a, b, bits);
+    } else {
+      f32x4 a, b;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a[e] = c0 + e < cols ? row[c0 + e] : 0.f;
+        b[e] = c0 + 4 + e < cols ? row[c0 + 4 + e] : 0.f;
+      }
+      f(c0, a, b, bits);
+    }
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void store_group(float* row, int cols, int c0, const f32x4& a,
+                                            const f32x4& b) {
+  if constexpr (V == 4) {
+    *reinterpret_cast<f32x4*>(row + c0) = a;
+    *reinterpret_cast<f32x4*>(row + c0 + 4) = b;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (c0 + e < cols) row[c0 + e] = a[e];
+      if (c0 + 4 + e < cols) row[c0 + 4 + e] = b[e];
+    }
+  }
+}
+
+// out = p * keep / (1 - p_drop) (the reference's gpu_dropout_forward, cuda/gpu_ops.cu:712-733,
+// with this mask). out may be p.
+template <int V>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void dropout_rows_kernel(
+    float* out, const float* p, long long rows, int cols, DropParams dr) {
+  const int lane = threadIdx.x & 63;
+  const long long r = (long long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  float* dst = out + r * cols;
+  row_groups<V>(p + r * cols, cols, lane, dr, r, [&](int c0, f32x4 a, f32x4 b, uint32_t bits) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[e] *= keep_factor(bits, e, dr.scale);
+      b[e] *= keep_factor(bits, 4 + e, dr.scale);
+    }
+    store_group<V>(dst, cols, c0, a, b);
+  });
+}
+
+// The attention backward's row pass with dropout (src/model.cpp:594-607): dP = dPd * keep /
+// (1 - p_drop) (gpu_dropout_backward, cuda/gpu_ops.cu:736-749), then the softmax backward
+// against the undropped P, zero past the causal diagonal, times scale. ds may be dpd.
+template <int V>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void attn_probs_backward_dropout_kernel(
+    float* ds, const float* dpd, const float* __restrict__ p, long long rows, int S,
+    float scale, DropParams dr) {
+  const int lane = threadIdx.x & 63;
+  const long long r = (long long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* g = dpd + r * S;
+  const float* pr = p + r * S;
+  float* d = ds + r * S;
+  float dot = 0.f;
+  row_groups<V>(g, S, lane, dr, r, [&](int c0, f32x4 a, f32x4 b, uint32_t bits) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (c0 + e < S) dot += a[e] * keep_factor(bits, e, dr.scale) * pr[c0 + e];
+      if (c0 + 4 + e < S) dot += b[e] * keep_factor(bits, 4 + e, dr.scale) * pr[c0 + 4 + e];
+    }
+  });
+  dot = wave_sum(dot);
+  const int limit = (int)(r % S) + 1;
+  row_groups<V>(g, S, lane, dr, r, [&](int c0, f32x4 a, f32x4 b, uint32_t bits) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ca = c0 + e, cb = c0 + 4 + e;
+      a[e] = ca < limit ? pr[ca] * (a[e] * keep_factor(bits, e, dr.scale) - dot) * scale : 0.f;
+      b[e] = cb < limit ? pr[cb] * (b[e] * keep_factor(bits, 4 + e, dr.scale) - dot) * scale
+                        : 0.f;
+    }
+    store_group<V>(d, S, c0, a, b);
+  });
+}
+
 // The head split and merge (cuda/gpu_ops.cu:426-474), a pure permutation between the
 // token-major [B*S, H*dh] layout and [B*H, S, dh]. One workgroup per token row (b, s): its
 // threads walk the row in W-float pieces (16 bytes when dh and both buffers allow), so the
@@ -232,6 +327,33 @@ hipError_t launch_decode_probs(float* p, const int* lens, int n_seq, int H, int 
                                float scale, hipStream_t stream) {
   return launch_softmax<kLength>(p, p, (long long)n_seq * H, max_len, 1, scale, lens, H,
                                  stream);
+}
+
+hipError_t launch_attention_dropout(float* out, const float* p, int BH, int S,
+                                   const Dropout& drop, hipStream_t stream) {
+  const long long rows = (long long)BH * S;
+  const DropParams dr = drop_params(&drop);
+  if (S % 8 == 0 && vec4(out, p, S))
+    dropout_rows_kernel<4><<<row_blocks(rows), 64 * kRowsPerBlock, 0, stream>>>(out, p, rows, S,
+                                                                                dr);
+  else
+    dropout_rows_kernel<1><<<row_blocks(rows), 64 * kRowsPerBlock, 0, stream>>>(out, p, rows, S,
+                                                                                dr);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_probs_backward_dropout(float* ds, const float* dpd, const float* p,
+                                                   int BH, int S, float scale,
+                                                   const Dropout& drop, hipStream_t stream) {
+  const long long rows = (long long)BH * S;
+  const DropParams dr = drop_params(&drop);
+  if (S % 8 == 0 && vec4(ds, dpd, S) && vec4(p, p, S))
+    attn_probs_backward_dropout_kernel<4><<<row_blocks(rows), 64 * kRowsPerBlock, 0, stream>>>(
+        ds, dpd, p, rows, S, scale, dr);
+  else
+    attn_probs_backward_dropout_kernel<1><<<row_blocks(rows), 64 * kRowsPerBlock, 0, stream>>>(
+        ds, dpd, p, rows, S, scale, dr);
+  return hipGetLastError();
 }
 
 hipError_t launch_split_heads(float* out, const float* in, int B, int S, int H, int dh,

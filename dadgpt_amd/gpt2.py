@@ -32,6 +32,8 @@ GEN_SYMBOLS = (
     "dadgpt_blas_create",
     "dadgpt_blas_destroy",
     "dadgpt_blas_library_version",
+    "dadgpt_blas_stack_versions",
+    "dadgpt_blas_stack_supported",
     "dadgpt_set_matmul_precision",
     "dadgpt_get_matmul_precision",
     "dadgpt_matmul_bf16",
@@ -40,6 +42,8 @@ GEN_SYMBOLS = (
     "dadgpt_matmul_f32_strided_batched",
     "dadgpt_attention_materialized_forward",
     "dadgpt_attention_materialized_backward",
+    "dadgpt_attention_materialized_forward_dropout",
+    "dadgpt_attention_materialized_backward_dropout",
     "dadgpt_gpt2_param_count",
     "dadgpt_gpt2_init_params",
     "dadgpt_gpt2_create",
@@ -99,6 +103,8 @@ def gen_lib():
     L.dadgpt_matmul_transposed_b_bf16.argtypes = [vp, vp, vp, vp, i, i, i, vp]
     ll = ctypes.c_longlong
     L.dadgpt_blas_library_version.argtypes = [vp]
+    L.dadgpt_blas_stack_versions.argtypes = [ctypes.POINTER(i), ctypes.POINTER(i)]
+    L.dadgpt_blas_stack_supported.argtypes = [i, i]
     L.dadgpt_set_matmul_precision.argtypes = [i]
     L.dadgpt_get_matmul_precision.argtypes = []
     L.dadgpt_matmul_f32.argtypes = [vp, vp, vp, vp, i, i, i, i, f, vp]
@@ -106,6 +112,11 @@ def gen_lib():
                                                     vp]
     L.dadgpt_attention_materialized_forward.argtypes = [vp] * 6 + [i, i, i, f, vp]
     L.dadgpt_attention_materialized_backward.argtypes = [vp] * 10 + [i, i, i, f, vp]
+    u64 = ctypes.c_uint64
+    L.dadgpt_attention_materialized_forward_dropout.argtypes = [vp] * 7 + [i, i, i, f, f, u64,
+                                                                           vp]
+    L.dadgpt_attention_materialized_backward_dropout.argtypes = [vp] * 10 + [i, i, i, f, f, u64,
+                                                                             vp]
     L.dadgpt_gpt2_param_count.argtypes = [cfgp]
     L.dadgpt_gpt2_param_count.restype = sz
     L.dadgpt_gpt2_init_params.argtypes = [vp, cfgp, ctypes.c_uint64, vp]
@@ -138,6 +149,24 @@ def _stream():
 
 
 # ------------------------------------------------------------------------------ GEMMs
+
+def _version_str(v: int, major: int, minor: int) -> str:
+    return "unknown" if v < 0 else f"{v // major}.{v // minor % (major // minor)}.{v % minor}"
+
+
+def blas_stack_versions() -> dict:
+    """The process's HIP runtime and hipBLASLt versions (as numbers and dotted), and whether
+    dadgpt_blas_create accepts the pair (a combination the GPU tests cover)."""
+    rt, lt = ctypes.c_int(), ctypes.c_int()
+    _check(gen_lib().dadgpt_blas_stack_versions(ctypes.byref(rt), ctypes.byref(lt)))
+    return {"hip_runtime": rt.value, "hipblaslt": lt.value,
+            "hip_runtime_str": _version_str(rt.value, 10_000_000, 100_000),
+            "hipblaslt_str": _version_str(lt.value, 100_000, 100),
+            "supported": bool(gen_lib().dadgpt_blas_stack_supported(rt.value, lt.value))}
+
+
+def blas_stack_supported(hip_runtime: int, hipblaslt: int) -> bool:
+    return bool(gen_lib().dadgpt_blas_stack_supported(hip_runtime, hipblaslt))
 
 # The reference's MatmulPrecision (cuda/gpu_ops.cuh:43), process-wide.
 PRECISIONS = {"fp32": 0, "tf32": 1, "bf16": 2}
@@ -241,6 +270,30 @@ class Blas:
             self._f32(t, nm)
         _check(gen_lib().dadgpt_attention_materialized_backward(
             self._h, *[t.data_ptr() for t in ts], BH, S, d_head, scale, _stream()))
+
+    def attention_materialized_forward_dropout(self, out, probs, dropped, q, k, v, BH: int,
+                                               S: int, d_head: int, scale: float,
+                                               dropout_p: float, seed: int) -> None:
+        """The forward with attention dropout (src/model.cpp:395-420): probs [BH,S,S] receives
+        the probabilities, dropped [BH,S,S] probs * keep / (1 - dropout_p), out = dropped v."""
+        ts = (out, probs, dropped, q, k, v)
+        for t, nm in zip(ts, ("out", "probs", "dropped", "q", "k", "v")):
+            self._f32(t, nm)
+        _check(gen_lib().dadgpt_attention_materialized_forward_dropout(
+            self._h, *[t.data_ptr() for t in ts], BH, S, d_head, scale, dropout_p, seed,
+            _stream()))
+
+    def attention_materialized_backward_dropout(self, dq, dk, dv, dscores, dout, probs, q, k, v,
+                                                BH: int, S: int, d_head: int, scale: float,
+                                                dropout_p: float, seed: int) -> None:
+        """Its backward (src/model.cpp:575-616 with :594-599): same seed and dropout_p as the
+        forward; dscores [BH,S,S] scratch."""
+        ts = (dq, dk, dv, dscores, dout, probs, q, k, v)
+        for t, nm in zip(ts, ("dq", "dk", "dv", "dscores", "dout", "probs", "q", "k", "v")):
+            self._f32(t, nm)
+        _check(gen_lib().dadgpt_attention_materialized_backward_dropout(
+            self._h, *[t.data_ptr() for t in ts], BH, S, d_head, scale, dropout_p, seed,
+            _stream()))
 
 
 # ------------------------------------------------------------------------ the model

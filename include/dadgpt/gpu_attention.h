@@ -285,6 +285,19 @@ int dadgpt_attention_probs(float* probs, int BH, int S, float scale, void* strea
  * src/model.cpp:601-607, in one pass). dscores may be dprobs. */
 int dadgpt_attention_probs_backward(float* dscores, const float* dprobs, const float* probs,
                                     int BH, int S, float scale, void* stream);
+/* Attention-probability dropout of the materialized path (src/model.cpp:406-416; the
+ * reference's gpu_dropout_forward, cuda/gpu_ops.cu:712-733): dropped [BH, S, S] =
+ * probs * keep / (1 - dropout_p), with the keep mask of the flash _dropout entry points
+ * (probability (bh, i, j) is row bh*S + i, key j of that mask; no mask is stored).
+ * dropped may be probs. dropout_p in [0, 1). */
+int dadgpt_attention_dropout(float* dropped, const float* probs, int BH, int S, float dropout_p,
+                             uint64_t seed, void* stream);
+/* dadgpt_attention_probs_backward with dropout (src/model.cpp:594-607): d(dropped probs) is
+ * first multiplied by keep / (1 - dropout_p) (gpu_dropout_backward, cuda/gpu_ops.cu:736-749),
+ * then taken through the softmax backward against the undropped probs. */
+int dadgpt_attention_probs_backward_dropout(float* dscores, const float* dprobs,
+                                            const float* probs, int BH, int S, float scale,
+                                            float dropout_p, uint64_t seed, void* stream);
 /* Decode scores [n_seq * n_heads, max_len] -> probabilities in place over each sequence's
  * first lens[seq] keys (DEVICE int32 lens; x scale, keys at or past the length -1e9, row
  * softmax; an empty cache gives a zero row): the gpu_scale + gpu_softmax step of the

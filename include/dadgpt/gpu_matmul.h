@@ -37,12 +37,22 @@ const char* dadgpt_gen_last_error(void);
 int dadgpt_blas_open(void);
 
 /* Creates a handle on the current device: a hipBLASLt handle, a 32 MiB workspace and a cache
- * of per-shape algorithm choices (replaces cublasCreate in model_alloc, src/model.cpp:236). */
+ * of per-shape algorithm choices (replaces cublasCreate in model_alloc, src/model.cpp:236).
+ * Refused (DADGPT_ERR_UNSUPPORTED, with both versions in the message) unless the process's
+ * HIP runtime and the opened hipBLASLt are a pair dadgpt_blas_stack_supported accepts. */
 int dadgpt_blas_create(dadgpt_blas** out);
 void dadgpt_blas_destroy(dadgpt_blas* h);
 
 /* hipBLASLt's own version (major*100000 + minor*100 + patch) behind a handle, -1 on error. */
 int dadgpt_blas_library_version(dadgpt_blas* h);
+
+/* The process's HIP runtime version (hipRuntimeGetVersion: major*10^7 + minor*10^5 + patch)
+ * and the opened hipBLASLt's (-1 for either one that cannot be read, e.g. no device). */
+int dadgpt_blas_stack_versions(int* hip_runtime, int* hipblaslt);
+/* 1 if (hip_runtime, hipblaslt) is a pair the GPU tests run on: HIP 7.0 (PyTorch's runtime)
+ * or 7.2 (the ROCm installation's) with the hipBLASLt version these sources were compiled
+ * against; 0 otherwise. */
+int dadgpt_blas_stack_supported(int hip_runtime, int hipblaslt);
 
 /* Process-wide multiply precision of the fp32 GEMMs below, as gpu_set_matmul_precision
  * (cuda/gpu_ops.cuh:43-44, cuda/gpu_ops.cu:61-67): storage and accumulation stay fp32.
@@ -100,6 +110,25 @@ int dadgpt_attention_materialized_backward(dadgpt_blas* h, float* dq, float* dk,
                                            const float* probs, const float* q, const float* k,
                                            const float* v, int BH, int S, int d_head,
                                            float scale, void* stream);
+/* The same with attention-probability dropout (src/model.cpp:406-416 forward, :594-599
+ * backward), the path use_fused_attention picks for every dropout call: the forward writes
+ * the probabilities to probs (kept for the backward) and probs * keep / (1 - dropout_p) to
+ * dropped [BH, S, S] (a separate buffer, as the reference's attn_dropped), and out =
+ * dropped v. The backward regenerates the dropped probabilities from probs and the mask into
+ * dscores (no mask is stored: same seed and dropout_p as the forward). The mask is the one of
+ * the flash _dropout entry points of <dadgpt/gpu_attention.h>, so both paths drop the same
+ * probabilities. */
+int dadgpt_attention_materialized_forward_dropout(dadgpt_blas* h, float* out, float* probs,
+                                                  float* dropped, const float* q,
+                                                  const float* k, const float* v, int BH, int S,
+                                                  int d_head, float scale, float dropout_p,
+                                                  uint64_t seed, void* stream);
+int dadgpt_attention_materialized_backward_dropout(dadgpt_blas* h, float* dq, float* dk,
+                                                   float* dv, float* dscores, const float* dout,
+                                                   const float* probs, const float* q,
+                                                   const float* k, const float* v, int BH, int S,
+                                                   int d_head, float scale, float dropout_p,
+                                                   uint64_t seed, void* stream);
 
 #ifdef __cplusplus
 }

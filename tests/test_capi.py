@@ -293,6 +293,12 @@ def test_materialized_ops_validation():
     assert L.dadgpt_attention_probs_backward(FAKE, FAKE, None, 2, 64, 0.125, None) == 1
     assert L.dadgpt_decode_probs(FAKE, None, 2, 12, 1024, 0.125, None) == 1
     assert L.dadgpt_decode_probs(FAKE, FAKE, 2, 0, 1024, 0.125, None) == 1
+    assert L.dadgpt_attention_dropout(FAKE, FAKE, 2, 64, 1.0, 7, None) == 1
+    assert L.dadgpt_attention_dropout(None, FAKE, 2, 64, 0.1, 7, None) == 1
+    assert L.dadgpt_attention_probs_backward_dropout(FAKE, FAKE, FAKE, 2, 64, 0.125, -0.5, 7,
+                                                     None) == 1
+    assert L.dadgpt_attention_probs_backward_dropout(FAKE, FAKE, FAKE, 2, 64, float("inf"), 0.1,
+                                                     7, None) == 1
 
 
 def test_cxx_reference_names_link_and_throw(tmp_path):

@@ -14,6 +14,7 @@ import ctypes
 import math
 import os
 import re
+import subprocess
 
 import numpy as np
 import pytest
@@ -269,6 +270,78 @@ def test_materialized_matches_fused_fp32(blas):
         assert max_abs(a, host(b)) <= TOL_F32
 
 
+def _materialized_dropout(blas, qn, kn, vn, gn, scale, p, seed):
+    BH, S, D = qn.shape
+    q, k, v, g = dev(qn), dev(kn), dev(vn), dev(gn)
+    out = torch.empty_like(q)
+    probs = torch.empty(BH, S, S, device="cuda")
+    dropped = torch.empty(BH, S, S, device="cuda")
+    blas.attention_materialized_forward_dropout(out, probs, dropped, q, k, v, BH, S, D, scale, p,
+                                                seed)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    ds = torch.empty(BH, S, S, device="cuda")
+    blas.attention_materialized_backward_dropout(dq, dk, dv, ds, g, probs, q, k, v, BH, S, D,
+                                                 scale, p, seed)
+    torch.cuda.synchronize()
+    return host(out), host(probs), host(dropped), host(dq), host(dk), host(dv)
+
+
+@pytest.mark.parametrize("BH,S,D,p", [(2, 70, 64, 0.1), (3, 129, 32, 0.5), (2, 256, 64, 0.25),
+                                      (1, 1, 64, 0.3), (2, 64, 48, 0.9)])
+def test_materialized_dropout_against_oracle(blas, BH, S, D, p):
+    """The materialized path with attention dropout (src/model.cpp:406-416, 594-599), the one
+    use_fused_attention picks for dropout: O and dQ/dK/dV against the oracle's dropout path
+    (the same keep mask, the materialized op order) at the fp32 tolerance; the dropped
+    probabilities are exactly probs * keep * 1/(1-p) with the oracle's mask."""
+    seed = 0x5EED_0000_0000_0000 + 97 * S + D
+    case(f"materialized dropout vs oracle BH={BH} S={S} D={D} p={p}")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=650 + S + D, with_dout=True)
+    scale = float(np.float32(1.0 / math.sqrt(D)))
+    out, probs, dropped, dq, dk, dv = _materialized_dropout(blas, qn, kn, vn, gn, scale, p, seed)
+    keep = oracle.dropout_mask(BH, S, seed, p).astype(bool)
+    # the keep factor in fp32, as the reference's 1.0f / (1.0f - rate) (cuda/gpu_ops.cu:719)
+    factor = np.float32(1.0) / (np.float32(1.0) - np.float32(p))
+    want = np.where(keep, probs * factor, np.float32(0.0))
+    assert np.array_equal(dropped, want.astype(np.float32))
+    o_ref, _ = oracle.attn_fwd_dropout(qn, kn, vn, scale, p, seed)
+    dq_r, dk_r, dv_r, _ = oracle.attn_bwd_dropout(gn, qn, kn, vn, scale, p, seed)
+    tol = TOL_F32 / (1.0 - p)  # the values carry the factor 1/(1-p)
+    assert max_abs(out, o_ref) <= tol
+    for a, b, nm in ((dq, dq_r, "dq"), (dk, dk_r, "dk"), (dv, dv_r, "dv")):
+        assert max_abs(a, b) <= tol, nm
+
+
+def test_materialized_dropout_matches_flash_dropout_and_p0(blas):
+    """With the same seed and rate the materialized and the fp32 flash dropout paths drop the
+    same probabilities (one mask definition): outputs and gradients agree at 1e-5. At p = 0 the
+    dropout path's forward (O and the probabilities) equals the plain materialized path bit for
+    bit; its gradients agree at 1e-5 (the dropout row pass sums each row's dP.P in 8-column
+    groups, the plain one in 64-column strides: another fp32 summation order)."""
+    BH, S, D, p, seed = 4, 300, 64, 0.2, 1234567
+    case(f"materialized dropout vs flash fp32 dropout BH={BH} S={S}")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=710, with_dout=True)
+    scale = 0.125
+    out, _, _, dq, dk, dv = _materialized_dropout(blas, qn, kn, vn, gn, scale, p, seed)
+    q, k, v, g = dev(qn), dev(kn), dev(vn), dev(gn)
+    fo = torch.empty_like(q)
+    lse = torch.empty(BH, S, device="cuda")
+    A.flash_attention_forward_dropout(fo, lse, q, k, v, BH, S, D, scale, p, seed)
+    fdq, fdk, fdv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    delta = torch.empty_like(lse)
+    A.flash_attention_backward_dropout(fdq, fdk, fdv, delta, g, fo, lse, q, k, v, BH, S, D, scale,
+                                       p, seed)
+    torch.cuda.synchronize()
+    assert max_abs(out, host(fo)) <= TOL_F32 / (1 - p)
+    for a, b in ((dq, fdq), (dk, fdk), (dv, fdv)):
+        assert max_abs(a, host(b)) <= TOL_F32 / (1 - p)
+    plain = _materialized(blas, qn, kn, vn, gn, scale)
+    zero = _materialized_dropout(blas, qn, kn, vn, gn, scale, 0.0, seed)
+    assert np.array_equal(plain[0], zero[0]) and np.array_equal(plain[1], zero[1])
+    assert np.array_equal(zero[1], zero[2])  # nothing dropped, factor exactly 1
+    for a, b in zip(plain[2:], zero[3:]):
+        assert max_abs(a, b) <= TOL_F32
+
+
 def _softmax64(x):
     x = x.astype(np.float64)
     e = np.exp(x - x.max(-1, keepdims=True))
@@ -409,3 +482,28 @@ def test_split_merge_heads_reference_symbols(gpu, B, S, H, dh):
     torch.cuda.synchronize()
     assert np.array_equal(host(h2).reshape(B * H, S, dh), want)
     assert np.array_equal(host(b2), x)
+
+
+def test_blas_stack_in_this_process(gpu):
+    """The Python test process runs PyTorch's HIP 7.0 runtime under the compiled hipBLASLt: the
+    pair every other GPU test here exercises, and one dadgpt_blas_create accepts."""
+    v = gpt2.blas_stack_versions()
+    case(f"blas stack {v}")
+    assert v["supported"] and v["hip_runtime"] // 100000 == 700, v
+
+
+def test_blas_stack_cxx_caller_on_rocm_runtime(gpu, tmp_path):
+    """A C++ caller without PyTorch (tests/cxx/blas_stack_test.cpp): the ROCm installation's
+    7.2 HIP runtime with the same hipBLASLt; the pair is accepted, a handle is created and a
+    bf16 GEMM matches the CPU product."""
+    case("blas stack C++ caller on the ROCm runtime")
+    libdir = os.path.join(ROOT, "dadgpt_amd", "lib")
+    exe = str(tmp_path / "blas_stack_test")
+    subprocess.run(["g++", "-std=c++17", "-O1", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    f"-I{ROOT}/include", os.path.join(ROOT, "tests", "cxx", "blas_stack_test.cpp"),
+                    f"-L{libdir}", "-ldadgpt_gen", "-ldadgpt_attn", "-L/opt/rocm/lib",
+                    "-lamdhip64", f"-Wl,-rpath,{libdir}", "-Wl,-rpath,/opt/rocm/lib", "-o", exe],
+                   check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0 and r.stdout.strip().endswith("OK"), r.stdout + r.stderr

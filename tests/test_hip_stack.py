@@ -90,3 +90,54 @@ def test_gen_library_does_not_link_hipblaslt():
     out = subprocess.run(["readelf", "-d", LIBS[1]], check=True, capture_output=True,
                          text=True).stdout
     assert "hipblaslt" not in out
+
+
+def _compiled_hipblaslt():
+    """The hipBLASLt version the headers declare (major*100000 + minor*100 + patch)."""
+    text = open("/opt/rocm/include/hipblaslt/hipblaslt-version.h").read()
+    v = {k: int(re.search(rf"HIPBLASLT_VERSION_{k}\s+(\d+)", text).group(1))
+         for k in ("MAJOR", "MINOR", "PATCH")}
+    return v["MAJOR"] * 100000 + v["MINOR"] * 100 + v["PATCH"]
+
+
+def test_stack_pairs_accepted_and_refused():
+    """dadgpt_blas_create accepts only (HIP runtime, hipBLASLt) pairs the GPU tests run on:
+    HIP 7.0 (PyTorch's) or 7.2 (the ROCm installation's) with the compiled hipBLASLt."""
+    from dadgpt_amd import gpt2
+
+    lt = _compiled_hipblaslt()
+    assert gpt2.blas_stack_supported(70051831, lt)
+    assert gpt2.blas_stack_supported(70226015, lt)
+    assert not gpt2.blas_stack_supported(70226015, lt + 1)
+    assert not gpt2.blas_stack_supported(70051831, lt - 100)
+    for rt in (60400000, 70100000, 70300000, 80000000, -1):
+        assert not gpt2.blas_stack_supported(rt, lt), rt
+
+
+CREATE_PROBE = r"""
+import ctypes, sys
+sys.path.insert(0, {root!r})
+import dadgpt_amd
+from dadgpt_amd import gpt2
+import torch
+v = gpt2.blas_stack_versions()
+print("RUNTIME", v["hip_runtime"], v["hip_runtime_str"])
+if torch.cuda.device_count() == 0:
+    h = ctypes.c_void_p()
+    st = gpt2.gen_lib().dadgpt_blas_create(ctypes.byref(h))
+    print("CREATE", st, gpt2.last_error())
+"""
+
+
+def test_process_runtime_is_pytorchs_and_no_device_is_an_error():
+    """With the package imported before torch, the process's HIP runtime (the one the version
+    check sees) is PyTorch's 7.0; with no device, handle creation returns an error instead of
+    letting hipBLASLt end the process."""
+    r = subprocess.run([sys.executable, "-c", CREATE_PROBE.format(root=ROOT)],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr[-2000:]
+    rt = int(re.search(r"RUNTIME (-?\d+)", r.stdout).group(1))
+    assert rt // 100000 == 700, rt
+    m = re.search(r"CREATE (\d+) (.*)", r.stdout)
+    if m:
+        assert m.group(1) == "3" and "no HIP device" in m.group(2), r.stdout

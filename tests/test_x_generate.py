@@ -262,6 +262,16 @@ def test_gen_argument_checks_before_any_hip_call():
     assert L.dadgpt_gpt2_init_params(None, ctypes.byref(good), 1, None) == 1
     assert L.dadgpt_gpt2_generate(None, None, None, 1, 1, 1, None, None, None, None) == 1
     assert L.dadgpt_matmul_bf16(None, 0x1000, 0x1000, 0x1000, 1, 1, 1, None) == 1
+    # materialized attention with dropout: the rate, and probs kept apart from dropped
+    P = 0x1000
+    assert L.dadgpt_attention_materialized_forward_dropout(P, P, P, P + 64, P, P, P, 2, 8, 64,
+                                                           0.125, 1.0, 7, None) == 1
+    assert "dropout_p" in gpt2.last_error()
+    assert L.dadgpt_attention_materialized_forward_dropout(P, P, P, P, P, P, P, 2, 8, 64, 0.125,
+                                                           0.1, 7, None) == 1
+    assert "dropped" in gpt2.last_error()
+    assert L.dadgpt_attention_materialized_backward_dropout(*[P] * 10, 2, 8, 64, 0.125, -0.1, 7,
+                                                            None) == 1
 
 
 # ------------------------------------------------------------------------------- GPU
