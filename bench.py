@@ -97,18 +97,39 @@ def event_time_ms(fn, reps, stream):
     return start.elapsed_time(end) / reps
 
 
+# The sources of the profiled kernels: the traffic summary records their digest at profiling
+# time, so a bench line can say whether its traffic figures describe the kernels it timed.
+KERNEL_SOURCES = [os.path.join(ROOT, "dadgpt_amd", "csrc", n) for n in (
+    "attn_fwd_bf16.hip", "attn_bwd_bf16.hip", "decode.hip", "tiles.hpp", "common.hpp",
+    "lanes.hpp", "dropout.hpp", "kernels.hpp")]
+
+
+def kernel_sources_digest():
+    import hashlib
+
+    h = hashlib.sha256()
+    for path in KERNEL_SOURCES:
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def load_traffic():
-    """{kernel: HBM bytes per launch} from the committed --pmc summary (empty if absent)."""
-    out = {}
+    """({kernel: HBM bytes per launch}, digest of the kernel sources they were measured on)
+    from the committed --pmc summary (empty / None if absent)."""
+    out, digest = {}, None
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
                 m = re.match(r"^traffic\s+(\w+)\s+(\d+)\s*$", line)
                 if m:
                     out[m.group(1)] = int(m.group(2))
+                m = re.match(r"^# kernel sources digest\s+([0-9a-f]+)", line)
+                if m:
+                    digest = m.group(1)
     except OSError:
         pass
-    return out
+    return out, digest
 
 
 def decode_lens():
@@ -456,7 +477,9 @@ def generate_cfg5(gate: bool = True):
         "decode_graph": True,
         "eager_decode_ms": round(eager["decode_ms"], 3),
         "decode_attn_ms": round(eager["decode_attn_ms"], 3),
-        "attn_share_of_decode": round(eager["decode_attn_ms"] / t["decode_ms"], 4),
+        "attn_share_of_decode": round(eager["decode_attn_ms"] / eager["decode_ms"], 4),
+        "attn_share_basis": "eager decode steps: the attention launches timed with events over "
+                            "the same run's decode time (a replayed graph cannot hold events)",
         "fp32_attention": {
             "tokens_per_s": round(GEN_N * GEN_NEW / ((ref["timing"]["prefill_ms"] +
                                                       ref["timing"]["decode_ms"]) * 1e-3), 1),
@@ -480,6 +503,17 @@ def generate_cfg5(gate: bool = True):
         }
     print(f"[bench] generate cfg5 {json.dumps(out)}", file=sys.stderr, flush=True)
     return out
+
+
+def hip_stack():
+    """The HIP runtime and hipBLASLt versions this process runs on (the generation leg's and
+    materialized path's GEMMs), and whether the library accepts the pair."""
+    from dadgpt_amd import gpt2
+
+    try:
+        return gpt2.blas_stack_versions()
+    except Exception as e:  # the versions are a report, not a gate, here
+        return {"error": str(e)}
 
 
 def main():
@@ -604,7 +638,15 @@ def main():
     print(f"[bench] device copy of the decode's bytes: {copy_ms * 1e3:.2f} us "
           f"({copy_gbps:.0f} GB/s read + write)", file=sys.stderr, flush=True)
 
-    traffic = load_traffic()
+    traffic, traffic_digest = load_traffic()
+    digest_now = kernel_sources_digest()
+    traffic_src = {"file": os.path.relpath(TRAFFIC_FILE, ROOT),
+                   "kernel_sources_digest": traffic_digest,
+                   "current_sources_digest": digest_now,
+                   "current": traffic_digest == digest_now,
+                   "what": "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE per dispatch (scaled by a "
+                           "calibration copy), measured on the kernel sources of that digest; "
+                           "stale when the digests differ"}
     comps = {}
     for name, ms in kern_ms.items():
         c = {"ms": round(ms, 5)}
@@ -671,7 +713,8 @@ def main():
     ach = KERNEL_FLOPS[dom] / (kern_ms[dom] * 1e-3) / 1e12
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic.get(dom)}
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic.get(dom),
+                "traffic_source": traffic_src}
 
     value = (FWD_FLOPS + BWD_FLOPS) / (ms_step * 1e-3) / 1e12
     line = {
@@ -694,6 +737,7 @@ def main():
         "roofline": roofline,
         "components": comps,
         "decode_gbps": round(dec_gbps, 1),
+        "hip_stack": hip_stack(),
     }
     if not args.no_cpu_baseline:
         print(f"[bench] cpu baseline on {args.cpu_slices} slices ...", file=sys.stderr,
