@@ -218,7 +218,7 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks)
 __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_kernel(
     bf16* __restrict__ out, float* __restrict__ lse, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, int S, float scale_log2,
-    int negate_q, const AttnLayout L, const DropParams dr) {
+    int negate_q, int snake, const AttnLayout L, const DropParams dr) {
   // scale_log2 = |scale| * log2(e); a negative scale is applied by negating Q (exact in bf16),
   // so the row max of the raw scores is the row max of the scaled ones.
   constexpr int QB = kQW * kWaves;
@@ -232,8 +232,20 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
   __shared__ f32x4 smask[4][64];
   static_assert(kWaves * kQW <= 2 * kTileRows, "the epilogue stages every wave's rows in sk");
 
-  const int bh = blockIdx.x;
-  const int qblk = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks dispatch first
+  // Dispatch order: longest (latest) query blocks first, (b,h) fastest. With `snake` > 0 (a grid
+  // that fits on the CUs in one round) every other group of `snake` workgroups in dispatch
+  // order is reversed, so the workgroups a CU receives pair long query blocks with short ones.
+  int bh = blockIdx.x, yrev = blockIdx.y;
+  if (snake > 0) {
+    const int i = blockIdx.y * gridDim.x + blockIdx.x, g = i / snake;
+    if (g & 1) {
+      const int n = min(snake, (int)(gridDim.x * gridDim.y) - g * snake);  // ids in the group
+      const int j = g * snake + (n - 1 - (i - g * snake));
+      bh = j % gridDim.x;
+      yrev = j / gridDim.x;
+    }
+  }
+  const int qblk = gridDim.y - 1 - yrev;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
   const int l32 = lane & 31, hi = lane >> 5;
@@ -346,12 +358,32 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
   }
 }
 
+// Compute units of the current device (cached per device; 0 if unknown).
+int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static int cus[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 template <int D>
 hipError_t launch_fwd_bf16_t(bf16* out, float* lse, const bf16* q, const bf16* k, const bf16* v,
                              int BH, int S, float scale, const AttnLayout& L,
                              const Dropout* drop, hipStream_t stream) {
   constexpr int QB = kQW * kWaves;
   dim3 grid(BH, (S + QB - 1) / QB);
+  // Snake order only where the whole grid is resident at once (kMinBlocks per CU): measured
+  // 2% faster at B8 H12 T1024 (768 workgroups) and 6% slower at B16 (1,536, two rounds).
+  const int cus = device_cus();
+  const int snake =
+      cus > 0 && (long long)grid.x * grid.y <= (long long)cus * kMinBlocks ? cus : 0;
   // Masked scores are -inf and exponentiate as exp2(-inf * c - m), so c must be positive: a
   // zero scale (uniform attention) runs with c = 1e-30: every score below 1e22 in magnitude
   // then has |s*c - m| < 2^-25, an fp32 weight of exactly 1.
@@ -359,13 +391,13 @@ hipError_t launch_fwd_bf16_t(bf16* out, float* lse, const bf16* q, const bf16* k
   const DropParams dr = drop_params(drop);
   if (drop != nullptr) {  // contiguous layout only (checked by the caller)
     fwd_bf16_kernel<D, false, true><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c,
-                                                                      scale < 0.f, L, dr);
+                                                                      scale < 0.f, snake, L, dr);
   } else if (is_contiguous(L, S, D)) {
     fwd_bf16_kernel<D, false, false><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c,
-                                                                       scale < 0.f, L, dr);
+                                                                       scale < 0.f, snake, L, dr);
   } else {
     fwd_bf16_kernel<D, true, false><<<grid, 64 * kWaves, 0, stream>>>(out, lse, q, k, v, S, c,
-                                                                      scale < 0.f, L, dr);
+                                                                      scale < 0.f, snake, L, dr);
   }
   return hipGetLastError();
 }
