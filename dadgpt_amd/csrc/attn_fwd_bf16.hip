@@ -150,7 +150,8 @@ __device__ __forceinline__ float fwd_exp(bf16x8 (&pb)[2], const f32x16& s, float
                            p1 * keep_factor(keep, r + 1, dscale));
       else
         w[e] = pack_bf16x2(p0, p1);
-      ls += p0 + p1;
+      // (the first pair starts the sum: 0 + x cannot be folded, since it maps -0 to +0)
+      ls = r == 0 ? p0 + p1 : ls + (p0 + p1);
     }
     pb[j] = as_bf16x8(w);
   }
@@ -180,12 +181,13 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[
     float ls = fwd_exp<DROP>(pb[i], s[i], mrun[i], scale_log2, keep[i], dscale);
     // ls >= 2^64, +inf or NaN, compared on the bits: a row's first chunk with masked keys sums
     // to NaN (exp2 of -inf - (-inf)), and this file is built assuming no NaNs, under which a
-    // floating-point compare may be folded to one that NaN fails. Each row then takes the
-    // slow path on its own first chunk, whatever its wave-mates hold (a NaN query row
-    // included), and only the rows that need it move their maximum: the others keep m (a
-    // correction of exp2(0) = 1 and the same exponentials), so no row's bits depend on
+    // floating-point compare may be folded to one that NaN fails. ls is +0, positive or NaN,
+    // and the unsigned compare holds for every NaN (a negative one through its sign bit). Each
+    // row then takes the slow path on its own first chunk, whatever its wave-mates hold (a NaN
+    // query row included), and only the rows that need it move their maximum: the others keep
+    // m (a correction of exp2(0) = 1 and the same exponentials), so no row's bits depend on
     // another row.
-    const bool need = (__float_as_uint(ls) & 0x7fffffffu) >= __float_as_uint(kMaxP);
+    const bool need = __float_as_uint(ls) >= __float_as_uint(kMaxP);
     if (__builtin_amdgcn_ballot_w64(need) != 0) {  // wave-uniform
       float mx = s[i][0];
 #pragma unroll
