@@ -111,9 +111,8 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
   constexpr int DS = D / 16, DB = D / 32;
   const int l32 = lane & 31, hi = lane >> 5;
   const int qr = 32 * qb + sigma32(l32);
-  // Phases, fenced so the compiler keeps them apart (each phase's operands are dead before
-  // the next one's are read): S = stats + Q K^T, dP = stats + dO V^T, softmax,
-  // dV += dO^T P, dK += Q^T dS.
+  // Phases: S = stats + Q K^T, dP = stats + dO V^T, softmax, dV += dO^T P, dK += Q^T dS,
+  // ordered by the compiler's scheduler (fencing them apart measured 2-3% slower).
   auto stats = [&](const float* row, f32x16& acc) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -135,7 +134,6 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) s = mfma32(qa[ds], kop[ds], s);
   }
-  __builtin_amdgcn_sched_barrier(0);
   {
     bf16x8 da[DS];
 #pragma unroll
@@ -147,7 +145,6 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) dp = mfma32(da[ds], vop[ds], dp);
   }
-  __builtin_amdgcn_sched_barrier(0);
   bf16x8 pb[2], dsb[2];
   f32x16 nd;  // -delta of the block's queries (dropout only)
   if constexpr (DROP) stats(sdl, nd);
@@ -188,7 +185,6 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
     pb[j] = as_bf16x8(wp);
     dsb[j] = as_bf16x8(wd);
   }
-  __builtin_amdgcn_sched_barrier(0);
   {
     bf16x8 t[DB][2];  // A = dO^T: lane d = 32db + l32 gets tile queries 32qb + 16j + 8hi + 0..7
 #pragma unroll
@@ -200,7 +196,6 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
 #pragma unroll
       for (int db = 0; db < DB; ++db) dvacc[db] = mfma32(t[db][j], pb[j], dvacc[db]);
   }
-  __builtin_amdgcn_sched_barrier(0);
   {
     bf16x8 t[DB][2];  // A = Q^T
 #pragma unroll
