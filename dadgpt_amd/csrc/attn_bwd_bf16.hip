@@ -326,14 +326,14 @@ constexpr int kQW = 32;  // queries per wave
 
 // One 32-key chunk (tile keys 32*kb ..) against the wave's 32 queries. Register 8j+e of lane
 // half hi holds tile key 32kb + 16j + 8hi + e. With dropout (DROP), dS = P (dP * f - delta)
-// with f = keep/(1-p) from bit 8j+e of `keep`.
+// with f = keep/(1-p) from register 8j+e's uniform in `keep`.
 template <int D, bool DROP>
 __device__ __forceinline__ void dq_chunk(bool diag, f32x16 (&dqacc)[D / 32],
                                          const bf16x8 (&qop)[D / 16],
                                          const bf16x8 (&doop)[D / 16], const bf16* sk,
                                          const bf16* sv, int kb, int qrow_minus_k0, float lse2,
-                                         float dlt, int lane, float scale_log2, uint32_t keep,
-                                         float dscale) {
+                                         float dlt, int lane, float scale_log2,
+                                         const KeepWords16& keep, const DropParams& dr) {
   constexpr int DS = D / 16, DB = D / 32;
   const int l32 = lane & 31, hi = lane >> 5;
   f32x16 s = f32x16{}, dp = f32x16{};
@@ -373,7 +373,7 @@ __device__ __forceinline__ void dq_chunk(bool diag, f32x16 (&dqacc)[D / 32],
         const int e = 2 * e2 + h;
         const float p = pr[8 * j + e];
         if constexpr (DROP)
-          d[h] = p * fmaf(dp[8 * j + e], keep_factor(keep, 8 * j + e, dscale), -dlt);
+          d[h] = p * fmaf(dp[8 * j + e], keep_factor(keep, 8 * j + e, dr), -dlt);
         else
           d[h] = p * (dp[8 * j + e] - dlt);
       }
@@ -475,11 +475,11 @@ __global__ __launch_bounds__(64 * kWaves, kDqMinBlocks) void dq_bf16_kernel(
       for (int kb = 0; kb < 2; ++kb) {
         const int klo = k0 + 32 * kb;        // first key of the chunk
         if (klo > q0 + kQW - 1) continue;    // every key after every query of the wave
-        uint32_t keep = 0;
-        if constexpr (DROP) keep = keep_row16(dr, (uint64_t)bh * S + qrow, klo, hi);
+        KeepWords16 keep = {};
+        if constexpr (DROP) keep = keep_words16(dr, (uint64_t)bh * S + qrow, klo, hi);
         // some key after some query: mask
         dq_chunk<D, DROP>(klo + 31 > q0, dqacc, qop, doop, ck, cv, kb, qrow - k0, lse2, dlt,
-                          lane, scale_log2, keep, dr.scale);
+                          lane, scale_log2, keep, dr);
       }
     }
     wait_vm_lds<0>();

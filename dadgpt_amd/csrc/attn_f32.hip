@@ -20,7 +20,7 @@
 // while the current one is on the matrix cores.
 //
 // The DROP instantiations apply attention-probability dropout with the keep bits of
-// dropout.hpp: the forward and dQ hold keys along registers (keep_row16), dK/dV holds queries
+// dropout.hpp: the forward and dQ hold keys along registers (keep_words16), dK/dV holds queries
 // along registers (keep_col16).
 #include "common.hpp"
 #include "dropout.hpp"
@@ -216,13 +216,13 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void fwd_f32_kernel(
       const float alpha = expf(m - mn);
       m = mn;
       float ps = 0.f;
-      uint32_t keep = 0;
-      if constexpr (DROP) keep = keep_row16(dr, (uint64_t)bh * S + qi, key0, h);
+      KeepWords16 keep = {};
+      if constexpr (DROP) keep = keep_words16(dr, (uint64_t)bh * S + qi, key0, h);
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
         const float p = expf(s[u] - mn);
         ps += p;
-        s[u] = DROP ? p * keep_factor(keep, u, dr.scale) : p;
+        s[u] = DROP ? p * keep_factor(keep, u, dr) : p;
       }
       l = l * alpha + sum_halves(ps);
 #pragma unroll
@@ -384,14 +384,14 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
       // lane (l32, h), register u: query qi, key key0 + reg_row(u, h)
       f32x16 s = score_tile<D>(sk, 32 * c, qr, lane);   // K Q^T
       f32x16 dp = score_tile<D>(sv, 32 * c, gr, lane);  // V dO^T
-      uint32_t keep = 0;
-      if constexpr (DROP) keep = keep_row16(dr, (uint64_t)bh * S + qi, key0, h);
+      KeepWords16 keep = {};
+      if constexpr (DROP) keep = keep_words16(dr, (uint64_t)bh * S + qi, key0, h);
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
         const bool vis = key0 + reg_row(u, h) <= qi;
         const float p = vis ? expf(s[u] * scale - my_lse) : 0.f;
         float g = dp[u];
-        if constexpr (DROP) g *= keep_factor(keep, u, dr.scale);
+        if constexpr (DROP) g *= keep_factor(keep, u, dr);
         s[u] = p * (g - my_delta) * scale;
       }
       accumulate_t<D>(acc, sk, 32 * c, s, lane);  // dQ^T += K^T dS^T

@@ -130,11 +130,13 @@ __device__ __forceinline__ void fwd_v_ops(bf16x8 (&va)[D / 32][2], const bf16* l
 }
 
 // P = exp2(s*c - m) of one chunk as bf16 B operands; returns this lane's fp32 sum of them.
-// With dropout (DROP), the operands are P * keep/(1-p) (register r kept iff bit r of keep) and
-// the sum stays that of P: the normaliser and logsumexp are those of the undropped row.
+// With dropout (DROP), the operands are P * keep/(1-p) (register r kept iff its uniform in
+// `keep` passes the threshold) and the sum stays that of P: the normaliser and logsumexp are
+// those of the undropped row.
 template <bool DROP>
 __device__ __forceinline__ float fwd_exp(bf16x8 (&pb)[2], const f32x16& s, float m,
-                                         float scale_log2, uint32_t keep, float dscale) {
+                                         float scale_log2, const KeepWords16& keep,
+                                         const DropParams& dr) {
   const float mneg = -m;
   float ls = 0.f;
 #pragma unroll
@@ -146,8 +148,7 @@ __device__ __forceinline__ float fwd_exp(bf16x8 (&pb)[2], const f32x16& s, float
       const float p0 = fast_exp2(fmaf(s[r], scale_log2, mneg));
       const float p1 = fast_exp2(fmaf(s[r + 1], scale_log2, mneg));
       if constexpr (DROP)
-        w[e] = pack_bf16x2(p0 * keep_factor(keep, r, dscale),
-                           p1 * keep_factor(keep, r + 1, dscale));
+        w[e] = pack_bf16x2(p0 * keep_factor(keep, r, dr), p1 * keep_factor(keep, r + 1, dr));
       else
         w[e] = pack_bf16x2(p0, p1);
       // (the first pair starts the sum: 0 + x cannot be folded, since it maps -0 to +0)
@@ -173,12 +174,13 @@ template <int D, int NQB, bool DROP>
 __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[NQB][D / 32],
                                                float (&mrun)[NQB], float (&lrun)[NQB],
                                                const bf16x8 (&va)[D / 32][2], float scale_log2,
-                                               const uint32_t (&keep)[NQB], float dscale) {
+                                               const KeepWords16 (&keep)[NQB],
+                                               const DropParams& dr) {
   constexpr int DB = D / 32;
   bf16x8 pb[NQB][2];
 #pragma unroll
   for (int i = 0; i < NQB; ++i) {
-    float ls = fwd_exp<DROP>(pb[i], s[i], mrun[i], scale_log2, keep[i], dscale);
+    float ls = fwd_exp<DROP>(pb[i], s[i], mrun[i], scale_log2, keep[i], dr);
     // ls >= 2^64, +inf or NaN, compared on the bits: a row's first chunk with masked keys sums
     // to NaN (exp2 of -inf - (-inf)), and this file is built assuming no NaNs, under which a
     // floating-point compare may be folded to one that NaN fails. ls is +0, positive or NaN,
@@ -202,7 +204,7 @@ __device__ __forceinline__ void fwd_softmax_pv(f32x16 (&s)[NQB], f32x16 (&oacc)[
       lrun[i] *= corr;
 #pragma unroll
       for (int db = 0; db < DB; ++db) oacc[i][db] *= corr;
-      ls = fwd_exp<DROP>(pb[i], s[i], mnew, scale_log2, keep[i], dscale);
+      ls = fwd_exp<DROP>(pb[i], s[i], mnew, scale_log2, keep[i], dr);
     }
     lrun[i] += ls;
   }
@@ -320,11 +322,11 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
         if (c0 > q0 + kQW - 1) break;  // every key of the chunk after every query
         bf16x8 ka[DS], va[DB][2];
         f32x16 sc[kNQB];
-        uint32_t keep[kNQB] = {};
+        KeepWords16 keep[kNQB] = {};
         if constexpr (DROP) {
 #pragma unroll
           for (int i = 0; i < kNQB; ++i)
-            keep[i] = keep_row16(dr, (uint64_t)bh * S + q0 + 32 * i + l32, c0, hi);
+            keep[i] = keep_words16(dr, (uint64_t)bh * S + q0 + 32 * i + l32, c0, hi);
         }
         fwd_k_ops<D>(ka, ck, kb, lane);
         // the chunk whose first key is the wave's first query is the one to mask
@@ -335,7 +337,7 @@ __attribute__((amdgpu_num_vgpr(512 / (kMinBlocks * kWaves / 4)))) void fwd_bf16_
         // V^T operands only now (K's are dead): their latency hides under the softmax
         __builtin_amdgcn_sched_barrier(0);
         fwd_v_ops<D>(va, cv, kb, lane);
-        fwd_softmax_pv<D, kNQB, DROP>(sc, oacc, mrun, lrun, va, scale_log2, keep, dr.scale);
+        fwd_softmax_pv<D, kNQB, DROP>(sc, oacc, mrun, lrun, va, scale_log2, keep, dr);
       }
     }
     wait_vm_lds<0>();

@@ -49,9 +49,11 @@ __device__ __forceinline__ u32x4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_
     const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
     const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
     const uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
-    c0 = hi1 ^ c1 ^ k0;
+    // three-input XORs as one v_bitop3_b32 each (truth table 0x96: odd parity), the key from
+    // a scalar register; the compiler otherwise issues two v_xor_b32
+    c0 = __builtin_amdgcn_bitop3_b32(hi1, c1, k0, 0x96);
     c1 = lo1;
-    c2 = hi0 ^ c3 ^ k1;
+    c2 = __builtin_amdgcn_bitop3_b32(hi0, c3, k1, 0x96);
     c3 = lo0;
   }
   return u32x4{c0, c1, c2, c3};
@@ -69,16 +71,23 @@ __device__ __forceinline__ uint32_t keep8(const DropParams& dr, uint64_t row, ui
   return bits;
 }
 
-// Keep bits for the score layout with a fixed row per lane and keys along the registers:
+// Keep tests for the score layout with a fixed row per lane and keys along the registers:
 // register 8j + e of lane half hi holds key key0 + 16j + 8hi + e (j < 2, e < 8; key0 a
-// multiple of 8), i.e. two groups of 8 consecutive keys, one Philox block each. Bit 8j + e of
-// the result = register 8j + e.
-__device__ __forceinline__ uint32_t keep_row16(const DropParams& dr, uint64_t row, int key0,
-                                               int hi) {
-  uint32_t bits = 0;
+// multiple of 8), i.e. two groups of 8 consecutive keys, one Philox block each. The blocks'
+// words are kept as they are: register 8j + e tests 16-bit half e%2 of word e/2 of block j.
+// Testing a half where it is used (extract, compare, select: three VALU per register) replaces
+// packing it into a bit (about four) and unpacking that again (three).
+struct KeepWords16 {
+  u32x4 w[2];
+};
+__device__ __forceinline__ KeepWords16 keep_words16(const DropParams& dr, uint64_t row, int key0,
+                                                    int hi) {
+  KeepWords16 k;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) bits |= keep8(dr, row, (uint32_t)(key0 + 16 * j + 8 * hi) >> 3) << (8 * j);
-  return bits;
+  for (int j = 0; j < 2; ++j)
+    k.w[j] = philox4x32_10((uint32_t)row, (uint32_t)(row >> 32),
+                           (uint32_t)(key0 + 16 * j + 8 * hi) >> 3, 0u, dr.k0, dr.k1);
+  return k;
 }
 
 // Bit-matrix transpose across the 8 lanes of a group, for each byte of x (bits 8j .. 8j+7)
@@ -123,6 +132,10 @@ __device__ __forceinline__ uint32_t keep_col16(const DropParams& dr, uint64_t ro
 // The factor of a probability: scale if kept, 0 if dropped.
 __device__ __forceinline__ float keep_factor(uint32_t bits, int i, float scale) {
   return (bits >> i) & 1u ? scale : 0.0f;
+}
+__device__ __forceinline__ float keep_factor(const KeepWords16& k, int r, const DropParams& dr) {
+  const uint32_t w = k.w[r >> 3][(r & 7) >> 1];
+  return ((r & 1) ? w >> 16 : w & 0xFFFFu) >= dr.thr ? dr.scale : 0.0f;
 }
 
 }  // namespace dadgpt
