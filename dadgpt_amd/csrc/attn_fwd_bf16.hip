@@ -44,10 +44,12 @@ namespace dadgpt {
 namespace {
 
 // Geometry: NQB 32-query blocks per wave, WAVES waves per workgroup, MINB workgroups per CU
-// (the register budget: 512 / (MINB * WAVES / 4) per lane). 4 waves of one query block and 3
-// workgroups per CU (3 waves per SIMD) measured fastest; 4 per SIMD (the kernel fits 128
-// registers), 8- and 16-wave workgroups and two query blocks per wave were no faster, and
-// 2-wave workgroups (twice as many, for small batches) were slower at both B16 and B8.
+// the register budget is sized for (512 / (MINB * WAVES / 4) per lane). The kernel takes 127
+// registers and 36 KB of LDS, so up to 4 workgroups (4 waves per SIMD) are resident per CU
+// when the grid has them (per-workgroup stamps at B16 H12 T1024 show 4). 4-wave workgroups of
+// one query block measured fastest: 8- and 16-wave workgroups and two query blocks per wave
+// were no faster, and 2-wave workgroups (twice as many, for small batches) were slower at
+// both B16 and B8.
 #ifndef DADGPT_FWD_NQB
 #define DADGPT_FWD_NQB 1
 #endif
@@ -383,8 +385,9 @@ hipError_t launch_fwd_bf16_t(bf16* out, float* lse, const bf16* q, const bf16* k
                              const Dropout* drop, hipStream_t stream) {
   constexpr int QB = kQW * kWaves;
   dim3 grid(BH, (S + QB - 1) / QB);
-  // Snake order only where the whole grid is resident at once (kMinBlocks per CU): measured
-  // 2% faster at B8 H12 T1024 (768 workgroups) and 6% slower at B16 (1,536, two rounds).
+  // Snake order only for grids of at most kMinBlocks workgroups per CU (all resident at once,
+  // the dispatcher dealing each CU the same number): measured 2% faster at B8 H12 T1024 (768
+  // workgroups, 3 per CU) and 6% slower at B16 (1,536).
   const int cus = device_cus();
   const int snake =
       cus > 0 && (long long)grid.x * grid.y <= (long long)cus * kMinBlocks ? cus : 0;
