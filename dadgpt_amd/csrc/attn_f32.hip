@@ -1,8 +1,12 @@
 // fp32 causal flash attention on the fp32 matrix cores of gfx950 (v_mfma_f32_32x32x2_f32:
 // fp32 operands, fp32 products and accumulation). This is the reference's precision
 // (cuda/attention.cu:1): forward with online softmax and a saved natural-log logsumexp, backward
-// recomputing the probabilities from it. Softmax exponentials and logarithms use the accurate
-// expf/logf; results match the fp32 CPU path to a few 1e-7.
+// recomputing the probabilities from it. The softmax exponentials are exp_acc (below: 1.24 ulp
+// in six VALU operations, the library expf 0.85 in thirteen) and the logsumexp's logarithm
+// is logf; results match float64 to ~1e-6 (O, lse) and the fp32 CPU path within its own
+// rounding. On gfx950 the fp32 MFMA and the VALU do not execute side by side, so every VALU
+// instruction in these kernels adds to their time: the forward moves its running maximum
+// lazily (as the bf16 forward does) and masking runs only where a chunk needs it.
 //
 // Work decomposition (every product a 32 x 32 MFMA tile, one wave per 32 rows):
 //  forward  a wave owns 32 queries (lane l holds query l % 32): S^T = K Q^T over each 32-key
@@ -56,6 +60,26 @@ __device__ __forceinline__ f32x16 zero16() {
   for (int i = 0; i < 16; ++i) z[i] = 0.f;
   return z;
 }
+
+// e^x to ~1.3 ulp (measured over [-87, 44] against double exp: 1.24 ulp, the library expf
+// 0.85) in six VALU operations instead of the library's thirteen: x log2(e) as a rounded
+// product e plus its exact remainder r (an FMA, with log2(e) split into two floats), then
+// 2^e on the hardware exp2 and the first-order correction 2^(e+r) = 2^e (1 + r ln 2). Results
+// below 2^-126 flush to zero and above 2^128 are +inf (no range reduction): the softmax
+// weights these kernels exponentiate are either negligible there or take the rescaling path.
+// An infinite x gives NaN (its remainder is inf - inf): callers keep -inf out.
+__device__ __forceinline__ float exp_acc(float x) {
+  constexpr float kL1 = 1.44269502162933349609375f;  // log2(e) rounded to float
+  constexpr float kL2 = 1.925963033500011079e-08f;   // log2(e) - kL1
+  const float e = x * kL1;
+  const float r = fmaf(x, kL2, fmaf(x, kL1, -e));
+  const float p = __builtin_amdgcn_exp2f(e);
+  return fmaf(p, r * kLn2, p);
+}
+
+// A chunk whose weights reach this in some row moves that row's running maximum: with
+// weights below 2^64, the running sums stay far inside fp32 range over any sequence length.
+constexpr float kMaxW = 0x1p64f;
 
 // A 64-row fp32 tile in LDS (pitch D + 4 floats) and its register prefetch: 256 threads, D/16
 // 16-byte pieces each; rows at or past S read as zeros.
@@ -174,7 +198,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void fwd_f32_kernel(
   __shared__ __attribute__((aligned(16))) float sv[kTile * Tile<D>::kPitch];
   const int bh = blockIdx.x;
   const int blk = gridDim.y - 1 - blockIdx.y;  // longest query blocks first
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31, h = lane >> 5;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar
   const size_t base = (size_t)bh * S * D;
   const int q0 = blk * kRows + 32 * wave;  // the wave's first query
   const int qi = q0 + l32;                 // this lane's query
@@ -186,7 +211,7 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void fwd_f32_kernel(
   f32x16 o[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) o[db] = zero16();
-  float m = neg_inf(), l = 0.f;
+  float m = neg_inf(), lh = 0.f;  // running maximum; this lane half's sum of weights
 
   Tile<D> tk, tv;
   tk.load(k + base, 0, S);
@@ -205,33 +230,56 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void fwd_f32_kernel(
       const int key0 = t * kTile + 32 * c;
       if (key0 > q0 + 31) continue;  // wave-uniform: the whole chunk is in the future
       f32x16 s = score_tile<D>(sk, 32 * c, qr, lane);
-      float cm = neg_inf();
+      // only the chunk whose first key is the wave's first query holds keys after a query
+      // (or past S); waves are 32-query aligned, so it is the one with key0 == q0
+      const bool diag = key0 == q0;
+      // weights against the running maximum m as it stands (natural-log units)
+      float w[16], ps;
+      auto weights = [&](float mref) {
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const float x = key0 + reg_row(u, h) > qi ? neg_inf() : s[u] * scale;
-        s[u] = x;
-        cm = fmaxf(cm, x);
+        for (int u = 0; u < 16; ++u) w[u] = exp_acc(fmaf(s[u], scale, -mref));
+        if (diag) {
+#pragma unroll
+          for (int u = 0; u < 16; ++u)
+            if (key0 + reg_row(u, h) > qi) w[u] = 0.f;
+        }
+        ps = w[0];  // (0 + w[0] could not be folded: it maps -0 to +0)
+#pragma unroll
+        for (int u = 1; u < 16; ++u) ps += w[u];
+      };
+      weights(m);
+      // The maximum moves only when a row's weights would reach 2^64 (or are inf/NaN: m is
+      // -inf before a row's first chunk), compared on the bits (ps is +0, positive or NaN).
+      // Both lane halves of a row take the row's decision, and only the rows that need it
+      // move: the others rescale by exp(0) = 1 and recompute the same weights, so no row's
+      // bits depend on another row.
+      const bool need = __float_as_uint(ps) >= __float_as_uint(kMaxW);
+      if (__builtin_amdgcn_ballot_w64(need) != 0) {  // wave-uniform
+        float cm = neg_inf();
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          if (!(diag && key0 + reg_row(u, h) > qi)) cm = fmaxf(cm, s[u] * scale);
+        // every row of a chunk the wave computes has a visible key: the row maximum is finite
+        const float mn = or_halves(need) ? fmaxf(m, max_halves(cm)) : m;
+        // 0 on a row's first chunk (exp_acc has no -inf input path)
+        const float alpha = m == neg_inf() ? 0.f : exp_acc(m - mn);
+        m = mn;
+        lh *= alpha;
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+        weights(m);
       }
-      const float mn = fmaxf(m, max_halves(cm));  // key 0 <= qi: finite from the first chunk
-      const float alpha = expf(m - mn);
-      m = mn;
-      float ps = 0.f;
+      lh += ps;
       KeepWords16 keep = {};
       if constexpr (DROP) keep = keep_words16(dr, (uint64_t)bh * S + qi, key0, h);
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const float p = expf(s[u] - mn);
-        ps += p;
-        s[u] = DROP ? p * keep_factor(keep, u, dr) : p;
-      }
-      l = l * alpha + sum_halves(ps);
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      for (int u = 0; u < 16; ++u) s[u] = DROP ? w[u] * keep_factor(keep, u, dr) : w[u];
       accumulate_t<D>(o, sv, 32 * c, s, lane);
     }
   }
+  const float l = sum_halves(lh);
   if (h == 0 && qi < S) lse[(size_t)bh * S + qi] = m + logf(l);
   __syncthreads();  // every wave is done with the tiles: reuse sk as per-wave staging
   store_rows_t<D>(out + base, q0, S, o, 1.0f / l, stage_slot<D>(sk, sv, wave), lane);
@@ -268,9 +316,11 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
     const DropParams dr) {
   __shared__ __attribute__((aligned(16))) float sq[kTile * Tile<D>::kPitch];
   __shared__ __attribute__((aligned(16))) float sg[kTile * Tile<D>::kPitch];
-  __shared__ float sl[kTile], sd[kTile];
+  // per query row of the tile: lse, and delta * scale
+  __shared__ __attribute__((aligned(16))) float sl[kTile], sd[kTile];
   const int bh = blockIdx.x, blk = blockIdx.y;  // early key blocks see the most queries: first
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31, h = lane >> 5;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar
   const size_t base = (size_t)bh * S * D;
   const int k0 = blk * kRows + 32 * wave;  // the wave's first key
   const int kj = k0 + l32;                 // this lane's key
@@ -298,7 +348,7 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
     __syncthreads();
     tq.store(sq);
     tg.store(sg);
-    if (threadIdx.x < kTile) sl[threadIdx.x] = pl, sd[threadIdx.x] = pd;
+    if (threadIdx.x < kTile) sl[threadIdx.x] = pl, sd[threadIdx.x] = pd * scale;
     __syncthreads();
     if (t + 1 < n_tiles) {
       tq.load(q + base, (t + 1) * kTile, S);
@@ -314,12 +364,27 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
       f32x16 dp = score_tile<D>(sg, 32 * c, vr, lane);  // dO V^T
       uint32_t keep = 0;
       if constexpr (DROP) keep = keep_col16(dr, (uint64_t)bh * S + qrow0, k0, lane);
+      // Statistics of the chunk's rows 32c + reg_row(u, h): registers 8j..8j+7 are the 8
+      // consecutive rows 32c + 16j + 8h .., two 16-byte LDS reads each.
+      float ls[16], ds[16];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int r = 32 * c + 16 * j + 8 * h + 4 * i;
+          const f32x4 a = *reinterpret_cast<const f32x4*>(sl + r);
+          const f32x4 b = *reinterpret_cast<const f32x4*>(sd + r);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ls[8 * j + 4 * i + e] = a[e], ds[8 * j + 4 * i + e] = b[e];
+        }
+      // keys after a query, or rows past S, only where the chunk reaches the wave's first
+      // keys or S (wave-uniform)
+      const bool mask = qrow0 < k0 + 31 || qrow0 + 31 >= S;
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
         const int qrow = qrow0 + reg_row(u, h);
-        const int rl = 32 * c + reg_row(u, h);
-        const bool vis = kj <= qrow && qrow < S;
-        const float p = vis ? expf(s[u] * scale - sl[rl]) : 0.f;
+        float p = exp_acc(fmaf(s[u], scale, -ls[u]));
+        if (mask && !(kj <= qrow && qrow < S)) p = 0.f;
         float g = dp[u];
         if constexpr (DROP) {
           const float f = keep_factor(keep, u, dr.scale);
@@ -328,7 +393,7 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
         } else {
           s[u] = p;
         }
-        dp[u] = p * (g - sd[rl]) * scale;
+        dp[u] = p * fmaf(g, scale, -ds[u]);  // P (dP - delta) scale
       }
       accumulate_t<D>(dva, sg, 32 * c, s, lane);   // dV^T += dO^T P
       accumulate_t<D>(dka, sq, 32 * c, dp, lane);  // dK^T += Q^T dS
@@ -349,7 +414,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
   __shared__ __attribute__((aligned(16))) float sv[kTile * Tile<D>::kPitch];
   const int bh = blockIdx.x;
   const int blk = gridDim.y - 1 - blockIdx.y;  // longest query blocks first
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31, h = lane >> 5;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar
   const size_t base = (size_t)bh * S * D;
   const int q0 = blk * kRows + 32 * wave;
   const int qi = q0 + l32;
@@ -360,7 +426,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
   float qr[D / 2], gr[D / 2];
   load_half_row<D>(qr, q + base + (size_t)qc * D, h);
   load_half_row<D>(gr, dout + base + (size_t)qc * D, h);
-  const float my_lse = lse[(size_t)bh * S + qc], my_delta = delta[(size_t)bh * S + qc];
+  const float my_lse = lse[(size_t)bh * S + qc];
+  const float my_dscale = delta[(size_t)bh * S + qc] * scale;
   f32x16 acc[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
@@ -386,13 +453,22 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
       f32x16 dp = score_tile<D>(sv, 32 * c, gr, lane);  // V dO^T
       KeepWords16 keep = {};
       if constexpr (DROP) keep = keep_words16(dr, (uint64_t)bh * S + qi, key0, h);
+      // only the chunk whose first key is the wave's first query holds keys after a query (or
+      // past S): waves are 32-query aligned
+      const bool diag = key0 == q0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) s[u] = exp_acc(fmaf(s[u], scale, -my_lse));  // P
+      if (diag) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          if (key0 + reg_row(u, h) > qi) s[u] = 0.f;
+      }
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
-        const bool vis = key0 + reg_row(u, h) <= qi;
-        const float p = vis ? expf(s[u] * scale - my_lse) : 0.f;
+        const float p = s[u];
         float g = dp[u];
         if constexpr (DROP) g *= keep_factor(keep, u, dr);
-        s[u] = p * (g - my_delta) * scale;
+        s[u] = p * fmaf(g, scale, -my_dscale);  // P (dP - delta) scale
       }
       accumulate_t<D>(acc, sk, 32 * c, s, lane);  // dQ^T += K^T dS^T
     }
