@@ -207,6 +207,31 @@ def test_bf16_scale_zero_negative_large(gpu, scale, D):
         assert max_abs(host(a), b) <= tol_grad, nm
 
 
+@pytest.mark.parametrize("scale", [0.0, -0.125, 1.0, 4.0])
+@pytest.mark.parametrize("D", [64, 32])
+def test_fp32_scale_zero_negative_large(gpu, scale, D):
+    """The fp32 kernels' lazy running maximum at the scales that stress it: zero (every weight
+    exp(0) = 1), negative, and large ones whose sharp rows move the maximum on many chunks
+    (scale 4 with N(0,1) inputs puts score gaps of ~100 natural-log units between keys)."""
+    BH, S = 2, 300
+    case(f"fp32 scale={scale} BH={BH} S={S} D={D}")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=190 + D, with_dout=True)
+    q, k, v, g = (dev(x, torch.float32) for x in (qn, kn, vn, gn))
+    out, lse = A.attention_forward(q, k, v, scale)
+    dq, dk, dv, _ = A.attention_backward(g, out, lse, q, k, v, scale)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oracle.attn_fwd(qn, kn, vn, scale, threads=8)
+    # values and gradients grow with |scale| (P is sharper, dQ and dK carry the factor):
+    # the fp32 bound is relative to the largest reference value
+    ref = oracle.attn_bwd(gn, qn, kn, vn, scale, threads=8)[:3]
+    assert max_abs(host(out), o_ref) <= TOL_F32 * max(1.0, np.abs(o_ref).max())
+    assert max_abs(host(lse), l_ref) <= TOL_F32 * max(1.0, np.abs(l_ref).max())
+    if scale == 0.0:
+        assert max_abs(host(lse)[0], np.log(np.arange(1, S + 1))) <= TOL_F32 * np.log(S)
+    for a, b, nm in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+        assert max_abs(host(a), b) <= TOL_F32 * max(1.0, np.abs(b).max()), nm
+
+
 def torch_reference(q, k, v, scale, dout=None, chunk=16):
     """Materialized fp32 causal attention on the GPU with torch (GEMMs on contiguous
     operands): O, lse and, with dout, dQ/dK/dV plus the two quantities the column-sum bounds
