@@ -1,27 +1,33 @@
-// fp32 causal flash attention on the fp32 matrix cores of gfx950 (v_mfma_f32_32x32x2_f32:
-// fp32 operands, fp32 products and accumulation). This is the reference's precision
+// fp32 causal flash attention at fp32 accuracy on gfx950. This is the reference's precision
 // (cuda/attention.cu:1): forward with online softmax and a saved natural-log logsumexp, backward
-// recomputing the probabilities from it. The softmax exponentials are exp_acc (below: 1.24 ulp
-// in six VALU operations, the library expf 0.85 in thirteen) and the logsumexp's logarithm
-// is logf; results match float64 to ~1e-6 (O, lse) and the fp32 CPU path within its own
-// rounding. On gfx950 the fp32 MFMA and the VALU do not execute side by side, so every VALU
-// instruction in these kernels adds to their time: the forward moves its running maximum
-// lazily (as the bf16 forward does) and masking runs only where a chunk needs it.
+// recomputing the probabilities from it. The forward computes its fp32 products on the bf16
+// matrix cores, each float split into three bf16 values and each product formed from the six
+// cross terms that matter (see X3 below: as accurate as the fp32 MFMA, in 37% of its matrix
+// time, and beside the VALU); the backward uses the fp32 MFMA (v_mfma_f32_32x32x2_f32). The
+// softmax exponentials are exp_acc (below: 1.24 ulp in six VALU operations, the library expf
+// 0.85 in thirteen) and the logsumexp's logarithm is logf; results match float64 to ~1e-6
+// (O, lse) and the fp32 CPU path within its own rounding. On gfx950 the fp32 MFMA and the VALU
+// do not execute side by side, so every VALU instruction of the backward adds to its time;
+// the forward moves its running maximum lazily (as the bf16 forward does) and masking runs
+// only where a chunk needs it.
 //
 // Work decomposition (every product a 32 x 32 MFMA tile, one wave per 32 rows):
 //  forward  a wave owns 32 queries (lane l holds query l % 32): S^T = K Q^T over each 32-key
-//           chunk with Q in registers, the online softmax per lane, O^T += V^T P^T with P taken
-//           straight from the score registers (the K rows are read through sigma32, so score
-//           register u of lane half h is the MFMA k-index u of that half: no lane exchange);
+//           chunk with Q in registers (split once), the online softmax per lane, O^T += V^T P^T
+//           with P split from the score registers (the K rows are read through sigma32, so
+//           score registers 8j..8j+7 of lane half h are the MFMA k-slice of that half: no lane
+//           exchange). K and V tiles are split once per workgroup as they are staged, into
+//           three bf16 planes each in the bf16 kernels' swizzled layout, read with
+//           ds_read_b128 (K rows) and ds_read_b64_tr_b16 (V^T);
 //  dK/dV    a wave owns 32 keys (lane l holds key l % 32) and walks every later query chunk:
 //           S = Q K^T and dP = dO V^T with K and V in registers, P and dS in registers,
 //           dV^T += dO^T P and dK^T += Q^T dS; nothing is shared between waves (no atomics);
 //  dQ       a wave owns 32 queries again: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T;
 //  delta    rowsum(dO * O), a separate pass that dK/dV and dQ both read.
-// The MFMA k-index of the score products runs over d_head as (lane half h, step t) -> d =
-// h * D/2 + t, so every lane reads D/2 contiguous floats of a row. Tiles of 64 rows are
-// staged in LDS with the row pitch padded by 4 floats; the next tile is loaded into registers
-// while the current one is on the matrix cores.
+// In the backward the MFMA k-index of the score products runs over d_head as (lane half h,
+// step t) -> d = h * D/2 + t, so every lane reads D/2 contiguous floats of a row. Its tiles of
+// 64 rows are staged in LDS with the row pitch padded by 4 floats. In both directions the next
+// tile is loaded into registers while the current one is on the matrix cores.
 //
 // The DROP instantiations apply attention-probability dropout with the keep bits of
 // dropout.hpp: the forward and dQ hold keys along registers (keep_words16), dK/dV holds queries
@@ -30,6 +36,7 @@
 #include "dropout.hpp"
 #include "kernels.hpp"
 #include "lanes.hpp"
+#include "tiles.hpp"
 
 namespace dadgpt {
 namespace {
@@ -155,6 +162,110 @@ __device__ __forceinline__ void accumulate_t(f32x16 (&acc)[D / 32], const float*
   }
 }
 
+// fp32 products on the bf16 matrix cores. A float x is split into three bf16 values
+// x = x1 + x2 + x3 (each the round-to-nearest of what the previous ones leave, so the three
+// carry 24 significant bits and the rest is below 2^-27 |x|); a product x y is then the six
+// cross terms whose weight is at least 2^-18 (x1y1, x1y2, x2y1, x1y3, x3y1, x2y2), each exact
+// in fp32 and summed by the MFMA in fp32. Six v_mfma_f32_32x32x16_bf16 (32 cycles each) do
+// the work of eight v_mfma_f32_32x32x2_f32 (64 cycles each), and, unlike the fp32 MFMA, they
+// run beside the VALU. Measured over random 32x32x64 products: largest error 2.5e-7 of
+// sum |x_k y_k|, against 3.5e-7 for the fp32 MFMA.
+struct X3 {
+  bf16x8 v[3];
+};
+
+__device__ __forceinline__ X3 split3(const float (&x)[8]) {
+  u32x4 w[3];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a0 = x[2 * i], a1 = x[2 * i + 1];
+    const uint32_t p = pack_bf16x2(a0, a1);
+    const float b0 = a0 - bf16_lo(p), b1 = a1 - bf16_hi(p);  // exact
+    const uint32_t q = pack_bf16x2(b0, b1);
+    const float c0 = b0 - bf16_lo(q), c1 = b1 - bf16_hi(q);  // exact
+    w[0][i] = p;
+    w[1][i] = q;
+    w[2][i] = pack_bf16x2(c0, c1);
+  }
+  return X3{{as_bf16x8(w[0]), as_bf16x8(w[1]), as_bf16x8(w[2])}};
+}
+
+// acc += A B over a 16-deep slice, A and B as X3 (smallest terms first).
+__device__ __forceinline__ f32x16 mfma_x6(const X3& a, const X3& b, f32x16 acc) {
+  acc = mfma32(a.v[1], b.v[1], acc);
+  acc = mfma32(a.v[2], b.v[0], acc);
+  acc = mfma32(a.v[0], b.v[2], acc);
+  acc = mfma32(a.v[1], b.v[0], acc);
+  acc = mfma32(a.v[0], b.v[1], acc);
+  return mfma32(a.v[0], b.v[0], acc);
+}
+
+// A 64-row tile split into three bf16 planes in LDS, each in the row-major swizzled layout of
+// the bf16 kernels (tiles.hpp), so the score operands are ds_read_b128 and the transposed
+// ones ds_read_b64_tr_b16 reads. Each float is split once per workgroup, when the tile is
+// staged, instead of once per wave that reads it.
+template <int D>
+__device__ __forceinline__ void store_x3(const Tile<D>& t, bf16* planes) {
+#pragma unroll
+  for (int i = 0; i < Tile<D>::kPieces; ++i) {
+    const int u = threadIdx.x + 256 * i, row = u / (D / 4), c = u % (D / 4);
+    const int off = rm_off<D>(row, c >> 1) + 4 * (c & 1);  // 4 floats: half a 16-byte chunk
+    uint32_t w[3][2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float a0 = t.r[i][2 * k], a1 = t.r[i][2 * k + 1];
+      const uint32_t p = pack_bf16x2(a0, a1);
+      const float b0 = a0 - bf16_lo(p), b1 = a1 - bf16_hi(p);
+      const uint32_t q = pack_bf16x2(b0, b1);
+      w[0][k] = p;
+      w[1][k] = q;
+      w[2][k] = pack_bf16x2(b0 - bf16_lo(q), b1 - bf16_hi(q));
+    }
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+      *reinterpret_cast<u32x2*>(planes + pl * kTile * D + off) = u32x2{w[pl][0], w[pl][1]};
+  }
+}
+
+template <int D>
+__device__ __forceinline__ f32x16 score_tile_p(const bf16* planes, int chunk_row0,
+                                               const X3 (&qb)[D / 16], int lane) {
+  const int krow = chunk_row0 + sigma32(lane & 31), hi = lane >> 5;
+  f32x16 acc = zero16();
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds) {
+    X3 a;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+      a.v[pl] = lds_op(planes + pl * kTile * D, rm_off<D>(krow, 2 * ds + hi));
+    acc = mfma_x6(a, qb[ds], acc);
+  }
+  return acc;
+}
+
+template <int D>
+__device__ __forceinline__ void accumulate_t_p(f32x16 (&acc)[D / 32], const bf16* planes,
+                                               int chunk_row0, const f32x16& p, int lane) {
+  X3 pb[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = p[8 * j + e];
+    pb[j] = split3(x);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      X3 a;
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        a.v[pl] = lds_tr_op<D>(planes + pl * kTile * D, chunk_row0 + 16 * j, 32 * db, lane);
+      acc[db] = mfma_x6(a, pb[j], acc[db]);
+    }
+}
+
 // Writes a wave's transposed accumulators (element r of lane (l32, h), block db: row l32 of
 // the wave, column 32 db + c32_row(r, h)) as 32 contiguous rows of D floats through the wave's
 // LDS slot `stage` (32 x (D + 4) floats), times `mul` (per lane).
@@ -194,8 +305,11 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void fwd_f32_kernel(
     float* __restrict__ out, float* __restrict__ lse, const float* __restrict__ q,
     const float* __restrict__ k, const float* __restrict__ v, int S, float scale,
     const DropParams dr) {
-  __shared__ __attribute__((aligned(16))) float sk[kTile * Tile<D>::kPitch];
-  __shared__ __attribute__((aligned(16))) float sv[kTile * Tile<D>::kPitch];
+  // K and V tiles as three bf16 planes each; after the tile loop the first holds the
+  // epilogue's fp32 staging rows
+  __shared__ __attribute__((aligned(16))) bf16 skp[3 * kTile * D];
+  __shared__ __attribute__((aligned(16))) bf16 svp[3 * kTile * D];
+  static_assert(3 * kTile * D * 2 >= 2 * 32 * Tile<D>::kPitch * 4, "epilogue staging fits");
   const int bh = blockIdx.x;
   const int blk = gridDim.y - 1 - blockIdx.y;  // longest query blocks first
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
@@ -206,8 +320,19 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void fwd_f32_kernel(
   const int last = min(S, (blk + 1) * kRows) - 1;  // the workgroup's last query
   const int n_tiles = last / kTile + 1;
 
-  float qr[D / 2];
-  load_half_row<D>(qr, q + base + (size_t)min(qi, S - 1) * D, h);
+  X3 qb[D / 16];  // the lane's query row, columns 16 ds + 8 h + 0..7, split
+  {
+    const float* qrow = q + base + (size_t)min(qi, S - 1) * D + 8 * h;
+#pragma unroll
+    for (int ds = 0; ds < D / 16; ++ds) {
+      float a[8];
+      const f32x4 v0 = *reinterpret_cast<const f32x4*>(qrow + 16 * ds);
+      const f32x4 v1 = *reinterpret_cast<const f32x4*>(qrow + 16 * ds + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] = v0[e], a[4 + e] = v1[e];
+      qb[ds] = split3(a);
+    }
+  }
   f32x16 o[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) o[db] = zero16();
@@ -218,8 +343,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void fwd_f32_kernel(
   tv.load(v + base, 0, S);
   for (int t = 0; t < n_tiles; ++t) {
     __syncthreads();  // the previous tile's reads are done
-    tk.store(sk);
-    tv.store(sv);
+    store_x3<D>(tk, skp);
+    store_x3<D>(tv, svp);
     __syncthreads();
     if (t + 1 < n_tiles) {  // next tile in flight during this one
       tk.load(k + base, (t + 1) * kTile, S);
@@ -229,7 +354,7 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void fwd_f32_kernel(
     for (int c = 0; c < 2; ++c) {
       const int key0 = t * kTile + 32 * c;
       if (key0 > q0 + 31) continue;  // wave-uniform: the whole chunk is in the future
-      f32x16 s = score_tile<D>(sk, 32 * c, qr, lane);
+      f32x16 s = score_tile_p<D>(skp, 32 * c, qb, lane);
       // only the chunk whose first key is the wave's first query holds keys after a query
       // (or past S); waves are 32-query aligned, so it is the one with key0 == q0
       const bool diag = key0 == q0;
@@ -276,13 +401,14 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void fwd_f32_kernel(
       if constexpr (DROP) keep = keep_words16(dr, (uint64_t)bh * S + qi, key0, h);
 #pragma unroll
       for (int u = 0; u < 16; ++u) s[u] = DROP ? w[u] * keep_factor(keep, u, dr) : w[u];
-      accumulate_t<D>(o, sv, 32 * c, s, lane);
+      accumulate_t_p<D>(o, svp, 32 * c, s, lane);
     }
   }
   const float l = sum_halves(lh);
   if (h == 0 && qi < S) lse[(size_t)bh * S + qi] = m + logf(l);
   __syncthreads();  // every wave is done with the tiles: reuse sk as per-wave staging
-  store_rows_t<D>(out + base, q0, S, o, 1.0f / l, stage_slot<D>(sk, sv, wave), lane);
+  float* stage = reinterpret_cast<float*>(wave < 2 ? skp : svp) + (wave & 1) * 32 * Tile<D>::kPitch;
+  store_rows_t<D>(out + base, q0, S, o, 1.0f / l, stage, lane);
 }
 
 // ----------------------------------------------------------------------------- backward

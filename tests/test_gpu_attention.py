@@ -221,15 +221,18 @@ def test_fp32_scale_zero_negative_large(gpu, scale, D):
     dq, dk, dv, _ = A.attention_backward(g, out, lse, q, k, v, scale)
     torch.cuda.synchronize()
     o_ref, l_ref = oracle.attn_fwd(qn, kn, vn, scale, threads=8)
-    # values and gradients grow with |scale| (P is sharper, dQ and dK carry the factor):
-    # the fp32 bound is relative to the largest reference value
     ref = oracle.attn_bwd(gn, qn, kn, vn, scale, threads=8)[:3]
-    assert max_abs(host(out), o_ref) <= TOL_F32 * max(1.0, np.abs(o_ref).max())
-    assert max_abs(host(lse), l_ref) <= TOL_F32 * max(1.0, np.abs(l_ref).max())
+    # The bound is relative to the largest reference value (gradients grow with |scale|), and
+    # above the default scale it grows with |scale| / default: the weights exponentiate the
+    # scores times the scale, so fp32 rounding in a score moves them that much more (any fp32
+    # product reaches 0.7-1.0e-5 of max |O| at |scale| = 4, D = 64: 32x the default).
+    tol = TOL_F32 * max(1.0, abs(scale) / scale_of(D))
+    assert max_abs(host(out), o_ref) <= tol * max(1.0, np.abs(o_ref).max())
+    assert max_abs(host(lse), l_ref) <= tol * max(1.0, np.abs(l_ref).max())
     if scale == 0.0:
         assert max_abs(host(lse)[0], np.log(np.arange(1, S + 1))) <= TOL_F32 * np.log(S)
     for a, b, nm in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
-        assert max_abs(host(a), b) <= TOL_F32 * max(1.0, np.abs(b).max()), nm
+        assert max_abs(host(a), b) <= tol * max(1.0, np.abs(b).max()), nm
 
 
 def torch_reference(q, k, v, scale, dout=None, chunk=16):
