@@ -676,10 +676,10 @@ def main():
                          "config": "BASELINE config 2: B8 H12 T1024 D64 bf16 causal forward"}
     for key, (fk, bk), what in (
             ("fp32_flash", ("f32_fwd", "f32_bwd"),
-             "fp32 flash kernels at fp32 accuracy, config 3 shape: the forward's products on "
-             "the bf16 MFMA as six bf16 cross terms of a three-way split (so its fraction of "
-             "the fp32 MFMA peak can exceed 1; fwd_frac_bf16_peak_executed counts the six "
-             "bf16 products it executes per fp32 product), the backward on the fp32 MFMA"),
+             "fp32 flash kernels at fp32 accuracy, config 3 shape: every product on the "
+             "bf16 MFMA as six bf16 cross terms of a three-way split (so the fractions of the "
+             "fp32 MFMA peak can exceed 1; *_frac_bf16_peak_executed count the six bf16 "
+             "products executed per fp32 product)"),
             ("fp32_materialized", ("mat_fwd", "mat_bwd"),
              "fp32 materialized path (hipBLASLt fp32 strided-batched GEMMs over the full "
              "T x T scores + fused row passes; executes twice the causal FLOPs), config 3 "
@@ -693,6 +693,7 @@ def main():
                       "peak_tflops": PEAK_F32_TFLOPS, "what": what}
         if key == "fp32_flash":
             comps[key]["fwd_frac_bf16_peak_executed"] = round(6 * ftf / PEAK_BF16_TFLOPS, 4)
+            comps[key]["bwd_frac_bf16_peak_executed"] = round(6 * btf / PEAK_BF16_TFLOPS, 4)
     comps["dropout"] = {
         "p": 0.1, "fwd_ms": round(drop_ms[0], 5), "bwd_ms": round(drop_ms[1], 5),
         "fwd_tflops": round(FWD_FLOPS / (drop_ms[0] * 1e-3) / 1e12, 2),

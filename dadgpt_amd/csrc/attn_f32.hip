@@ -1,15 +1,13 @@
 // fp32 causal flash attention at fp32 accuracy on gfx950. This is the reference's precision
 // (cuda/attention.cu:1): forward with online softmax and a saved natural-log logsumexp, backward
-// recomputing the probabilities from it. The forward computes its fp32 products on the bf16
-// matrix cores, each float split into three bf16 values and each product formed from the six
-// cross terms that matter (see X3 below: as accurate as the fp32 MFMA, in 37% of its matrix
-// time, and beside the VALU); the backward uses the fp32 MFMA (v_mfma_f32_32x32x2_f32). The
-// softmax exponentials are exp_acc (below: 1.24 ulp in six VALU operations, the library expf
-// 0.85 in thirteen) and the logsumexp's logarithm is logf; results match float64 to ~1e-6
-// (O, lse) and the fp32 CPU path within its own rounding. On gfx950 the fp32 MFMA and the VALU
-// do not execute side by side, so every VALU instruction of the backward adds to its time;
-// the forward moves its running maximum lazily (as the bf16 forward does) and masking runs
-// only where a chunk needs it.
+// recomputing the probabilities from it. Every fp32 product runs on the bf16 matrix cores,
+// each float split into three bf16 values and each product formed from the six cross terms
+// that matter (see X3 below: as accurate as the fp32 MFMA, in 37% of its matrix time, and
+// beside the VALU, which the fp32 MFMA of gfx950 does not run beside). The softmax
+// exponentials are exp_acc (below: 1.24 ulp in six VALU operations, the library expf 0.85 in
+// thirteen) and the logsumexp's logarithm is logf; results match float64 to ~1e-6 (O, lse)
+// and the fp32 CPU path within its own rounding. The forward moves its running maximum lazily
+// (as the bf16 forward does) and masking runs only where a chunk needs it.
 //
 // Work decomposition (every product a 32 x 32 MFMA tile, one wave per 32 rows):
 //  forward  a wave owns 32 queries (lane l holds query l % 32): S^T = K Q^T over each 32-key
@@ -20,14 +18,14 @@
 //           three bf16 planes each in the bf16 kernels' swizzled layout, read with
 //           ds_read_b128 (K rows) and ds_read_b64_tr_b16 (V^T);
 //  dK/dV    a wave owns 32 keys (lane l holds key l % 32) and walks every later query chunk:
-//           S = Q K^T and dP = dO V^T with K and V in registers, P and dS in registers,
-//           dV^T += dO^T P and dK^T += Q^T dS; nothing is shared between waves (no atomics);
-//  dQ       a wave owns 32 queries again: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T;
+//           S = Q K^T and dP = dO V^T with K and V in registers (floats, split at each use),
+//           Q and dO as bf16 planes, P and dS in registers, dV^T += dO^T P and
+//           dK^T += Q^T dS; nothing is shared between waves (no atomics);
+//  dQ       a wave owns 32 queries again: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T, with
+//           Q split once, dO split at each use and K, V as bf16 planes;
 //  delta    rowsum(dO * O), a separate pass that dK/dV and dQ both read.
-// In the backward the MFMA k-index of the score products runs over d_head as (lane half h,
-// step t) -> d = h * D/2 + t, so every lane reads D/2 contiguous floats of a row. Its tiles of
-// 64 rows are staged in LDS with the row pitch padded by 4 floats. In both directions the next
-// tile is loaded into registers while the current one is on the matrix cores.
+// The next 64-row tile is loaded into registers while the current one is on the matrix cores
+// and split into planes as it is stored.
 //
 // The DROP instantiations apply attention-probability dropout with the keep bits of
 // dropout.hpp: the forward and dQ hold keys along registers (keep_words16), dK/dV holds queries
@@ -48,12 +46,6 @@ constexpr int kWaves = 4;             // waves per workgroup
 constexpr int kMinBlocks = 2;
 constexpr int kRows = 32 * kWaves;    // rows (queries or keys) a workgroup owns
 constexpr int kTile = 64;             // rows per staged tile (two 32-row chunks)
-
-// D(32x32) += A(32x2) B(2x32), fp32. Lane l supplies A[l%32][l/32] and B[l/32][l%32] and
-// receives C[c32_row(r, l/32)][l%32] in element r.
-__device__ __forceinline__ f32x16 mfma32f(float a, float b, const f32x16& c) {
-  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
 
 // Row (within a 32-row chunk) that score register u of lane half h stands for, when the A
 // operand rows were read through sigma32: 16 * (u / 8) + 8 * h + u % 8.
@@ -113,54 +105,6 @@ struct Tile {
     }
   }
 };
-
-// The D/2 floats of row `row` that lane half h supplies as score-product operands.
-template <int D>
-__device__ __forceinline__ void read_half_row(float (&x)[D / 2], const float* lds, int row,
-                                              int h) {
-  const float* p = lds + row * Tile<D>::kPitch + h * (D / 2);
-#pragma unroll
-  for (int i = 0; i < D / 8; ++i) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * i);
-    x[4 * i] = v[0], x[4 * i + 1] = v[1], x[4 * i + 2] = v[2], x[4 * i + 3] = v[3];
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void load_half_row(float (&x)[D / 2], const float* g, int h) {
-#pragma unroll
-  for (int i = 0; i < D / 8; ++i) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(g + h * (D / 2) + 4 * i);
-    x[4 * i] = v[0], x[4 * i + 1] = v[1], x[4 * i + 2] = v[2], x[4 * i + 3] = v[3];
-  }
-}
-
-// acc = sum_t A_t B_t over the D/2 score steps: A rows from LDS (through sigma32), B from the
-// lane's registers.
-template <int D>
-__device__ __forceinline__ f32x16 score_tile(const float* lds, int chunk_row0,
-                                             const float (&b)[D / 2], int lane) {
-  float a[D / 2];
-  read_half_row<D>(a, lds, chunk_row0 + sigma32(lane & 31), lane >> 5);
-  f32x16 acc = zero16();
-#pragma unroll
-  for (int t = 0; t < D / 2; ++t) acc = mfma32f(a[t], b[t], acc);
-  return acc;
-}
-
-// acc[db] += M^T P over one 32-row chunk: A = rows reg_row(u, h) of the LDS tile at columns
-// 32 db + lane%32 (the transposed operand read across a row), B = register u of p.
-template <int D>
-__device__ __forceinline__ void accumulate_t(f32x16 (&acc)[D / 32], const float* lds,
-                                             int chunk_row0, const f32x16& p, int lane) {
-  const int l32 = lane & 31, h = lane >> 5;
-#pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const float* row = lds + (chunk_row0 + reg_row(u, h)) * Tile<D>::kPitch + l32;
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db) acc[db] = mfma32f(row[32 * db], p[u], acc[db]);
-  }
-}
 
 // fp32 products on the bf16 matrix cores. A float x is split into three bf16 values
 // x = x1 + x2 + x3 (each the round-to-nearest of what the previous ones leave, so the three
@@ -227,6 +171,21 @@ __device__ __forceinline__ void store_x3(const Tile<D>& t, bf16* planes) {
   }
 }
 
+// The B operand of a score product from a global row: lane half h supplies columns
+// 16 ds + 8 h + 0..7 of `row`, split into three bf16 planes.
+template <int D>
+__device__ __forceinline__ void load_split_row(X3 (&x)[D / 16], const float* row, int h) {
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds) {
+    float a[8];
+    const f32x4 v0 = *reinterpret_cast<const f32x4*>(row + 16 * ds + 8 * h);
+    const f32x4 v1 = *reinterpret_cast<const f32x4*>(row + 16 * ds + 8 * h + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = v0[e], a[4 + e] = v1[e];
+    x[ds] = split3(a);
+  }
+}
+
 template <int D>
 __device__ __forceinline__ f32x16 score_tile_p(const bf16* planes, int chunk_row0,
                                                const X3 (&qb)[D / 16], int lane) {
@@ -243,27 +202,63 @@ __device__ __forceinline__ f32x16 score_tile_p(const bf16* planes, int chunk_row
   return acc;
 }
 
+// A global row in the B-operand layout of the score products, as floats: element 8 ds + e is
+// column 16 ds + 8 h + e.
+template <int D>
+__device__ __forceinline__ void load_row_b(float (&x)[D / 2], const float* row, int h) {
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds) {
+    const f32x4 v0 = *reinterpret_cast<const f32x4*>(row + 16 * ds + 8 * h);
+    const f32x4 v1 = *reinterpret_cast<const f32x4*>(row + 16 * ds + 8 * h + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[8 * ds + e] = v0[e], x[8 * ds + 4 + e] = v1[e];
+  }
+}
+
+// score_tile_p with the B operand held as floats (the load_split_row layout) and split at
+// each use: for kernels whose registers cannot hold two split rows.
+template <int D>
+__device__ __forceinline__ f32x16 score_tile_pf(const bf16* planes, int chunk_row0,
+                                                const float (&bf)[D / 2], int lane) {
+  const int krow = chunk_row0 + sigma32(lane & 31), hi = lane >> 5;
+  f32x16 acc = zero16();
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds) {
+    X3 a;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+      a.v[pl] = lds_op(planes + pl * kTile * D, rm_off<D>(krow, 2 * ds + hi));
+    float b[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      b[e] = bf[8 * ds + e];
+      // split here, at each use: hoisted out of the tile loop, the splits of a whole row would
+      // hold 1.5x its registers for the kernel's life
+      asm volatile("" : "+v"(b[e]));
+    }
+    acc = mfma_x6(a, split3(b), acc);
+  }
+  return acc;
+}
+
 template <int D>
 __device__ __forceinline__ void accumulate_t_p(f32x16 (&acc)[D / 32], const bf16* planes,
                                                int chunk_row0, const f32x16& p, int lane) {
-  X3 pb[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     float x[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = p[8 * j + e];
-    pb[j] = split3(x);
-  }
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
+    const X3 pb = split3(x);
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
       X3 a;
 #pragma unroll
       for (int pl = 0; pl < 3; ++pl)
         a.v[pl] = lds_tr_op<D>(planes + pl * kTile * D, chunk_row0 + 16 * j, 32 * db, lane);
-      acc[db] = mfma_x6(a, pb[j], acc[db]);
+      acc[db] = mfma_x6(a, pb, acc[db]);
     }
+  }
 }
 
 // Writes a wave's transposed accumulators (element r of lane (l32, h), block db: row l32 of
@@ -291,13 +286,6 @@ __device__ __forceinline__ void store_rows_t(float* dst, int row0, int S,
   }
 }
 
-// The epilogue staging slot of wave w: 32 rows of one of the workgroup's two 64-row tile
-// buffers (waves 0-1 in the first, 2-3 in the second), free once every wave left the tiles.
-template <int D>
-__device__ __forceinline__ float* stage_slot(float* first, float* second, int wave) {
-  return (wave < 2 ? first : second) + (wave & 1) * 32 * Tile<D>::kPitch;
-}
-
 // ------------------------------------------------------------------------------ forward
 
 template <int D, bool DROP>
@@ -320,19 +308,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void fwd_f32_kernel(
   const int last = min(S, (blk + 1) * kRows) - 1;  // the workgroup's last query
   const int n_tiles = last / kTile + 1;
 
-  X3 qb[D / 16];  // the lane's query row, columns 16 ds + 8 h + 0..7, split
-  {
-    const float* qrow = q + base + (size_t)min(qi, S - 1) * D + 8 * h;
-#pragma unroll
-    for (int ds = 0; ds < D / 16; ++ds) {
-      float a[8];
-      const f32x4 v0 = *reinterpret_cast<const f32x4*>(qrow + 16 * ds);
-      const f32x4 v1 = *reinterpret_cast<const f32x4*>(qrow + 16 * ds + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) a[e] = v0[e], a[4 + e] = v1[e];
-      qb[ds] = split3(a);
-    }
-  }
+  X3 qb[D / 16];  // the lane's query row, split
+  load_split_row<D>(qb, q + base + (size_t)min(qi, S - 1) * D, h);
   f32x16 o[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) o[db] = zero16();
@@ -440,8 +417,9 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
     const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, float scale,
     const DropParams dr) {
-  __shared__ __attribute__((aligned(16))) float sq[kTile * Tile<D>::kPitch];
-  __shared__ __attribute__((aligned(16))) float sg[kTile * Tile<D>::kPitch];
+  // Q and dO tiles as three bf16 planes each (see the forward)
+  __shared__ __attribute__((aligned(16))) bf16 sqp[3 * kTile * D];
+  __shared__ __attribute__((aligned(16))) bf16 sgp[3 * kTile * D];
   // per query row of the tile: lse, and delta * scale
   __shared__ __attribute__((aligned(16))) float sl[kTile], sd[kTile];
   const int bh = blockIdx.x, blk = blockIdx.y;  // early key blocks see the most queries: first
@@ -453,9 +431,10 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
   const int t0 = (blk * kRows) / kTile;    // first query tile with a query >= the first key
   const int n_tiles = (S + kTile - 1) / kTile;
 
-  float kr[D / 2], vr[D / 2];
-  load_half_row<D>(kr, k + base + (size_t)min(kj, S - 1) * D, h);
-  load_half_row<D>(vr, v + base + (size_t)min(kj, S - 1) * D, h);
+  // the lane's K and V rows (score-product B layout), split at each use
+  float kf[D / 2], vf[D / 2];
+  load_row_b<D>(kf, k + base + (size_t)min(kj, S - 1) * D, h);
+  load_row_b<D>(vf, v + base + (size_t)min(kj, S - 1) * D, h);
   f32x16 dka[D / 32], dva[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) dka[db] = zero16(), dva[db] = zero16();
@@ -472,8 +451,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
   load_stats(t0 * kTile);
   for (int t = t0; t < n_tiles; ++t) {
     __syncthreads();
-    tq.store(sq);
-    tg.store(sg);
+    store_x3<D>(tq, sqp);
+    store_x3<D>(tg, sgp);
     if (threadIdx.x < kTile) sl[threadIdx.x] = pl, sd[threadIdx.x] = pd * scale;
     __syncthreads();
     if (t + 1 < n_tiles) {
@@ -486,8 +465,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
       const int qrow0 = t * kTile + 32 * c;
       if (qrow0 + 31 < k0) continue;  // wave-uniform: every query of the chunk precedes every key
       // lane (l32, h), register u: query qrow0 + reg_row(u, h), key kj
-      f32x16 s = score_tile<D>(sq, 32 * c, kr, lane);   // Q K^T
-      f32x16 dp = score_tile<D>(sg, 32 * c, vr, lane);  // dO V^T
+      f32x16 s = score_tile_pf<D>(sqp, 32 * c, kf, lane);   // Q K^T
+      f32x16 dp = score_tile_pf<D>(sgp, 32 * c, vf, lane);  // dO V^T
       uint32_t keep = 0;
       if constexpr (DROP) keep = keep_col16(dr, (uint64_t)bh * S + qrow0, k0, lane);
       // Statistics of the chunk's rows 32c + reg_row(u, h): registers 8j..8j+7 are the 8
@@ -521,12 +500,12 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
         }
         dp[u] = p * fmaf(g, scale, -ds[u]);  // P (dP - delta) scale
       }
-      accumulate_t<D>(dva, sg, 32 * c, s, lane);   // dV^T += dO^T P
-      accumulate_t<D>(dka, sq, 32 * c, dp, lane);  // dK^T += Q^T dS
+      accumulate_t_p<D>(dva, sgp, 32 * c, s, lane);   // dV^T += dO^T P
+      accumulate_t_p<D>(dka, sqp, 32 * c, dp, lane);  // dK^T += Q^T dS
     }
   }
   __syncthreads();
-  float* stage = stage_slot<D>(sq, sg, wave);
+  float* stage = reinterpret_cast<float*>(wave < 2 ? sqp : sgp) + (wave & 1) * 32 * Tile<D>::kPitch;
   store_rows_t<D>(dk + base, k0, S, dka, 1.0f, stage, lane);
   store_rows_t<D>(dv + base, k0, S, dva, 1.0f, stage, lane);  // after the wave's dK reads
 }
@@ -536,8 +515,9 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
     float* __restrict__ dq, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta, int S, float scale, const DropParams dr) {
-  __shared__ __attribute__((aligned(16))) float sk[kTile * Tile<D>::kPitch];
-  __shared__ __attribute__((aligned(16))) float sv[kTile * Tile<D>::kPitch];
+  // K and V tiles as three bf16 planes each (see the forward)
+  __shared__ __attribute__((aligned(16))) bf16 skp[3 * kTile * D];
+  __shared__ __attribute__((aligned(16))) bf16 svp[3 * kTile * D];
   const int bh = blockIdx.x;
   const int blk = gridDim.y - 1 - blockIdx.y;  // longest query blocks first
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
@@ -549,9 +529,11 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
   const int last = min(S, (blk + 1) * kRows) - 1;
   const int n_tiles = last / kTile + 1;
 
-  float qr[D / 2], gr[D / 2];
-  load_half_row<D>(qr, q + base + (size_t)qc * D, h);
-  load_half_row<D>(gr, dout + base + (size_t)qc * D, h);
+  // the lane's Q row split once, its dO row (columns 16 ds + 8 h + 0..7) split at each use
+  X3 qb[D / 16];
+  load_split_row<D>(qb, q + base + (size_t)qc * D, h);
+  float gf[D / 2];
+  load_row_b<D>(gf, dout + base + (size_t)qc * D, h);
   const float my_lse = lse[(size_t)bh * S + qc];
   const float my_dscale = delta[(size_t)bh * S + qc] * scale;
   f32x16 acc[D / 32];
@@ -563,8 +545,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
   tv.load(v + base, 0, S);
   for (int t = 0; t < n_tiles; ++t) {
     __syncthreads();
-    tk.store(sk);
-    tv.store(sv);
+    store_x3<D>(tk, skp);
+    store_x3<D>(tv, svp);
     __syncthreads();
     if (t + 1 < n_tiles) {
       tk.load(k + base, (t + 1) * kTile, S);
@@ -575,8 +557,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
       const int key0 = t * kTile + 32 * c;
       if (key0 > q0 + 31) continue;
       // lane (l32, h), register u: query qi, key key0 + reg_row(u, h)
-      f32x16 s = score_tile<D>(sk, 32 * c, qr, lane);   // K Q^T
-      f32x16 dp = score_tile<D>(sv, 32 * c, gr, lane);  // V dO^T
+      f32x16 s = score_tile_p<D>(skp, 32 * c, qb, lane);   // K Q^T
+      f32x16 dp = score_tile_pf<D>(svp, 32 * c, gf, lane);  // V dO^T
       KeepWords16 keep = {};
       if constexpr (DROP) keep = keep_words16(dr, (uint64_t)bh * S + qi, key0, h);
       // only the chunk whose first key is the wave's first query holds keys after a query (or
@@ -596,11 +578,12 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
         if constexpr (DROP) g *= keep_factor(keep, u, dr);
         s[u] = p * fmaf(g, scale, -my_dscale);  // P (dP - delta) scale
       }
-      accumulate_t<D>(acc, sk, 32 * c, s, lane);  // dQ^T += K^T dS^T
+      accumulate_t_p<D>(acc, skp, 32 * c, s, lane);  // dQ^T += K^T dS^T
     }
   }
   __syncthreads();
-  store_rows_t<D>(dq + base, q0, S, acc, 1.0f, stage_slot<D>(sk, sv, wave), lane);
+  float* stage = reinterpret_cast<float*>(wave < 2 ? skp : svp) + (wave & 1) * 32 * Tile<D>::kPitch;
+  store_rows_t<D>(dq + base, q0, S, acc, 1.0f, stage, lane);
 }
 
 template <int D>
