@@ -24,8 +24,9 @@
 //  dQ       a wave owns 32 queries again: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T, with
 //           Q split once, dO split at each use and K, V as bf16 planes;
 //  delta    rowsum(dO * O), a separate pass that dK/dV and dQ both read.
-// The next 64-row tile is loaded into registers while the current one is on the matrix cores
-// and split into planes as it is stored.
+// The next tile is loaded into registers while the current one is on the matrix cores and
+// split into planes as it is stored: 64 rows in the forward, 32 in dK/dV and dQ, where the
+// prefetch registers are needed for the operands.
 //
 // The DROP instantiations apply attention-probability dropout with the keep bits of
 // dropout.hpp: the forward and dQ hold keys along registers (keep_words16), dK/dV holds queries
@@ -40,9 +41,9 @@ namespace dadgpt {
 namespace {
 
 constexpr int kWaves = 4;             // waves per workgroup
-// Two workgroups per CU, i.e. at most 256 registers a lane: dK/dV would otherwise take 320 and
-// run one wave per SIMD. With the cap nothing spills at D = 64 except 4 registers of the
-// dropout dK/dV, and the backward runs 15% faster (the forward 3%).
+// Two workgroups per CU, i.e. at most 256 registers a lane (one wave per SIMD runs the backward
+// ~15% slower). At D = 64 the forward and dQ fit; dK/dV spills 5 registers (26 with dropout),
+// loop-invariant values reloaded once per chunk.
 constexpr int kMinBlocks = 2;
 constexpr int kRows = 32 * kWaves;    // rows (queries or keys) a workgroup owns
 constexpr int kTile = 64;             // rows per staged tile (two 32-row chunks)
@@ -80,12 +81,13 @@ __device__ __forceinline__ float exp_acc(float x) {
 // weights below 2^64, the running sums stay far inside fp32 range over any sequence length.
 constexpr float kMaxW = 0x1p64f;
 
-// A 64-row fp32 tile in LDS (pitch D + 4 floats) and its register prefetch: 256 threads, D/16
-// 16-byte pieces each; rows at or past S read as zeros.
-template <int D>
+// A TR-row fp32 tile (64 rows in the forward, 32 in the backward kernels, whose registers are
+// scarcer) and its register prefetch: 256 threads, TR*D/1024 16-byte pieces each; rows at or
+// past S read as zeros. Epilogues stage rows at pitch D + 4 floats.
+template <int D, int TR = kTile>
 struct Tile {
   static constexpr int kPitch = D + 4;
-  static constexpr int kPieces = kTile * D / 4 / 256;
+  static constexpr int kPieces = TR * D / 4 / 256;
   f32x4 r[kPieces];
 
   __device__ __forceinline__ void load(const float* src, int row0, int S) {
@@ -148,10 +150,10 @@ __device__ __forceinline__ f32x16 mfma_x6(const X3& a, const X3& b, f32x16 acc) 
 // the bf16 kernels (tiles.hpp), so the score operands are ds_read_b128 and the transposed
 // ones ds_read_b64_tr_b16 reads. Each float is split once per workgroup, when the tile is
 // staged, instead of once per wave that reads it.
-template <int D>
-__device__ __forceinline__ void store_x3(const Tile<D>& t, bf16* planes) {
+template <int D, int TR = kTile>
+__device__ __forceinline__ void store_x3(const Tile<D, TR>& t, bf16* planes) {
 #pragma unroll
-  for (int i = 0; i < Tile<D>::kPieces; ++i) {
+  for (int i = 0; i < Tile<D, TR>::kPieces; ++i) {
     const int u = threadIdx.x + 256 * i, row = u / (D / 4), c = u % (D / 4);
     const int off = rm_off<D>(row, c >> 1) + 4 * (c & 1);  // 4 floats: half a 16-byte chunk
     uint32_t w[3][2];
@@ -167,7 +169,7 @@ __device__ __forceinline__ void store_x3(const Tile<D>& t, bf16* planes) {
     }
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl)
-      *reinterpret_cast<u32x2*>(planes + pl * kTile * D + off) = u32x2{w[pl][0], w[pl][1]};
+      *reinterpret_cast<u32x2*>(planes + pl * TR * D + off) = u32x2{w[pl][0], w[pl][1]};
   }
 }
 
@@ -186,7 +188,7 @@ __device__ __forceinline__ void load_split_row(X3 (&x)[D / 16], const float* row
   }
 }
 
-template <int D>
+template <int D, int TR = kTile>
 __device__ __forceinline__ f32x16 score_tile_p(const bf16* planes, int chunk_row0,
                                                const X3 (&qb)[D / 16], int lane) {
   const int krow = chunk_row0 + sigma32(lane & 31), hi = lane >> 5;
@@ -196,7 +198,7 @@ __device__ __forceinline__ f32x16 score_tile_p(const bf16* planes, int chunk_row
     X3 a;
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl)
-      a.v[pl] = lds_op(planes + pl * kTile * D, rm_off<D>(krow, 2 * ds + hi));
+      a.v[pl] = lds_op(planes + pl * TR * D, rm_off<D>(krow, 2 * ds + hi));
     acc = mfma_x6(a, qb[ds], acc);
   }
   return acc;
@@ -217,7 +219,7 @@ __device__ __forceinline__ void load_row_b(float (&x)[D / 2], const float* row, 
 
 // score_tile_p with the B operand held as floats (the load_split_row layout) and split at
 // each use: for kernels whose registers cannot hold two split rows.
-template <int D>
+template <int D, int TR = kTile>
 __device__ __forceinline__ f32x16 score_tile_pf(const bf16* planes, int chunk_row0,
                                                 const float (&bf)[D / 2], int lane) {
   const int krow = chunk_row0 + sigma32(lane & 31), hi = lane >> 5;
@@ -227,7 +229,7 @@ __device__ __forceinline__ f32x16 score_tile_pf(const bf16* planes, int chunk_ro
     X3 a;
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl)
-      a.v[pl] = lds_op(planes + pl * kTile * D, rm_off<D>(krow, 2 * ds + hi));
+      a.v[pl] = lds_op(planes + pl * TR * D, rm_off<D>(krow, 2 * ds + hi));
     float b[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -241,7 +243,7 @@ __device__ __forceinline__ f32x16 score_tile_pf(const bf16* planes, int chunk_ro
   return acc;
 }
 
-template <int D>
+template <int D, int TR = kTile>
 __device__ __forceinline__ void accumulate_t_p(f32x16 (&acc)[D / 32], const bf16* planes,
                                                int chunk_row0, const f32x16& p, int lane) {
 #pragma unroll
@@ -255,7 +257,7 @@ __device__ __forceinline__ void accumulate_t_p(f32x16 (&acc)[D / 32], const bf16
       X3 a;
 #pragma unroll
       for (int pl = 0; pl < 3; ++pl)
-        a.v[pl] = lds_tr_op<D>(planes + pl * kTile * D, chunk_row0 + 16 * j, 32 * db, lane);
+        a.v[pl] = lds_tr_op<D>(planes + pl * TR * D, chunk_row0 + 16 * j, 32 * db, lane);
       acc[db] = mfma_x6(a, pb, acc[db]);
     }
   }
@@ -417,19 +419,23 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
     const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, float scale,
     const DropParams dr) {
-  // Q and dO tiles as three bf16 planes each (see the forward)
-  __shared__ __attribute__((aligned(16))) bf16 sqp[3 * kTile * D];
-  __shared__ __attribute__((aligned(16))) bf16 sgp[3 * kTile * D];
+  // Q and dO tiles of TR rows as three bf16 planes each (see the forward); each array also
+  // holds two waves' epilogue staging
+  constexpr int TR = 32;
+  constexpr int kLds = 3 * TR * D > 4 * 32 * Tile<D>::kPitch ? 3 * TR * D
+                                                               : 4 * 32 * Tile<D>::kPitch;
+  __shared__ __attribute__((aligned(16))) bf16 sqp[kLds];
+  __shared__ __attribute__((aligned(16))) bf16 sgp[kLds];
   // per query row of the tile: lse, and delta * scale
-  __shared__ __attribute__((aligned(16))) float sl[kTile], sd[kTile];
+  __shared__ __attribute__((aligned(16))) float sl[TR], sd[TR];
   const int bh = blockIdx.x, blk = blockIdx.y;  // early key blocks see the most queries: first
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar
   const size_t base = (size_t)bh * S * D;
   const int k0 = blk * kRows + 32 * wave;  // the wave's first key
   const int kj = k0 + l32;                 // this lane's key
-  const int t0 = (blk * kRows) / kTile;    // first query tile with a query >= the first key
-  const int n_tiles = (S + kTile - 1) / kTile;
+  const int t0 = (blk * kRows) / TR;  // first query tile with a query >= the first key
+  const int n_tiles = (S + TR - 1) / TR;
 
   // the lane's K and V rows (score-product B layout), split at each use
   float kf[D / 2], vf[D / 2];
@@ -439,69 +445,68 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) dka[db] = zero16(), dva[db] = zero16();
 
-  Tile<D> tq, tg;
+  Tile<D, TR> tq, tg;
   float pl = 0.f, pd = 0.f;
   auto load_stats = [&](int row0) {
-    const int r = row0 + (threadIdx.x & 63);
+    const int r = row0 + (threadIdx.x & (TR - 1));
     pl = r < S ? lse[(size_t)bh * S + r] : 0.f;
     pd = r < S ? delta[(size_t)bh * S + r] : 0.f;
   };
-  tq.load(q + base, t0 * kTile, S);
-  tg.load(dout + base, t0 * kTile, S);
-  load_stats(t0 * kTile);
+  tq.load(q + base, t0 * TR, S);
+  tg.load(dout + base, t0 * TR, S);
+  load_stats(t0 * TR);
   for (int t = t0; t < n_tiles; ++t) {
     __syncthreads();
-    store_x3<D>(tq, sqp);
-    store_x3<D>(tg, sgp);
-    if (threadIdx.x < kTile) sl[threadIdx.x] = pl, sd[threadIdx.x] = pd * scale;
+    store_x3<D, TR>(tq, sqp);
+    store_x3<D, TR>(tg, sgp);
+    if (threadIdx.x < TR) sl[threadIdx.x] = pl, sd[threadIdx.x] = pd * scale;
     __syncthreads();
     if (t + 1 < n_tiles) {
-      tq.load(q + base, (t + 1) * kTile, S);
-      tg.load(dout + base, (t + 1) * kTile, S);
-      load_stats((t + 1) * kTile);
+      tq.load(q + base, (t + 1) * TR, S);
+      tg.load(dout + base, (t + 1) * TR, S);
+      load_stats((t + 1) * TR);
     }
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int qrow0 = t * kTile + 32 * c;
+    for (int c = 0; c < TR / 32; ++c) {
+      const int qrow0 = t * TR + 32 * c;
       if (qrow0 + 31 < k0) continue;  // wave-uniform: every query of the chunk precedes every key
       // lane (l32, h), register u: query qrow0 + reg_row(u, h), key kj
-      f32x16 s = score_tile_pf<D>(sqp, 32 * c, kf, lane);   // Q K^T
-      f32x16 dp = score_tile_pf<D>(sgp, 32 * c, vf, lane);  // dO V^T
+      f32x16 s = score_tile_pf<D, TR>(sqp, 32 * c, kf, lane);   // Q K^T
+      f32x16 dp = score_tile_pf<D, TR>(sgp, 32 * c, vf, lane);  // dO V^T
       uint32_t keep = 0;
       if constexpr (DROP) keep = keep_col16(dr, (uint64_t)bh * S + qrow0, k0, lane);
       // Statistics of the chunk's rows 32c + reg_row(u, h): registers 8j..8j+7 are the 8
       // consecutive rows 32c + 16j + 8h .., two 16-byte LDS reads each.
-      float ls[16], ds[16];
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int r = 32 * c + 16 * j + 8 * h + 4 * i;
-          const f32x4 a = *reinterpret_cast<const f32x4*>(sl + r);
-          const f32x4 b = *reinterpret_cast<const f32x4*>(sd + r);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) ls[8 * j + 4 * i + e] = a[e], ds[8 * j + 4 * i + e] = b[e];
-        }
       // keys after a query, or rows past S, only where the chunk reaches the wave's first
       // keys or S (wave-uniform)
       const bool mask = qrow0 < k0 + 31 || qrow0 + 31 >= S;
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int qrow = qrow0 + reg_row(u, h);
-        float p = exp_acc(fmaf(s[u], scale, -ls[u]));
-        if (mask && !(kj <= qrow && qrow < S)) p = 0.f;
-        float g = dp[u];
-        if constexpr (DROP) {
-          const float f = keep_factor(keep, u, dr.scale);
-          g *= f;
-          s[u] = p * f;  // the probability that multiplied V
-        } else {
-          s[u] = p;
+      for (int g4 = 0; g4 < 4; ++g4) {
+        // registers 4 g4 .. 4 g4 + 3 are the consecutive rows 32c + 16(g4/2) + 8h + 4(g4%2) ..;
+        // their statistics are read here, four at a time, rather than all ahead of the loop
+        const int r = 32 * c + 16 * (g4 >> 1) + 8 * h + 4 * (g4 & 1);
+        asm volatile("" ::: "memory");
+        const f32x4 ls = *reinterpret_cast<const f32x4*>(sl + r);
+        const f32x4 ds = *reinterpret_cast<const f32x4*>(sd + r);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int u = 4 * g4 + e;
+          const int qrow = qrow0 + reg_row(u, h);
+          float p = exp_acc(fmaf(s[u], scale, -ls[e]));
+          if (mask && !(kj <= qrow && qrow < S)) p = 0.f;
+          float g = dp[u];
+          if constexpr (DROP) {
+            const float f = keep_factor(keep, u, dr.scale);
+            g *= f;
+            s[u] = p * f;  // the probability that multiplied V
+          } else {
+            s[u] = p;
+          }
+          dp[u] = p * fmaf(g, scale, -ds[e]);  // P (dP - delta) scale
         }
-        dp[u] = p * fmaf(g, scale, -ds[u]);  // P (dP - delta) scale
       }
-      accumulate_t_p<D>(dva, sgp, 32 * c, s, lane);   // dV^T += dO^T P
-      accumulate_t_p<D>(dka, sqp, 32 * c, dp, lane);  // dK^T += Q^T dS
+      accumulate_t_p<D, TR>(dva, sgp, 32 * c, s, lane);   // dV^T += dO^T P
+      accumulate_t_p<D, TR>(dka, sqp, 32 * c, dp, lane);  // dK^T += Q^T dS
     }
   }
   __syncthreads();
@@ -515,9 +520,13 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
     float* __restrict__ dq, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta, int S, float scale, const DropParams dr) {
-  // K and V tiles as three bf16 planes each (see the forward)
-  __shared__ __attribute__((aligned(16))) bf16 skp[3 * kTile * D];
-  __shared__ __attribute__((aligned(16))) bf16 svp[3 * kTile * D];
+  // K and V tiles of TR rows as three bf16 planes each (see the forward); each array also
+  // holds two waves' epilogue staging
+  constexpr int TR = 32;
+  constexpr int kLds = 3 * TR * D > 4 * 32 * Tile<D>::kPitch ? 3 * TR * D
+                                                               : 4 * 32 * Tile<D>::kPitch;
+  __shared__ __attribute__((aligned(16))) bf16 skp[kLds];
+  __shared__ __attribute__((aligned(16))) bf16 svp[kLds];
   const int bh = blockIdx.x;
   const int blk = gridDim.y - 1 - blockIdx.y;  // longest query blocks first
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
@@ -527,7 +536,7 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
   const int qi = q0 + l32;
   const int qc = min(qi, S - 1);
   const int last = min(S, (blk + 1) * kRows) - 1;
-  const int n_tiles = last / kTile + 1;
+  const int n_tiles = last / TR + 1;
 
   // the lane's Q row split once, its dO row (columns 16 ds + 8 h + 0..7) split at each use
   X3 qb[D / 16];
@@ -540,25 +549,25 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
 
-  Tile<D> tk, tv;
+  Tile<D, TR> tk, tv;
   tk.load(k + base, 0, S);
   tv.load(v + base, 0, S);
   for (int t = 0; t < n_tiles; ++t) {
     __syncthreads();
-    store_x3<D>(tk, skp);
-    store_x3<D>(tv, svp);
+    store_x3<D, TR>(tk, skp);
+    store_x3<D, TR>(tv, svp);
     __syncthreads();
     if (t + 1 < n_tiles) {
-      tk.load(k + base, (t + 1) * kTile, S);
-      tv.load(v + base, (t + 1) * kTile, S);
+      tk.load(k + base, (t + 1) * TR, S);
+      tv.load(v + base, (t + 1) * TR, S);
     }
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int key0 = t * kTile + 32 * c;
+    for (int c = 0; c < TR / 32; ++c) {
+      const int key0 = t * TR + 32 * c;
       if (key0 > q0 + 31) continue;
       // lane (l32, h), register u: query qi, key key0 + reg_row(u, h)
-      f32x16 s = score_tile_p<D>(skp, 32 * c, qb, lane);   // K Q^T
-      f32x16 dp = score_tile_pf<D>(svp, 32 * c, gf, lane);  // V dO^T
+      f32x16 s = score_tile_p<D, TR>(skp, 32 * c, qb, lane);   // K Q^T
+      f32x16 dp = score_tile_pf<D, TR>(svp, 32 * c, gf, lane);  // V dO^T
       KeepWords16 keep = {};
       if constexpr (DROP) keep = keep_words16(dr, (uint64_t)bh * S + qi, key0, h);
       // only the chunk whose first key is the wave's first query holds keys after a query (or
@@ -578,7 +587,7 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dq_f32_kernel(
         if constexpr (DROP) g *= keep_factor(keep, u, dr);
         s[u] = p * fmaf(g, scale, -my_dscale);  // P (dP - delta) scale
       }
-      accumulate_t_p<D>(acc, skp, 32 * c, s, lane);  // dQ^T += K^T dS^T
+      accumulate_t_p<D, TR>(acc, skp, 32 * c, s, lane);  // dQ^T += K^T dS^T
     }
   }
   __syncthreads();
