@@ -578,3 +578,24 @@ def test_bf16_long_sequence(gpu, D):
     ref = oracle.attn_bwd(gn, qn, kn, vn, scale, threads=2)[:3]
     for a, b, nm in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
         assert max_abs(host(a), b) <= TOL_GRAD, nm
+
+
+@pytest.mark.parametrize("D", [64, 32])
+def test_fp32_long_sequence(gpu, D):
+    """fp32 at S = 2048: 64 query tiles of 32 rows in dK/dV and key tiles in dQ, 32 of 64 rows
+    in the forward, and fp32 sums over rows twice the configs' length. The bound is relative
+    to the largest reference value: the gradients are sums over up to 2048 rows."""
+    BH, S = 2, 2048
+    case(f"fp32 long sequence BH={BH} S={S} D={D}")
+    qn, kn, vn, gn = synth.attn_inputs(BH, S, D, seed=4096 + D, with_dout=True)
+    scale = scale_of(D)
+    q, k, v, g = (dev(x, torch.float32) for x in (qn, kn, vn, gn))
+    out, lse = A.attention_forward(q, k, v, scale)
+    dq, dk, dv, _ = A.attention_backward(g, out, lse, q, k, v, scale)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oracle.attn_fwd(qn, kn, vn, scale, threads=8)
+    assert max_abs(host(out), o_ref) <= TOL_F32 * max(1.0, np.abs(o_ref).max())
+    assert max_abs(host(lse), l_ref) <= TOL_F32 * max(1.0, np.abs(l_ref).max())
+    ref = oracle.attn_bwd(gn, qn, kn, vn, scale, threads=8)[:3]
+    for a, b, nm in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+        assert max_abs(host(a), b) <= TOL_F32 * max(1.0, np.abs(b).max()), nm
