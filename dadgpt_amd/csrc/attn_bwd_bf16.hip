@@ -32,13 +32,19 @@ namespace {
 
 constexpr int kWaves = 4;
 // Workgroups per CU the registers are sized for (4 waves each: 2 -> 256 VGPRs, 3 -> 168).
+// The plain dK/dV kernel fits 168 with its LDS addresses derived at use (DkdvLds below);
+// the dropout and strided ones keep 256.
 #ifndef DADGPT_DKDV_MINB
 #define DADGPT_DKDV_MINB 2
+#endif
+#ifndef DADGPT_DKDV_MINB_PLAIN
+#define DADGPT_DKDV_MINB_PLAIN 3
 #endif
 #ifndef DADGPT_DQ_MINB
 #define DADGPT_DQ_MINB 3
 #endif
 constexpr int kDkdvMinBlocks = DADGPT_DKDV_MINB;
+constexpr int kDkdvMinBlocksPlain = DADGPT_DKDV_MINB_PLAIN;
 constexpr int kDqMinBlocks = DADGPT_DQ_MINB;
 
 // ---------------------------------------------------------------- delta
@@ -101,13 +107,57 @@ constexpr int kKW = 32;  // keys per wave
 //
 // With dropout (DROP; f = keep/(1-p) from bit 8j+e of `keep`): dV accumulates (P f)^T dO and
 // dS = P (dP f - delta), so dp starts from zero and -delta is read separately.
-template <int D, bool DROP>
+// Per-lane LDS byte offsets, within a tile, of dK/dV's operand reads, from which every read of
+// a block is one XOR and an immediate offset away. Row reads (row 32qb + sigma32(l32), chunk
+// 2ds + hi): ro ^ 32ds, because the swizzle XORs the chunk index and 2ds + hi = 2ds ^ hi.
+// Transposed reads of half h (rows 32qb + 16j + ..., columns 32db + ...): tr[h] ^ 64db, the
+// column block flipping chunk bit 2; 32qb and 16j add whole rows, which leave the swizzle alone.
+// The XORs are issued where they are used (volatile asm), so three registers stay live instead
+// of every derived address, which the compiler otherwise hoists out of the tile loop: this is
+// what brings the plain kernel to 168 VGPRs (three workgroups per CU) without spilling in the
+// loop.
+struct DkdvLds {
+  uint32_t ro, tr[2];
+};
+template <int D>
+__device__ __forceinline__ DkdvLds dkdv_lds(int lane) {
+  DkdvLds o;
+  const int l32 = lane & 31, hi = lane >> 5, g = lane >> 4;
+  o.ro = 2u * (uint32_t)rm_off<D>(sigma32(l32), hi);
+  const int cl = 16 * (g & 1) + 4 * (lane & 3);  // the lane's column within a 32-column block
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int rl = 8 * (g >> 1) + 4 * h + ((lane >> 2) & 3);  // its row within 16 rows
+    o.tr[h] = 2u * (uint32_t)(rl * D + (((cl >> 3) ^ swz<D>(rl)) << 3) + (cl & 7));
+  }
+  return o;
+}
+__device__ __forceinline__ uint32_t xor_at_use(uint32_t x, uint32_t m) {
+  if (m == 0) return x;
+  uint32_t r;
+  asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "v"(x), "s"(m));
+  return r;
+}
+__device__ __forceinline__ bf16x8 lds_row_at(const bf16* base, uint32_t byte_off) {
+  return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+// lds_tr_op's read, at byte offsets (within `base`) of its two halves
+__device__ __forceinline__ bf16x8 lds_tr_at(const bf16* base, uint32_t off0, uint32_t off1) {
+  const lds_bf16* t = (const lds_bf16*)base;
+  const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + off0 / 2));
+  const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + off1 / 2));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// XA: operand addresses from `lo` (DkdvLds) instead of computed per read.
+template <int D, bool DROP, bool XA>
 __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
                                            f32x16 (&dvacc)[D / 32], const bf16x8 (&kop)[D / 16],
                                            const bf16x8 (&vop)[D / 16], const bf16* sq,
                                            const bf16* sdo, const float* slc, const float* sdl,
                                            int qb, int key_minus_r0, int rows_left, int lane,
-                                           float c, uint32_t keep, float dscale) {
+                                           float c, uint32_t keep, float dscale,
+                                           const DkdvLds& lo) {
   constexpr int DS = D / 16, DB = D / 32;
   const int l32 = lane & 31, hi = lane >> 5;
   const int qr = 32 * qb + sigma32(l32);
@@ -129,7 +179,9 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
   {
     bf16x8 qa[DS];
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) qa[ds] = lds_op(sq, rm_off<D>(qr, 2 * ds + hi));
+    for (int ds = 0; ds < DS; ++ds)
+      qa[ds] = XA ? lds_row_at(sq + 32 * qb * D, xor_at_use(lo.ro, 32u * ds))
+                  : lds_op(sq, rm_off<D>(qr, 2 * ds + hi));
     stats(slc, s);
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) s = mfma32(qa[ds], kop[ds], s);
@@ -137,7 +189,9 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
   {
     bf16x8 da[DS];
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) da[ds] = lds_op(sdo, rm_off<D>(qr, 2 * ds + hi));
+    for (int ds = 0; ds < DS; ++ds)
+      da[ds] = XA ? lds_row_at(sdo + 32 * qb * D, xor_at_use(lo.ro, 32u * ds))
+                  : lds_op(sdo, rm_off<D>(qr, 2 * ds + hi));
     if constexpr (DROP)
       dp = f32x16{};
     else
@@ -190,7 +244,10 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) t[db][j] = lds_tr_op<D>(sdo, 32 * qb + 16 * j, 32 * db, lane);
+      for (int j = 0; j < 2; ++j)
+        t[db][j] = XA ? lds_tr_at(sdo + (32 * qb + 16 * j) * D, xor_at_use(lo.tr[0], 64u * db),
+                                  xor_at_use(lo.tr[1], 64u * db))
+                      : lds_tr_op<D>(sdo, 32 * qb + 16 * j, 32 * db, lane);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -201,7 +258,10 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) t[db][j] = lds_tr_op<D>(sq, 32 * qb + 16 * j, 32 * db, lane);
+      for (int j = 0; j < 2; ++j)
+        t[db][j] = XA ? lds_tr_at(sq + (32 * qb + 16 * j) * D, xor_at_use(lo.tr[0], 64u * db),
+                                  xor_at_use(lo.tr[1], 64u * db))
+                      : lds_tr_op<D>(sq, 32 * qb + 16 * j, 32 * db, lane);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -210,7 +270,8 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
 }
 
 template <int D, bool STRIDED, bool DROP>
-__global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
+__global__ __launch_bounds__(64 * kWaves, (DROP || STRIDED) ? kDkdvMinBlocks
+                                                            : kDkdvMinBlocksPlain) void dkdv_bf16_kernel(
     bf16* __restrict__ dk, bf16* __restrict__ dv, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, float c,
@@ -260,6 +321,9 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
     dkacc[db] = f32x16{};
     dvacc[db] = f32x16{};
   }
+  constexpr bool XA = !(DROP || STRIDED);
+  DkdvLds lo{};
+  if constexpr (XA) lo = dkdv_lds<D>(lane);
 
   // Direct loads per wave per tile: its share of Q and dO, and its own lse and delta rows.
   using Dma = DmaTile<D, kWaves>;
@@ -298,9 +362,9 @@ __global__ __launch_bounds__(64 * kWaves, kDkdvMinBlocks) void dkdv_bf16_kernel(
         uint32_t keep = 0;
         if constexpr (DROP) keep = keep_col16(dr, (uint64_t)bh * S + qlo, kw0, lane);
         // some key after some query, or rows past S: mask
-        dkdv_block<D, DROP>(edge || qlo < kw0 + kKW - 1, dkacc, dvacc, kop, vop, cq, cdo,
-                            st[cb][0], st[cb][1], qb, key - r0, S - r0, lane, c, keep,
-                            dr.scale);
+        dkdv_block<D, DROP, XA>(edge || qlo < kw0 + kKW - 1, dkacc, dvacc, kop, vop, cq, cdo,
+                                st[cb][0], st[cb][1], qb, key - r0, S - r0, lane, c, keep,
+                                dr.scale, lo);
       }
     }
     wait_vm_lds<0>();
