@@ -112,10 +112,10 @@ constexpr int kKW = 32;  // keys per wave
 // 2ds + hi): ro ^ 32ds, because the swizzle XORs the chunk index and 2ds + hi = 2ds ^ hi.
 // Transposed reads of half h (rows 32qb + 16j + ..., columns 32db + ...): tr[h] ^ 64db, the
 // column block flipping chunk bit 2; 32qb and 16j add whole rows, which leave the swizzle alone.
-// The XORs are issued where they are used (volatile asm), so three registers stay live instead
-// of every derived address, which the compiler otherwise hoists out of the tile loop: this is
-// what brings the plain kernel to 168 VGPRs (three workgroups per CU) without spilling in the
-// loop.
+// The XORs are issued once per block (volatile asm, dkdv_row_addr and dkdv_tr_addr), so three registers stay live
+// across the tile loop instead of every derived address, which the compiler otherwise hoists
+// out of it: this is what brings the plain kernel to 168 VGPRs (three workgroups per CU)
+// without spilling in the loop.
 struct DkdvLds {
   uint32_t ro, tr[2];
 };
@@ -132,11 +132,27 @@ __device__ __forceinline__ DkdvLds dkdv_lds(int lane) {
   }
   return o;
 }
-__device__ __forceinline__ uint32_t xor_at_use(uint32_t x, uint32_t m) {
-  if (m == 0) return x;
-  uint32_t r;
-  asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "v"(x), "s"(m));
-  return r;
+// The addresses one block reads, derived once per block (volatile: not hoisted out of the
+// tile loop), each set right before the phase that reads it. Row reads: ro ^ {0, 32, 64, 96}
+// (D = 64; ro ^ {0, 32} for D = 32); transposed reads: tr[h] ^ {0, 64} (tr[h] for D = 32).
+template <int D>
+__device__ __forceinline__ void dkdv_row_addr(uint32_t (&a)[D / 16], uint32_t ro) {
+  a[0] = ro;
+  if constexpr (D == 64)
+    asm volatile("v_xor_b32 %0, 32, %3\n\tv_xor_b32 %1, 64, %3\n\tv_xor_b32 %2, 0x60, %3"
+                 : "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3])
+                 : "v"(ro));
+  else
+    asm volatile("v_xor_b32 %0, 32, %1" : "=&v"(a[1]) : "v"(ro));
+}
+template <int D>
+__device__ __forceinline__ void dkdv_tr_addr(uint32_t (&a)[2][D / 32], const uint32_t (&tr)[2]) {
+  a[0][0] = tr[0];
+  a[1][0] = tr[1];
+  if constexpr (D == 64)
+    asm volatile("v_xor_b32 %0, 64, %2\n\tv_xor_b32 %1, 64, %3"
+                 : "=&v"(a[0][1]), "=&v"(a[1][1])
+                 : "v"(tr[0]), "v"(tr[1]));
 }
 __device__ __forceinline__ bf16x8 lds_row_at(const bf16* base, uint32_t byte_off) {
   return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(base) + byte_off);
@@ -176,11 +192,13 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
     }
   };
   f32x16 s, dp;
+  uint32_t ra[DS] = {};
+  if constexpr (XA) dkdv_row_addr<D>(ra, lo.ro);
   {
     bf16x8 qa[DS];
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds)
-      qa[ds] = XA ? lds_row_at(sq + 32 * qb * D, xor_at_use(lo.ro, 32u * ds))
+      qa[ds] = XA ? lds_row_at(sq + 32 * qb * D, ra[ds])
                   : lds_op(sq, rm_off<D>(qr, 2 * ds + hi));
     stats(slc, s);
 #pragma unroll
@@ -190,7 +208,7 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
     bf16x8 da[DS];
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds)
-      da[ds] = XA ? lds_row_at(sdo + 32 * qb * D, xor_at_use(lo.ro, 32u * ds))
+      da[ds] = XA ? lds_row_at(sdo + 32 * qb * D, ra[ds])
                   : lds_op(sdo, rm_off<D>(qr, 2 * ds + hi));
     if constexpr (DROP)
       dp = f32x16{};
@@ -239,14 +257,15 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
     pb[j] = as_bf16x8(wp);
     dsb[j] = as_bf16x8(wd);
   }
+  uint32_t ta[2][DB] = {};
+  if constexpr (XA) dkdv_tr_addr<D>(ta, lo.tr);
   {
     bf16x8 t[DB][2];  // A = dO^T: lane d = 32db + l32 gets tile queries 32qb + 16j + 8hi + 0..7
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        t[db][j] = XA ? lds_tr_at(sdo + (32 * qb + 16 * j) * D, xor_at_use(lo.tr[0], 64u * db),
-                                  xor_at_use(lo.tr[1], 64u * db))
+        t[db][j] = XA ? lds_tr_at(sdo + (32 * qb + 16 * j) * D, ta[0][db], ta[1][db])
                       : lds_tr_op<D>(sdo, 32 * qb + 16 * j, 32 * db, lane);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -259,8 +278,7 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        t[db][j] = XA ? lds_tr_at(sq + (32 * qb + 16 * j) * D, xor_at_use(lo.tr[0], 64u * db),
-                                  xor_at_use(lo.tr[1], 64u * db))
+        t[db][j] = XA ? lds_tr_at(sq + (32 * qb + 16 * j) * D, ta[0][db], ta[1][db])
                       : lds_tr_op<D>(sq, 32 * qb + 16 * j, 32 * db, lane);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
