@@ -32,19 +32,19 @@ namespace {
 
 constexpr int kWaves = 4;
 // Workgroups per CU the registers are sized for (4 waves each: 2 -> 256 VGPRs, 3 -> 168).
-// The plain dK/dV kernel fits 168 with its LDS addresses derived at use (DkdvLds below);
-// the dropout and strided ones keep 256.
+// dK/dV fits 168 with its LDS addresses derived at use (DkdvLds below); the dropout one keeps
+// 256.
 #ifndef DADGPT_DKDV_MINB
 #define DADGPT_DKDV_MINB 2
 #endif
-#ifndef DADGPT_DKDV_MINB_PLAIN
-#define DADGPT_DKDV_MINB_PLAIN 3
+#ifndef DADGPT_DKDV_MINB_NODROP
+#define DADGPT_DKDV_MINB_NODROP 3
 #endif
 #ifndef DADGPT_DQ_MINB
 #define DADGPT_DQ_MINB 3
 #endif
 constexpr int kDkdvMinBlocks = DADGPT_DKDV_MINB;
-constexpr int kDkdvMinBlocksPlain = DADGPT_DKDV_MINB_PLAIN;
+constexpr int kDkdvMinBlocksNoDrop = DADGPT_DKDV_MINB_NODROP;
 constexpr int kDqMinBlocks = DADGPT_DQ_MINB;
 
 // ---------------------------------------------------------------- delta
@@ -112,10 +112,10 @@ constexpr int kKW = 32;  // keys per wave
 // 2ds + hi): ro ^ 32ds, because the swizzle XORs the chunk index and 2ds + hi = 2ds ^ hi.
 // Transposed reads of half h (rows 32qb + 16j + ..., columns 32db + ...): tr[h] ^ 64db, the
 // column block flipping chunk bit 2; 32qb and 16j add whole rows, which leave the swizzle alone.
-// The XORs are issued once per block (volatile asm, dkdv_row_addr and dkdv_tr_addr), so three registers stay live
-// across the tile loop instead of every derived address, which the compiler otherwise hoists
-// out of it: this is what brings the plain kernel to 168 VGPRs (three workgroups per CU)
-// without spilling in the loop.
+// The XORs are issued once per block (volatile asm: dkdv_row_addr, dkdv_tr_addr), so three
+// registers stay live across the tile loop instead of every derived address, which the
+// compiler otherwise hoists out of it: this is what brings dK/dV (all but the dropout
+// instantiation) to 168 VGPRs, three workgroups per CU, without spilling in the loop.
 struct DkdvLds {
   uint32_t ro, tr[2];
 };
@@ -288,8 +288,7 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
 }
 
 template <int D, bool STRIDED, bool DROP>
-__global__ __launch_bounds__(64 * kWaves, (DROP || STRIDED) ? kDkdvMinBlocks
-                                                            : kDkdvMinBlocksPlain) void dkdv_bf16_kernel(
+__global__ __launch_bounds__(64 * kWaves, DROP ? kDkdvMinBlocks : kDkdvMinBlocksNoDrop) void dkdv_bf16_kernel(
     bf16* __restrict__ dk, bf16* __restrict__ dv, const bf16* __restrict__ q,
     const bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, int S, float c,
@@ -339,7 +338,7 @@ __global__ __launch_bounds__(64 * kWaves, (DROP || STRIDED) ? kDkdvMinBlocks
     dkacc[db] = f32x16{};
     dvacc[db] = f32x16{};
   }
-  constexpr bool XA = !(DROP || STRIDED);
+  constexpr bool XA = !DROP;
   DkdvLds lo{};
   if constexpr (XA) lo = dkdv_lds<D>(lane);
 
@@ -350,8 +349,8 @@ __global__ __launch_bounds__(64 * kWaves, (DROP || STRIDED) ? kDkdvMinBlocks
   Dma::offsets(dooff, wave, lane, dop);
   float(*st)[2][kTileRows] = sst[wave];
   auto issue = [&](int t, bf16* nq, bf16* ndo, int buf) {
-    Dma::load_any(nq, qg, t * kTileRows, S, qoff, wave, lane, qp);
-    Dma::load_any(ndo, dog, t * kTileRows, S, dooff, wave, lane, dop);
+    Dma::template load_any<STRIDED>(nq, qg, t * kTileRows, S, qoff, wave, lane, qp);
+    Dma::template load_any<STRIDED>(ndo, dog, t * kTileRows, S, dooff, wave, lane, dop);
     dma_row64(st[buf][0], lseg, t * kTileRows, S, lane);
     dma_row64(st[buf][1], delg, t * kTileRows, S, lane);
   };

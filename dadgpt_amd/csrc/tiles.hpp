@@ -178,18 +178,24 @@ struct DmaTile {
 
   // Tile rows row0 .. row0+63 of g (rows `pitch` elements apart, offsets from offsets() with
   // the same pitch). A tile that crosses S moves the offsets of rows past S back to row S-1
-  // (the slot's chunk swizzle is kept; it is the destination's).
+  // (the slot's chunk swizzle is kept; it is the destination's). FRESH_LANE: that correction
+  // is computed here from a fresh copy of the lane index, for callers short of registers
+  // with a runtime pitch, where the compiler would otherwise hoist its per-lane products out
+  // of the tile loop (the fresh copy costs the other kernels time).
+  template <bool FRESH_LANE = false>
   __device__ __forceinline__ static void load_any(bf16* lds_tile, const bf16* g, int row0, int S,
                                                   const uint32_t (&off)[PER_WAVE], int wave,
                                                   int lane, int pitch) {
     if (wave >= ACTIVE) return;
     const int rows_left = S - row0;  // wave-uniform
     const bf16* base = g + (size_t)row0 * pitch;
+    int ln = lane;
+    if constexpr (FRESH_LANE) asm volatile("" : "+v"(ln));
 #pragma unroll
     for (int n = 0; n < PER_WAVE; ++n) {
       uint32_t o = off[n];
       if (rows_left < kTileRows) {
-        const int r = (wave * PER_WAVE + n) * (64 / C) + lane / C;
+        const int r = (wave * PER_WAVE + n) * (64 / C) + ln / C;
         if (r >= rows_left) o -= (uint32_t)((r - rows_left + 1) * pitch * 2);
       }
       dma_lds16_sbase(base, o, lds_tile + (wave * PER_WAVE + n) * 64 * 8);
