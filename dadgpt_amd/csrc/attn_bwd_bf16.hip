@@ -349,8 +349,8 @@ __global__ __launch_bounds__(64 * kWaves, DROP ? kDkdvMinBlocks : kDkdvMinBlocks
   Dma::offsets(dooff, wave, lane, dop);
   float(*st)[2][kTileRows] = sst[wave];
   auto issue = [&](int t, bf16* nq, bf16* ndo, int buf) {
-    Dma::template load_any<STRIDED>(nq, qg, t * kTileRows, S, qoff, wave, lane, qp);
-    Dma::template load_any<STRIDED>(ndo, dog, t * kTileRows, S, dooff, wave, lane, dop);
+    Dma::template load_any<true>(nq, qg, t * kTileRows, S, qoff, wave, lane, qp);
+    Dma::template load_any<true>(ndo, dog, t * kTileRows, S, dooff, wave, lane, dop);
     dma_row64(st[buf][0], lseg, t * kTileRows, S, lane);
     dma_row64(st[buf][1], delg, t * kTileRows, S, lane);
   };

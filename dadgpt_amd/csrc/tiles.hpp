@@ -179,9 +179,9 @@ struct DmaTile {
   // Tile rows row0 .. row0+63 of g (rows `pitch` elements apart, offsets from offsets() with
   // the same pitch). A tile that crosses S moves the offsets of rows past S back to row S-1
   // (the slot's chunk swizzle is kept; it is the destination's). FRESH_LANE: that correction
-  // is computed here from a fresh copy of the lane index, for callers short of registers
-  // with a runtime pitch, where the compiler would otherwise hoist its per-lane products out
-  // of the tile loop (the fresh copy costs the other kernels time).
+  // is computed here from a fresh copy of the lane index, for callers short of registers,
+  // where the compiler would otherwise hoist its per-lane products out of the tile loop and
+  // spill them (the fresh copy costs the kernels with registers to spare time).
   template <bool FRESH_LANE = false>
   __device__ __forceinline__ static void load_any(bf16* lds_tile, const bf16* g, int row0, int S,
                                                   const uint32_t (&off)[PER_WAVE], int wave,
