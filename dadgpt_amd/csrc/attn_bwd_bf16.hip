@@ -32,7 +32,7 @@ namespace {
 
 constexpr int kWaves = 4;
 // Workgroups per CU the registers are sized for (4 waves each: 2 -> 256 VGPRs, 3 -> 168).
-// dK/dV fits 168 with its LDS addresses derived at use (DkdvLds below); the dropout one keeps
+// dK/dV fits 168 with its LDS addresses derived at use (LaneLds); the dropout one keeps
 // 256.
 #ifndef DADGPT_DKDV_MINB
 #define DADGPT_DKDV_MINB 2
@@ -107,65 +107,9 @@ constexpr int kKW = 32;  // keys per wave
 //
 // With dropout (DROP; f = keep/(1-p) from bit 8j+e of `keep`): dV accumulates (P f)^T dO and
 // dS = P (dP f - delta), so dp starts from zero and -delta is read separately.
-// Per-lane LDS byte offsets, within a tile, of dK/dV's operand reads, from which every read of
-// a block is one XOR and an immediate offset away. Row reads (row 32qb + sigma32(l32), chunk
-// 2ds + hi): ro ^ 32ds, because the swizzle XORs the chunk index and 2ds + hi = 2ds ^ hi.
-// Transposed reads of half h (rows 32qb + 16j + ..., columns 32db + ...): tr[h] ^ 64db, the
-// column block flipping chunk bit 2; 32qb and 16j add whole rows, which leave the swizzle alone.
-// The XORs are issued once per block (volatile asm: dkdv_row_addr, dkdv_tr_addr), so three
-// registers stay live across the tile loop instead of every derived address, which the
-// compiler otherwise hoists out of it: this is what brings dK/dV (all but the dropout
-// instantiation) to 168 VGPRs, three workgroups per CU, without spilling in the loop.
-struct DkdvLds {
-  uint32_t ro, tr[2];
-};
-template <int D>
-__device__ __forceinline__ DkdvLds dkdv_lds(int lane) {
-  DkdvLds o;
-  const int l32 = lane & 31, hi = lane >> 5, g = lane >> 4;
-  o.ro = 2u * (uint32_t)rm_off<D>(sigma32(l32), hi);
-  const int cl = 16 * (g & 1) + 4 * (lane & 3);  // the lane's column within a 32-column block
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int rl = 8 * (g >> 1) + 4 * h + ((lane >> 2) & 3);  // its row within 16 rows
-    o.tr[h] = 2u * (uint32_t)(rl * D + (((cl >> 3) ^ swz<D>(rl)) << 3) + (cl & 7));
-  }
-  return o;
-}
-// The addresses one block reads, derived once per block (volatile: not hoisted out of the
-// tile loop), each set right before the phase that reads it. Row reads: ro ^ {0, 32, 64, 96}
-// (D = 64; ro ^ {0, 32} for D = 32); transposed reads: tr[h] ^ {0, 64} (tr[h] for D = 32).
-template <int D>
-__device__ __forceinline__ void dkdv_row_addr(uint32_t (&a)[D / 16], uint32_t ro) {
-  a[0] = ro;
-  if constexpr (D == 64)
-    asm volatile("v_xor_b32 %0, 32, %3\n\tv_xor_b32 %1, 64, %3\n\tv_xor_b32 %2, 0x60, %3"
-                 : "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3])
-                 : "v"(ro));
-  else
-    asm volatile("v_xor_b32 %0, 32, %1" : "=&v"(a[1]) : "v"(ro));
-}
-template <int D>
-__device__ __forceinline__ void dkdv_tr_addr(uint32_t (&a)[2][D / 32], const uint32_t (&tr)[2]) {
-  a[0][0] = tr[0];
-  a[1][0] = tr[1];
-  if constexpr (D == 64)
-    asm volatile("v_xor_b32 %0, 64, %2\n\tv_xor_b32 %1, 64, %3"
-                 : "=&v"(a[0][1]), "=&v"(a[1][1])
-                 : "v"(tr[0]), "v"(tr[1]));
-}
-__device__ __forceinline__ bf16x8 lds_row_at(const bf16* base, uint32_t byte_off) {
-  return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(base) + byte_off);
-}
-// lds_tr_op's read, at byte offsets (within `base`) of its two halves
-__device__ __forceinline__ bf16x8 lds_tr_at(const bf16* base, uint32_t off0, uint32_t off1) {
-  const lds_bf16* t = (const lds_bf16*)base;
-  const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + off0 / 2));
-  const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + off1 / 2));
-  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
-}
-
-// XA: operand addresses from `lo` (DkdvLds) instead of computed per read.
+// XA: operand addresses from `lo` (LaneLds, tiles.hpp), XORed once per phase, instead of
+// computed per read: what brings dK/dV (all but the dropout instantiation) to 168 VGPRs,
+// three workgroups per CU, without spilling in the loop.
 template <int D, bool DROP, bool XA>
 __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
                                            f32x16 (&dvacc)[D / 32], const bf16x8 (&kop)[D / 16],
@@ -173,7 +117,7 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
                                            const bf16* sdo, const float* slc, const float* sdl,
                                            int qb, int key_minus_r0, int rows_left, int lane,
                                            float c, uint32_t keep, float dscale,
-                                           const DkdvLds& lo) {
+                                           const LaneLds& lo) {
   constexpr int DS = D / 16, DB = D / 32;
   const int l32 = lane & 31, hi = lane >> 5;
   const int qr = 32 * qb + sigma32(l32);
@@ -193,7 +137,7 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
   };
   f32x16 s, dp;
   uint32_t ra[DS] = {};
-  if constexpr (XA) dkdv_row_addr<D>(ra, lo.ro);
+  if constexpr (XA) row_addr_xor<D>(ra, lo.ro);
   {
     bf16x8 qa[DS];
 #pragma unroll
@@ -258,7 +202,7 @@ __device__ __forceinline__ void dkdv_block(bool mask, f32x16 (&dkacc)[D / 32],
     dsb[j] = as_bf16x8(wd);
   }
   uint32_t ta[2][DB] = {};
-  if constexpr (XA) dkdv_tr_addr<D>(ta, lo.tr);
+  if constexpr (XA) tr_addr_xor<D>(ta, lo.tr);
   {
     bf16x8 t[DB][2];  // A = dO^T: lane d = 32db + l32 gets tile queries 32qb + 16j + 8hi + 0..7
 #pragma unroll
@@ -339,8 +283,8 @@ __global__ __launch_bounds__(64 * kWaves, DROP ? kDkdvMinBlocks : kDkdvMinBlocks
     dvacc[db] = f32x16{};
   }
   constexpr bool XA = !DROP;
-  DkdvLds lo{};
-  if constexpr (XA) lo = dkdv_lds<D>(lane);
+  LaneLds lo{};
+  if constexpr (XA) lo = lane_lds<D>(lane);
 
   // Direct loads per wave per tile: its share of Q and dO, and its own lse and delta rows.
   using Dma = DmaTile<D, kWaves>;

@@ -42,8 +42,8 @@ namespace {
 
 constexpr int kWaves = 4;             // waves per workgroup
 // Two workgroups per CU, i.e. at most 256 registers a lane (one wave per SIMD runs the backward
-// ~15% slower). At D = 64 the forward and dQ fit; dK/dV spills 5 registers (26 with dropout),
-// loop-invariant values reloaded once per chunk.
+// ~15% slower). At D = 64 the forward, dQ and dK/dV fit (dK/dV with its plane addresses from
+// LaneLds); the dropout dK/dV spills 19 registers, loop-invariant values reloaded per chunk.
 constexpr int kMinBlocks = 2;
 constexpr int kRows = 32 * kWaves;    // rows (queries or keys) a workgroup owns
 constexpr int kTile = 64;             // rows per staged tile (two 32-row chunks)
@@ -263,6 +263,51 @@ __device__ __forceinline__ void accumulate_t_p(f32x16 (&acc)[D / 32], const bf16
   }
 }
 
+// score_tile_pf and accumulate_t_p at chunk row 0 of TR-row planes, with the addresses from
+// LaneLds (tiles.hpp): the dK/dV kernel's register relief (no spills at D = 64).
+template <int D, int TR>
+__device__ __forceinline__ f32x16 score_tile_pfx(const bf16* planes, const float (&bf)[D / 2],
+                                                 const LaneLds& lo) {
+  uint32_t ra[D / 16];
+  row_addr_xor<D>(ra, lo.ro);
+  f32x16 acc = zero16();
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds) {
+    X3 a;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) a.v[pl] = lds_row_at(planes + pl * TR * D, ra[ds]);
+    float b[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      b[e] = bf[8 * ds + e];
+      asm volatile("" : "+v"(b[e]));
+    }
+    acc = mfma_x6(a, split3(b), acc);
+  }
+  return acc;
+}
+template <int D, int TR>
+__device__ __forceinline__ void accumulate_t_px(f32x16 (&acc)[D / 32], const bf16* planes,
+                                                const f32x16& p, const LaneLds& lo) {
+  uint32_t ta[2][D / 32];
+  tr_addr_xor<D>(ta, lo.tr);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = p[8 * j + e];
+    const X3 pb = split3(x);
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      X3 a;
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        a.v[pl] = lds_tr_at(planes + pl * TR * D + 16 * j * D, ta[0][db], ta[1][db]);
+      acc[db] = mfma_x6(a, pb, acc[db]);
+    }
+  }
+}
+
 // Writes a wave's transposed accumulators (element r of lane (l32, h), block db: row l32 of
 // the wave, column 32 db + c32_row(r, h)) as 32 contiguous rows of D floats through the wave's
 // LDS slot `stage` (32 x (D + 4) floats), times `mul` (per lane).
@@ -445,6 +490,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) dka[db] = zero16(), dva[db] = zero16();
 
+  static_assert(TR == 32, "one chunk per tile");
+  const LaneLds lo = lane_lds<D>(lane);
   Tile<D, TR> tq, tg;
   float pl = 0.f, pd = 0.f;
   auto load_stats = [&](int row0) {
@@ -471,8 +518,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
       const int qrow0 = t * TR + 32 * c;
       if (qrow0 + 31 < k0) continue;  // wave-uniform: every query of the chunk precedes every key
       // lane (l32, h), register u: query qrow0 + reg_row(u, h), key kj
-      f32x16 s = score_tile_pf<D, TR>(sqp, 32 * c, kf, lane);   // Q K^T
-      f32x16 dp = score_tile_pf<D, TR>(sgp, 32 * c, vf, lane);  // dO V^T
+      f32x16 s = score_tile_pfx<D, TR>(sqp, kf, lo);   // Q K^T
+      f32x16 dp = score_tile_pfx<D, TR>(sgp, vf, lo);  // dO V^T
       uint32_t keep = 0;
       if constexpr (DROP) keep = keep_col16(dr, (uint64_t)bh * S + qrow0, k0, lane);
       // Statistics of the chunk's rows 32c + reg_row(u, h): registers 8j..8j+7 are the 8
@@ -505,8 +552,8 @@ __global__ __launch_bounds__(64 * kWaves, kMinBlocks) void dkdv_f32_kernel(
           dp[u] = p * fmaf(g, scale, -ds[e]);  // P (dP - delta) scale
         }
       }
-      accumulate_t_p<D, TR>(dva, sgp, 32 * c, s, lane);   // dV^T += dO^T P
-      accumulate_t_p<D, TR>(dka, sqp, 32 * c, dp, lane);  // dK^T += Q^T dS
+      accumulate_t_px<D, TR>(dva, sgp, s, lo);   // dV^T += dO^T P
+      accumulate_t_px<D, TR>(dka, sqp, dp, lo);  // dK^T += Q^T dS
     }
   }
   __syncthreads();

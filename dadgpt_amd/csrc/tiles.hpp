@@ -91,6 +91,66 @@ __device__ __forceinline__ bf16x8 lds_tr_op(const bf16* tile, int row0, int col0
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// Per-lane LDS byte offsets, within a [64][D] (or [32][D]) tile, of the two read patterns of
+// a 32-row score block, from which every read of a block is one XOR and an immediate offset
+// away:
+//   row reads (row r0 + sigma32(l32), chunk 2ds + hi)   ro ^ 32ds: the swizzle XORs the chunk
+//       index, and 2ds + hi = 2ds ^ hi
+//   transposed reads (lds_tr_op at rows r0 + 16j ..., columns 32db ...), half h
+//                                                       tr[h] ^ 64db: the column block flips
+//       chunk bit 2
+// where r0 and 16j, whole groups of 16 rows, leave the swizzle alone and add constants. A
+// kernel short of registers keeps these three and issues the XORs once per phase (volatile
+// asm: row_addr_xor, tr_addr_xor), where the compiler otherwise hoists every derived address
+// out of its tile loop.
+struct LaneLds {
+  uint32_t ro, tr[2];
+};
+template <int D>
+__device__ __forceinline__ LaneLds lane_lds(int lane) {
+  LaneLds o;
+  const int l32 = lane & 31, hi = lane >> 5, g = lane >> 4;
+  o.ro = 2u * (uint32_t)rm_off<D>(sigma32(l32), hi);
+  const int cl = 16 * (g & 1) + 4 * (lane & 3);  // the lane's column within a 32-column block
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int rl = 8 * (g >> 1) + 4 * h + ((lane >> 2) & 3);  // its row within 16 rows
+    o.tr[h] = 2u * (uint32_t)(rl * D + (((cl >> 3) ^ swz<D>(rl)) << 3) + (cl & 7));
+  }
+  return o;
+}
+// Row-read offsets of chunks ds = 0 .. D/16-1.
+template <int D>
+__device__ __forceinline__ void row_addr_xor(uint32_t (&a)[D / 16], uint32_t ro) {
+  a[0] = ro;
+  if constexpr (D == 64)
+    asm volatile("v_xor_b32 %0, 32, %3\n\tv_xor_b32 %1, 64, %3\n\tv_xor_b32 %2, 0x60, %3"
+                 : "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3])
+                 : "v"(ro));
+  else
+    asm volatile("v_xor_b32 %0, 32, %1" : "=&v"(a[1]) : "v"(ro));
+}
+// Transposed-read offsets [half][db].
+template <int D>
+__device__ __forceinline__ void tr_addr_xor(uint32_t (&a)[2][D / 32], const uint32_t (&tr)[2]) {
+  a[0][0] = tr[0];
+  a[1][0] = tr[1];
+  if constexpr (D == 64)
+    asm volatile("v_xor_b32 %0, 64, %2\n\tv_xor_b32 %1, 64, %3"
+                 : "=&v"(a[0][1]), "=&v"(a[1][1])
+                 : "v"(tr[0]), "v"(tr[1]));
+}
+__device__ __forceinline__ bf16x8 lds_row_at(const bf16* base, uint32_t byte_off) {
+  return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+// lds_tr_op's read, at byte offsets (within `base`) of its two halves
+__device__ __forceinline__ bf16x8 lds_tr_at(const bf16* base, uint32_t off0, uint32_t off1) {
+  const lds_bf16* t = (const lds_bf16*)base;
+  const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + off0 / 2));
+  const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + off1 / 2));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // Direct global -> LDS staging (global_load_lds_dwordx4): lane i of a wave-instruction writes
 // its 16 bytes to LDS at (M0 + 16*i), so the swizzle is applied on the global side: the lane
 // that fills LDS slot (row, physical chunk c) reads logical chunk c ^ swz(row). No registers
