@@ -144,7 +144,7 @@ def _sweep_shapes(n=10, seed=2026):
     return out
 
 
-@pytest.mark.parametrize("BH,S,D,scale", _sweep_shapes())
+@pytest.mark.parametrize("BH,S,D,scale", _sweep_shapes(n=30))
 def test_bf16_and_fp32_random_shapes(gpu, BH, S, D, scale):
     """bf16 and fp32 kernels, forward and backward, on seeded random shapes and scales against
     the oracle at the path's tolerances (the fixed shapes above cover the named edge cases)."""

@@ -85,6 +85,21 @@ def test_dropout_matches_oracle(gpu, BH, S, D, p):
         within_scaled(host(got), ref, TOL_GRAD, p, nm)
 
 
+def _dropout_shapes(n=8, seed=909):
+    """Seeded random dropout cases: BH in [1, 4], S in [1, 500], D in {32, 64}, p in
+    {0.05, 0.1, 0.3, 0.5}."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 5)), int(rng.integers(1, 501)), int(rng.choice([32, 64])),
+             float(rng.choice([0.05, 0.1, 0.3, 0.5]))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("BH,S,D,p", _dropout_shapes())
+def test_dropout_random_shapes(gpu, BH, S, D, p):
+    """The bf16 and fp32 dropout checks on seeded random shapes and rates."""
+    test_dropout_matches_oracle(gpu, BH, S, D, p)
+    test_dropout_f32_matches_oracle(gpu, BH, S, D, p)
+
+
 def test_dropout_rate_zero_equals_plain(gpu):
     """p = 0 keeps every probability with factor 1: the forward and dQ are bit for bit the
     plain kernels' (dK/dV folds delta in after its products instead of before: within

@@ -103,6 +103,20 @@ def test_tokens_fused_qkv(gpu, B, H, S, D):
             assert np.max(np.abs(got.reshape(B * H, S, D) - r)) <= TOL_GRAD, nm
 
 
+def _token_shapes(n=8, seed=707):
+    """Seeded random token-major shapes: B in [1, 3], H in [1, 4], S in [1, 700], D in {32, 64}."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 4)), int(rng.integers(1, 5)), int(rng.integers(1, 701)),
+             int(rng.choice([32, 64]))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("B,H,S,D", _token_shapes())
+def test_tokens_fused_qkv_random_shapes(gpu, B, H, S, D):
+    """The fused-QKV token-major check above on seeded random shapes (tiles crossing S at every
+    offset, both head sizes)."""
+    test_tokens_fused_qkv(gpu, B, H, S, D)
+
+
 @pytest.mark.parametrize("D", [64, 32])
 def test_strided_views_cache_rows(gpu, D):
     """Tensor views of different placements in one call: q contiguous, k and v the first S
